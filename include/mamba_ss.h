@@ -1,0 +1,144 @@
+/*
+ * mamba_ss.h -- C ABI of the MI355X selective-scan library (libmamba_ss.so).
+ *
+ * Replaces the reference's native module `selective_scan`
+ * (csrc/selective_scan/selective_scan.cpp:331-334, built by setup.py:10-16):
+ *   selective_scan.forward(u, delta, A, B, C, D?, delta_bias?, softplus)
+ *       -> [out, x]                          selective_scan.cpp:184-244
+ *   selective_scan.backward(u, delta, A, B, C, D?, delta_bias?, dout, x?, softplus)
+ *       -> [du, ddelta, dA, dB, dC, dD, ddelta_bias]   selective_scan.cpp:246-329
+ *
+ * Differences from the pybind boundary, all deliberate:
+ *  - plain C: POD argument structs, raw device pointers, 64-bit sizes and
+ *    element strides; no torch types and no C++ exceptions cross the ABI;
+ *  - the library never allocates: the caller passes every output, the
+ *    checkpoint buffer x and zero-initialised gradient accumulators
+ *    (dA, dB, dC, dD, ddelta_bias are accumulated into);
+ *  - errors are returned as status codes, with a message in
+ *    ss_last_error() (the reference has no argument checks at all);
+ *  - an optional fused z gate (out = y * silu(z)) and bf16/fp16 I/O, which
+ *    the reference kernels do not have (they are fp32-only).
+ *
+ * Layouts: u, delta, z, out, dout, du, ddelta, dz are (batch, dim, seqlen)
+ * with unit stride along seqlen; A is (dim, dstate) fp32; variable B/C are
+ * (batch, n_groups, dstate, seqlen) with unit stride along seqlen; constant
+ * B/C are (dim, dstate) fp32; D and delta_bias are (dim) fp32 contiguous.
+ * x is fp32 (batch, dim, n_chunks, dstate) contiguous: the state h at the
+ * end of every chunk of ss_chunk_size() steps (the last chunk holds the
+ * final state).  It plays the role of the reference's x
+ * (selective_scan.cpp:207-212) and is consumed only by ss_bwd.
+ *
+ * All calls are asynchronous on `stream` (a hipStream_t, NULL = default
+ * stream) and re-entrant: no global mutable state besides the thread-local
+ * error message.
+ */
+#ifndef MAMBA_SS_H
+#define MAMBA_SS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SS_ABI_VERSION 1
+
+/* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
+enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
+
+/* status codes */
+enum ss_status {
+    SS_OK = 0,
+    SS_ERR_INVALID = 1,     /* bad argument: shape, stride, null pointer, dtype */
+    SS_ERR_UNSUPPORTED = 2, /* valid but outside what the kernels implement */
+    SS_ERR_HIP = 3          /* a HIP runtime / launch error */
+};
+
+typedef struct ss_fwd_args {
+    int64_t batch, dim, seqlen, dstate, n_groups;
+    int32_t itype;           /* enum ss_dtype */
+    int32_t is_var_B, is_var_C;
+    int32_t has_D, has_delta_bias, has_z;
+    int32_t delta_softplus;
+    int64_t n_chunks;        /* must equal ceil(seqlen / ss_chunk_size()) */
+    /* element strides (batch, dim) of the (batch, dim, seqlen) tensors */
+    int64_t u_batch_stride, u_dim_stride;
+    int64_t delta_batch_stride, delta_dim_stride;
+    int64_t z_batch_stride, z_dim_stride;
+    int64_t out_batch_stride, out_dim_stride;
+    /* A (dim, dstate) */
+    int64_t A_dim_stride, A_dstate_stride;
+    /* variable B/C: (batch, group, dstate) strides; constant: (dim, dstate) in
+       (*_group_stride := dim stride, *_dstate_stride) and *_batch_stride = 0 */
+    int64_t B_batch_stride, B_group_stride, B_dstate_stride;
+    int64_t C_batch_stride, C_group_stride, C_dstate_stride;
+    const void* u;
+    const void* delta;
+    const float* A;
+    const void* B;
+    const void* C;
+    const float* D;          /* may be NULL iff !has_D */
+    const float* delta_bias; /* may be NULL iff !has_delta_bias */
+    const void* z;           /* may be NULL iff !has_z */
+    void* out;
+    float* x;
+    /* pre-gate output y = sum_n C h + D u, same layout as out.  Written by
+       ss_fwd when has_z and y != NULL; required (read) by ss_bwd when has_z. */
+    void* y;
+    int64_t y_batch_stride, y_dim_stride;
+} ss_fwd_args;
+
+typedef struct ss_bwd_args {
+    ss_fwd_args f;           /* inputs as for the forward; f.out is ignored, f.x is read */
+    int64_t dout_batch_stride, dout_dim_stride;
+    int64_t du_batch_stride, du_dim_stride;
+    int64_t ddelta_batch_stride, ddelta_dim_stride;
+    int64_t dz_batch_stride, dz_dim_stride;
+    const void* dout;
+    void* du;                /* overwritten, itype */
+    void* ddelta;            /* overwritten, itype */
+    void* dz;                /* overwritten, itype; may be NULL iff !has_z */
+    float* dA;               /* accumulated into, (dim, dstate) contiguous */
+    float* dB;               /* accumulated into, fp32, shape of B, contiguous */
+    float* dC;               /* accumulated into, fp32, shape of C, contiguous */
+    float* dD;               /* accumulated into; may be NULL iff !has_D */
+    float* ddelta_bias;      /* accumulated into; may be NULL iff !has_delta_bias */
+} ss_bwd_args;
+
+/* ABI version (SS_ABI_VERSION of the built library). */
+int ss_abi_version(void);
+
+/* Steps per checkpoint chunk of x (the reference's chunk is 128,
+   kernel_config.cuh:3-7). */
+int64_t ss_chunk_size(void);
+
+/* Largest dstate the kernels accept (the reference dispatches up to 256,
+   static_switch.h:15-37). */
+int64_t ss_max_dstate(void);
+
+/* sizeof(ss_fwd_args) and sizeof(ss_bwd_args) of the built library, so a
+   foreign-function binding can check its struct layout.  Either pointer may
+   be NULL. */
+void ss_struct_sizes(int64_t* fwd_args, int64_t* bwd_args);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* ss_last_error(void);
+
+/* Argument checks only, no device work: SS_OK or an error code. */
+int ss_fwd_check(const ss_fwd_args* a);
+int ss_bwd_check(const ss_bwd_args* a);
+
+/* Forward scan: writes out and x.  Replaces selective_scan.forward /
+   forward_kernel_launch (selective_scan.cpp:184-244, forward_kernel.cu:313-333). */
+int ss_fwd(const ss_fwd_args* a, void* stream);
+
+/* Backward scan: writes du, ddelta, dz; accumulates dA, dB, dC, dD,
+   ddelta_bias.  Replaces selective_scan.backward / backward_kernel_launch
+   (selective_scan.cpp:246-329, backward_kernel.cu:588-618). */
+int ss_bwd(const ss_bwd_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA_SS_H */

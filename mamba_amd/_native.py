@@ -1,0 +1,105 @@
+"""ctypes binding of libmamba_ss.so (declared in include/mamba_ss.h).
+
+The library is loaded lazily from ``mamba_amd/_lib/libmamba_ss.so``.  There
+is no fallback: if the library is missing or the tensors are not on a ROCm
+device, the call raises.
+"""
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
+
+SS_F32, SS_BF16, SS_F16 = 0, 1, 2
+SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
+ABI_VERSION = 1
+
+EXPORTED = (
+    "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
+    "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_fwd", "ss_bwd",
+)
+
+_i64, _i32, _p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("dim", _i64), ("seqlen", _i64), ("dstate", _i64), ("n_groups", _i64),
+        ("itype", _i32), ("is_var_B", _i32), ("is_var_C", _i32),
+        ("has_D", _i32), ("has_delta_bias", _i32), ("has_z", _i32), ("delta_softplus", _i32),
+        ("n_chunks", _i64),
+        ("u_batch_stride", _i64), ("u_dim_stride", _i64),
+        ("delta_batch_stride", _i64), ("delta_dim_stride", _i64),
+        ("z_batch_stride", _i64), ("z_dim_stride", _i64),
+        ("out_batch_stride", _i64), ("out_dim_stride", _i64),
+        ("A_dim_stride", _i64), ("A_dstate_stride", _i64),
+        ("B_batch_stride", _i64), ("B_group_stride", _i64), ("B_dstate_stride", _i64),
+        ("C_batch_stride", _i64), ("C_group_stride", _i64), ("C_dstate_stride", _i64),
+        ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
+        ("D", _p), ("delta_bias", _p), ("z", _p), ("out", _p), ("x", _p),
+        ("y", _p), ("y_batch_stride", _i64), ("y_dim_stride", _i64),
+    ]
+
+
+class BwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("f", FwdArgs),
+        ("dout_batch_stride", _i64), ("dout_dim_stride", _i64),
+        ("du_batch_stride", _i64), ("du_dim_stride", _i64),
+        ("ddelta_batch_stride", _i64), ("ddelta_dim_stride", _i64),
+        ("dz_batch_stride", _i64), ("dz_dim_stride", _i64),
+        ("dout", _p), ("du", _p), ("ddelta", _p), ("dz", _p),
+        ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("ddelta_bias", _p),
+    ]
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Loads and type-annotates the library; raises if it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"mamba_amd: HIP library not built ({LIB_PATH} missing); "
+                "run `python -m mamba_amd.build` or __graft_entry__.build()")
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.ss_abi_version.restype = ctypes.c_int
+        lib.ss_chunk_size.restype = _i64
+        lib.ss_max_dstate.restype = _i64
+        lib.ss_struct_sizes.argtypes = [ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
+        lib.ss_struct_sizes.restype = None
+        lib.ss_last_error.restype = ctypes.c_char_p
+        for name, T in (("ss_fwd_check", FwdArgs), ("ss_bwd_check", BwdArgs)):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.POINTER(T)]
+            fn.restype = ctypes.c_int
+        lib.ss_fwd.argtypes = [ctypes.POINTER(FwdArgs), _p]
+        lib.ss_fwd.restype = ctypes.c_int
+        lib.ss_bwd.argtypes = [ctypes.POINTER(BwdArgs), _p]
+        lib.ss_bwd.restype = ctypes.c_int
+        if lib.ss_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"mamba_amd: library ABI {lib.ss_abi_version()} != binding ABI {ABI_VERSION}")
+        fs, bs = _i64(), _i64()
+        lib.ss_struct_sizes(ctypes.byref(fs), ctypes.byref(bs))
+        if fs.value != ctypes.sizeof(FwdArgs) or bs.value != ctypes.sizeof(BwdArgs):
+            raise RuntimeError("mamba_amd: ctypes struct layout does not match the library")
+        _lib = lib
+    return _lib
+
+
+def check(rc, what):
+    """Maps a status code to an exception carrying ss_last_error()."""
+    if rc == SS_OK:
+        return
+    msg = load().ss_last_error().decode(errors="replace")
+    if rc in (SS_ERR_INVALID, SS_ERR_UNSUPPORTED):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")

@@ -1,0 +1,223 @@
+// extern "C" entry points of libmamba_ss.so: argument checks and dispatch.
+//
+// The reference binding (csrc/selective_scan/selective_scan.cpp:184-329)
+// checks nothing; here every call is validated first and failures come back
+// as status codes with a thread-local message, never as exceptions.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/mamba_ss.h"
+#include "ss_device.hpp"
+#include "ss_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return SS_OK;
+}
+
+size_t elem_size(int itype) { return itype == SS_F32 ? 4 : 2; }
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int64_t n_chunks_for(int64_t L) { return (L + ss::kChunk - 1) / ss::kChunk; }
+
+// Checks common to forward and backward.  `empty` is set when there is no
+// work (batch, dim or seqlen is 0); pointers are then not inspected.
+int check_fwd_common(const ss_fwd_args* a, bool* empty) {
+    if (!a) return fail(SS_ERR_INVALID, "null argument block");
+    if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
+        return fail(SS_ERR_INVALID, "negative size (batch=%lld dim=%lld seqlen=%lld)",
+                    (long long)a->batch, (long long)a->dim, (long long)a->seqlen);
+    if (a->dstate < 1 || a->dstate > 16 * ss::kMaxSPL)
+        return fail(SS_ERR_UNSUPPORTED, "dstate=%lld outside [1, %d]", (long long)a->dstate, 16 * ss::kMaxSPL);
+    if (a->itype != SS_F32 && a->itype != SS_BF16 && a->itype != SS_F16)
+        return fail(SS_ERR_INVALID, "unknown itype %d", a->itype);
+    if (a->is_var_B || a->is_var_C) {
+        if (a->n_groups < 1) return fail(SS_ERR_INVALID, "n_groups=%lld < 1", (long long)a->n_groups);
+        if (a->dim % a->n_groups != 0)
+            return fail(SS_ERR_INVALID, "dim=%lld is not a multiple of n_groups=%lld",
+                        (long long)a->dim, (long long)a->n_groups);
+    }
+    if (a->n_chunks != n_chunks_for(a->seqlen))
+        return fail(SS_ERR_INVALID, "n_chunks=%lld, expected ceil(seqlen / %d) = %lld",
+                    (long long)a->n_chunks, ss::kChunk, (long long)n_chunks_for(a->seqlen));
+    const int64_t nblk = (a->dim + ss::kChPerWG - 1) / ss::kChPerWG;
+    if (a->batch > 0 && nblk > (int64_t(INT32_MAX) / a->batch))
+        return fail(SS_ERR_UNSUPPORTED, "grid of %lld x %lld workgroups is too large",
+                    (long long)nblk, (long long)a->batch);
+    *empty = a->batch == 0 || a->dim == 0 || a->seqlen == 0;
+    if (*empty) return SS_OK;
+    const size_t es = elem_size(a->itype);
+    struct P { const void* p; const char* name; bool need; size_t align; };
+    const P ptrs[] = {
+        {a->u, "u", true, es}, {a->delta, "delta", true, es}, {a->A, "A", true, 4},
+        {a->B, "B", true, a->is_var_B ? es : 4}, {a->C, "C", true, a->is_var_C ? es : 4},
+        {a->D, "D", a->has_D != 0, 4}, {a->delta_bias, "delta_bias", a->has_delta_bias != 0, 4},
+        {a->z, "z", a->has_z != 0, es}, {a->x, "x", true, 4},
+    };
+    for (const P& q : ptrs) {
+        if (q.need && !q.p) return fail(SS_ERR_INVALID, "%s is NULL", q.name);
+        if (q.p && !aligned(q.p, q.align)) return fail(SS_ERR_INVALID, "%s is misaligned", q.name);
+    }
+    const int64_t strides[] = {a->u_batch_stride, a->u_dim_stride, a->delta_batch_stride, a->delta_dim_stride,
+                               a->z_batch_stride, a->z_dim_stride, a->A_dim_stride, a->A_dstate_stride,
+                               a->B_batch_stride, a->B_group_stride, a->B_dstate_stride,
+                               a->C_batch_stride, a->C_group_stride, a->C_dstate_stride};
+    for (int64_t s : strides)
+        if (s < 0) return fail(SS_ERR_INVALID, "negative stride");
+    return SS_OK;
+}
+
+bool vec_rows(const void* base, int64_t bs, int64_t gs, int64_t ns, int64_t L, size_t es) {
+    // 16-byte loads need aligned row starts and a whole number of 16-byte
+    // vectors per 16-step tile.
+    const int64_t per16 = int64_t(16 / es);
+    return aligned(base, 16) && bs % per16 == 0 && gs % per16 == 0 && ns % per16 == 0 && L >= 0;
+}
+
+ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
+    ss::FwdParams p{};
+    const size_t es = elem_size(a->itype);
+    p.batch = a->batch; p.dim = a->dim; p.seqlen = a->seqlen; p.dstate = a->dstate;
+    p.dpg = (a->is_var_B || a->is_var_C) ? a->dim / a->n_groups : a->dim;
+    if (p.dpg < 1) p.dpg = 1;
+    p.n_chunks = a->n_chunks;
+    p.var_B = a->is_var_B != 0; p.var_C = a->is_var_C != 0;
+    p.has_z = a->has_z != 0; p.softplus = a->delta_softplus != 0;
+    p.vec_B = p.var_B && vec_rows(a->B, a->B_batch_stride, a->B_group_stride, a->B_dstate_stride, a->seqlen, es);
+    p.vec_C = p.var_C && vec_rows(a->C, a->C_batch_stride, a->C_group_stride, a->C_dstate_stride, a->seqlen, es);
+    p.u_bs = a->u_batch_stride; p.u_ds = a->u_dim_stride;
+    p.dl_bs = a->delta_batch_stride; p.dl_ds = a->delta_dim_stride;
+    p.z_bs = a->z_batch_stride; p.z_ds = a->z_dim_stride;
+    p.o_bs = a->out_batch_stride; p.o_ds = a->out_dim_stride;
+    p.A_ds = a->A_dim_stride; p.A_ns = a->A_dstate_stride;
+    p.B_bs = a->B_batch_stride; p.B_gs = a->B_group_stride; p.B_ns = a->B_dstate_stride;
+    p.C_bs = a->C_batch_stride; p.C_gs = a->C_group_stride; p.C_ns = a->C_dstate_stride;
+    p.u = a->u; p.delta = a->delta; p.A = a->A; p.B = a->B; p.C = a->C;
+    p.D = a->has_D ? a->D : nullptr;
+    p.delta_bias = a->has_delta_bias ? a->delta_bias : nullptr;
+    p.z = a->has_z ? a->z : nullptr;
+    p.out = a->out; p.x = a->x;
+    p.y = a->has_z ? a->y : nullptr;
+    p.y_bs = a->y_batch_stride; p.y_ds = a->y_dim_stride;
+    return p;
+}
+
+int check_fwd(const ss_fwd_args* a, bool* empty) {
+    int rc = check_fwd_common(a, empty);
+    if (rc != SS_OK || *empty) return rc;
+    if (!a->out) return fail(SS_ERR_INVALID, "out is NULL");
+    if (!aligned(a->out, elem_size(a->itype))) return fail(SS_ERR_INVALID, "out is misaligned");
+    if (a->out_batch_stride < 0 || a->out_dim_stride < 0) return fail(SS_ERR_INVALID, "negative stride");
+    if (a->has_z && a->y) {
+        if (!aligned(a->y, elem_size(a->itype))) return fail(SS_ERR_INVALID, "y is misaligned");
+        if (a->y_batch_stride < 0 || a->y_dim_stride < 0) return fail(SS_ERR_INVALID, "negative stride");
+    }
+    return SS_OK;
+}
+
+int check_bwd(const ss_bwd_args* a, bool* empty) {
+    if (!a) return fail(SS_ERR_INVALID, "null argument block");
+    int rc = check_fwd_common(&a->f, empty);
+    if (rc != SS_OK || *empty) return rc;
+    const size_t es = elem_size(a->f.itype);
+    struct P { const void* p; const char* name; bool need; size_t align; };
+    const P ptrs[] = {
+        {a->dout, "dout", true, es}, {a->du, "du", true, es}, {a->ddelta, "ddelta", true, es},
+        {a->dz, "dz", a->f.has_z != 0, es}, {a->dA, "dA", true, 4}, {a->dB, "dB", true, 4},
+        {a->dC, "dC", true, 4}, {a->dD, "dD", a->f.has_D != 0, 4},
+        {a->ddelta_bias, "ddelta_bias", a->f.has_delta_bias != 0, 4},
+        {a->f.y, "y (saved pre-gate output)", a->f.has_z != 0, es},
+    };
+    for (const P& q : ptrs) {
+        if (q.need && !q.p) return fail(SS_ERR_INVALID, "%s is NULL", q.name);
+        if (q.p && !aligned(q.p, q.align)) return fail(SS_ERR_INVALID, "%s is misaligned", q.name);
+    }
+    const int64_t strides[] = {a->dout_batch_stride, a->dout_dim_stride, a->du_batch_stride, a->du_dim_stride,
+                               a->ddelta_batch_stride, a->ddelta_dim_stride, a->dz_batch_stride, a->dz_dim_stride,
+                               a->f.y_batch_stride, a->f.y_dim_stride};
+    for (int64_t s : strides)
+        if (s < 0) return fail(SS_ERR_INVALID, "negative stride");
+    return SS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ss_abi_version(void) { return SS_ABI_VERSION; }
+
+int64_t ss_chunk_size(void) { return ss::kChunk; }
+
+int64_t ss_max_dstate(void) { return 16 * ss::kMaxSPL; }
+
+void ss_struct_sizes(int64_t* fwd_args, int64_t* bwd_args) {
+    if (fwd_args) *fwd_args = int64_t(sizeof(ss_fwd_args));
+    if (bwd_args) *bwd_args = int64_t(sizeof(ss_bwd_args));
+}
+
+const char* ss_last_error(void) { return g_err.c_str(); }
+
+int ss_fwd_check(const ss_fwd_args* a) {
+    bool empty = false;
+    int rc = check_fwd(a, &empty);
+    return rc == SS_OK ? ok() : rc;
+}
+
+int ss_bwd_check(const ss_bwd_args* a) {
+    bool empty = false;
+    int rc = check_bwd(a, &empty);
+    return rc == SS_OK ? ok() : rc;
+}
+
+int ss_fwd(const ss_fwd_args* a, void* stream) {
+    bool empty = false;
+    int rc = check_fwd(a, &empty);
+    if (rc != SS_OK) return rc;
+    if (empty) return ok();
+    const ss::FwdParams p = make_fwd_params(a);
+    hipError_t e = ss::launch_fwd(p, a->itype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "forward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int ss_bwd(const ss_bwd_args* a, void* stream) {
+    bool empty = false;
+    int rc = check_bwd(a, &empty);
+    if (rc != SS_OK) return rc;
+    if (empty) return ok();
+    ss::BwdParams p{};
+    p.f = make_fwd_params(&a->f);
+    p.wg_reduce = (p.f.dpg % ss::kChPerWG) == 0;
+    p.do_bs = a->dout_batch_stride; p.do_ds = a->dout_dim_stride;
+    p.du_bs = a->du_batch_stride; p.du_ds = a->du_dim_stride;
+    p.dd_bs = a->ddelta_batch_stride; p.dd_ds = a->ddelta_dim_stride;
+    p.dz_bs = a->dz_batch_stride; p.dz_ds = a->dz_dim_stride;
+    p.dout = a->dout; p.du = a->du; p.ddelta = a->ddelta; p.dz = a->f.has_z ? a->dz : nullptr;
+    p.dA = a->dA; p.dB = a->dB; p.dC = a->dC;
+    p.dD = a->f.has_D ? a->dD : nullptr;
+    p.ddelta_bias = a->f.has_delta_bias ? a->ddelta_bias : nullptr;
+    hipError_t e = ss::launch_bwd(p, a->f.itype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,37 @@
+// Kernel-side argument blocks and launcher declarations (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mamba_ss.h"
+
+namespace ss {
+
+struct FwdParams {
+    int64_t batch, dim, seqlen, dstate, dpg;  // dpg: channels per group
+    int64_t n_chunks;
+    int32_t var_B, var_C, has_z, softplus;
+    int32_t vec_B, vec_C;                     // 16-byte aligned rows of variable B / C
+    int64_t u_bs, u_ds, dl_bs, dl_ds, z_bs, z_ds, o_bs, o_ds, y_bs, y_ds;
+    int64_t A_ds, A_ns;
+    int64_t B_bs, B_gs, B_ns, C_bs, C_gs, C_ns;
+    const void* u; const void* delta; const float* A; const void* B; const void* C;
+    const float* D; const float* delta_bias; const void* z;
+    void* out; float* x;
+    void* y;                                  // pre-gate output (z gate only); may be null in forward
+};
+
+struct BwdParams {
+    FwdParams f;
+    int32_t wg_reduce;                        // all channels of a workgroup share one group
+    int64_t do_bs, do_ds, du_bs, du_ds, dd_bs, dd_ds, dz_bs, dz_ds;
+    const void* dout; void* du; void* ddelta; void* dz;
+    float* dA; float* dB; float* dC; float* dD; float* ddelta_bias;
+};
+
+// Return hipSuccess or the launch error.
+hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream);
+hipError_t launch_bwd(const BwdParams& p, int itype, hipStream_t stream);
+
+}  // namespace ss

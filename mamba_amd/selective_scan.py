@@ -1,0 +1,180 @@
+"""Drop-in for the reference's native module ``selective_scan``.
+
+The reference builds a pybind extension named ``selective_scan``
+(setup.py:10-16, csrc/selective_scan/selective_scan.cpp:331-334) with
+
+    forward(u, delta, A, B, C, D, delta_bias, use_delta_softplus) -> [out, x]
+    backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus)
+        -> [du, ddelta, dA, dB, dC, dD, ddelta_bias]
+
+This module keeps those positional signatures and return lists and runs
+them on libmamba_ss.so through its C ABI.  Host-side rules mirror
+selective_scan.cpp:184-329: B (or C) with fewer than 3 dims is constant
+(dim, dstate) (:194-195); n_groups = B.size(1) (:202); out has delta's
+dtype (:206); du / ddelta have the dtypes of u / delta, dA / dD /
+ddelta_bias are zero-initialised fp32 accumulators and variable dB / dC are
+fp32 (:271-287).  Unlike the reference, inputs are validated, and a fused z
+gate is available through the keyword-only ``z`` (forward then also returns
+the pre-gate output y, which ``backward`` needs to produce dz).
+
+There is no CPU fallback: tensors must live on a ROCm device and the
+library must be built.
+"""
+import ctypes
+
+import torch
+
+from . import _native as nat
+
+_ITYPES = {torch.float32: nat.SS_F32, torch.bfloat16: nat.SS_BF16, torch.float16: nat.SS_F16}
+
+
+def chunk_size():
+    """Steps per checkpoint of the state h in x."""
+    return int(nat.load().ss_chunk_size())
+
+
+def n_chunks(seqlen):
+    cs = chunk_size()
+    return (seqlen + cs - 1) // cs
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _require(cond, msg):
+    if not cond:
+        raise ValueError(f"selective_scan: {msg}")
+
+
+def _check_seq_tensor(name, t, shape, itype_dtype, device):
+    _require(t.device == device, f"{name} is on {t.device}, expected {device}")
+    _require(tuple(t.shape) == tuple(shape), f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    _require(t.dtype == itype_dtype, f"{name} has dtype {t.dtype}, expected {itype_dtype}")
+    _require(t.shape[-1] <= 1 or t.stride(-1) == 1, f"{name} must have unit stride along seqlen")
+
+
+def _fill_fwd_args(u, delta, A, B, C, D, delta_bias, delta_softplus, z, out, x, y):
+    _require(u.dim() == 3, f"u must be (batch, dim, seqlen), got shape {tuple(u.shape)}")
+    device = u.device
+    _require(device.type == "cuda", "tensors must be on a ROCm GPU device (no CPU path)")
+    _require(u.dtype in _ITYPES, f"unsupported dtype {u.dtype}")
+    itype = u.dtype
+    batch, dim, seqlen = u.shape
+    _check_seq_tensor("delta", delta, u.shape, itype, device)
+    _require(A.dim() == 2 and A.shape[0] == dim, f"A must be (dim, dstate), got {tuple(A.shape)}")
+    _require(A.dtype == torch.float32 and A.device == device, "A must be fp32 on the same device")
+    dstate = A.shape[1]
+    var_B, var_C = B.dim() >= 3, C.dim() >= 3
+    n_groups = B.shape[1] if var_B else (C.shape[1] if var_C else 1)
+    for name, M, var in (("B", B, var_B), ("C", C, var_C)):
+        _require(M.device == device, f"{name} is on {M.device}, expected {device}")
+        if var:
+            _require(M.dim() == 4 and M.shape[0] == batch and M.shape[1] == n_groups
+                     and M.shape[2] == dstate and M.shape[3] == seqlen,
+                     f"{name} must be (batch, n_groups, dstate, seqlen), got {tuple(M.shape)}")
+            _require(M.dtype == itype, f"{name} has dtype {M.dtype}, expected {itype}")
+            _require(seqlen <= 1 or M.stride(3) == 1, f"{name} must have unit stride along seqlen")
+        else:
+            _require(M.dim() == 2 and tuple(M.shape) == (dim, dstate),
+                     f"constant {name} must be (dim, dstate), got {tuple(M.shape)}")
+            _require(M.dtype == torch.float32, f"constant {name} must be fp32")
+    for name, v in (("D", D), ("delta_bias", delta_bias)):
+        if v is not None:
+            _require(v.shape == (dim,) and v.dtype == torch.float32 and v.device == device
+                     and v.is_contiguous(), f"{name} must be a contiguous fp32 ({dim},) tensor")
+    if z is not None:
+        _check_seq_tensor("z", z, u.shape, itype, device)
+    a = nat.FwdArgs()
+    a.batch, a.dim, a.seqlen, a.dstate, a.n_groups = batch, dim, seqlen, dstate, n_groups
+    a.itype = _ITYPES[itype]
+    a.is_var_B, a.is_var_C = int(var_B), int(var_C)
+    a.has_D, a.has_delta_bias, a.has_z = int(D is not None), int(delta_bias is not None), int(z is not None)
+    a.delta_softplus = int(bool(delta_softplus))
+    a.n_chunks = n_chunks(seqlen)
+    a.u_batch_stride, a.u_dim_stride = u.stride(0), u.stride(1)
+    a.delta_batch_stride, a.delta_dim_stride = delta.stride(0), delta.stride(1)
+    if z is not None:
+        a.z_batch_stride, a.z_dim_stride = z.stride(0), z.stride(1)
+    if out is not None:
+        a.out_batch_stride, a.out_dim_stride = out.stride(0), out.stride(1)
+    if y is not None:
+        a.y_batch_stride, a.y_dim_stride = y.stride(0), y.stride(1)
+    a.A_dim_stride, a.A_dstate_stride = A.stride(0), A.stride(1)
+    if var_B:
+        a.B_batch_stride, a.B_group_stride, a.B_dstate_stride = B.stride(0), B.stride(1), B.stride(2)
+    else:
+        a.B_batch_stride, a.B_group_stride, a.B_dstate_stride = 0, B.stride(0), B.stride(1)
+    if var_C:
+        a.C_batch_stride, a.C_group_stride, a.C_dstate_stride = C.stride(0), C.stride(1), C.stride(2)
+    else:
+        a.C_batch_stride, a.C_group_stride, a.C_dstate_stride = 0, C.stride(0), C.stride(1)
+    a.u, a.delta, a.A, a.B, a.C = _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C)
+    a.D, a.delta_bias, a.z = _ptr(D), _ptr(delta_bias), _ptr(z)
+    a.out, a.x, a.y = _ptr(out), _ptr(x), _ptr(y)
+    return a
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def forward(u, delta, A, B, C, D=None, delta_bias=None, use_delta_softplus=True, *, z=None):
+    """selective_scan.forward (selective_scan.cpp:184-244).
+
+    Returns [out, x]; with ``z`` given, [out, x, y] where out = y * silu(z)
+    and y is the pre-gate output saved for ``backward``.
+    """
+    lib = nat.load()
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    out = torch.empty_like(delta, memory_format=torch.contiguous_format)
+    x = torch.empty((batch, dim, n_chunks(seqlen), dstate), dtype=torch.float32, device=u.device)
+    y = torch.empty_like(out) if z is not None else None
+    a = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
+    with torch.cuda.device(u.device):
+        nat.check(lib.ss_fwd(ctypes.byref(a), _stream(u.device)), "selective_scan.forward")
+    return [out, x] if z is None else [out, x, y]
+
+
+def backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus, *, z=None, y=None):
+    """selective_scan.backward (selective_scan.cpp:246-329).
+
+    Returns [du, ddelta, dA, dB, dC, dD, ddelta_bias]; with ``z`` (and the
+    forward's ``y``) also dz as an eighth entry.
+    """
+    lib = nat.load()
+    _require(x is not None, "x (the forward's checkpoints) is required")
+    _require(z is None or y is not None, "y from the forward is required with z")
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    _require(x.dtype == torch.float32 and tuple(x.shape) == (batch, dim, n_chunks(seqlen), dstate)
+             and x.is_contiguous() and x.device == u.device, "x does not come from forward")
+    _check_seq_tensor("dout", dout, u.shape, delta.dtype, u.device)
+    if y is not None:
+        _check_seq_tensor("y", y, u.shape, delta.dtype, u.device)
+    du = torch.empty_like(u, memory_format=torch.contiguous_format)
+    ddelta = torch.empty_like(delta, memory_format=torch.contiguous_format)
+    dA = torch.zeros_like(A, dtype=torch.float32, memory_format=torch.contiguous_format)
+    dB = torch.zeros(B.shape, dtype=torch.float32, device=B.device)
+    dC = torch.zeros(C.shape, dtype=torch.float32, device=C.device)
+    dD = torch.zeros_like(D, memory_format=torch.contiguous_format) if D is not None else None
+    ddelta_bias = (torch.zeros_like(delta_bias, memory_format=torch.contiguous_format)
+                   if delta_bias is not None else None)
+    dz = torch.empty_like(z, memory_format=torch.contiguous_format) if z is not None else None
+    b = nat.BwdArgs()
+    b.f = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, None, x, y)
+    b.dout_batch_stride, b.dout_dim_stride = dout.stride(0), dout.stride(1)
+    b.du_batch_stride, b.du_dim_stride = du.stride(0), du.stride(1)
+    b.ddelta_batch_stride, b.ddelta_dim_stride = ddelta.stride(0), ddelta.stride(1)
+    if dz is not None:
+        b.dz_batch_stride, b.dz_dim_stride = dz.stride(0), dz.stride(1)
+    b.dout, b.du, b.ddelta, b.dz = _ptr(dout), _ptr(du), _ptr(ddelta), _ptr(dz)
+    b.dA, b.dB, b.dC, b.dD, b.ddelta_bias = _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(ddelta_bias)
+    with torch.cuda.device(u.device):
+        nat.check(lib.ss_bwd(ctypes.byref(b), _stream(u.device)), "selective_scan.backward")
+    res = [du, ddelta, dA, dB, dC, dD, ddelta_bias]
+    if z is not None:
+        res.append(dz)
+    return res

@@ -17,30 +17,37 @@
 // backwards over the chunk.  Per-step partial values are streamed to LDS four
 // steps at a time:
 //  - sums over states (sum_n g B, sum_n A g a h) are in-row transposed sums;
-//  - sums over channels (dB, dC) are first reduced over the wave's 4 rows,
-//    then over the workgroup's 4 waves, then added to global memory once per
-//    workgroup and (state, step).
+//  - sums over channels (dB, dC) are summed over the workgroup's 16 channels
+//    and added to global memory once per workgroup and (state, step).
 #include "ss_device.hpp"
 #include "ss_kernels.hpp"
 
 namespace ss {
 
-constexpr int kTiles = kChunk / kT;
-static_assert(kChunk % kT == 0, "chunk must be a whole number of tiles");
+static_assert(kChunk == kT, "the backward walks one 16-step tile per checkpoint chunk");
 
-// Per-wave transposition buffer: [row j][lane r][step k], 256 floats per row,
-// 16-step rows of a lane stored as four float4 with the float4 index XORed by
-// (r >> 2), so the float4 writes of a row hit 64 distinct banks.
-constexpr int kArr = kRows * kT * kT;   // 1024 floats
+// LDS layouts (gfx950 LDS serves 32 banks of 4 bytes; a float4 write is
+// served 8 lanes at a time, a dword read 32 lanes at a time).
+//
+// Per-wave transposition buffers for the sums over states: [row j][lane r]
+// [step k], 256 floats per row, rows 272 floats apart (so odd rows start 16
+// banks over).  The four steps 4c..4c+3 of lane r are stored as a float4 at
+// chunk slot c ^ ((r >> 1) & 3), so 8 consecutive lanes write 8 distinct
+// bank groups and the two rows read by one dword read hit disjoint bank
+// halves.
+constexpr int kTrRowStride = kT * kT + 16;                      // 272 floats
+constexpr int kTrArr = (kRows - 1) * kTrRowStride + kT * kT;    // 1072 floats
+__device__ __forceinline__ int tr_row(int j) { return j * kTrRowStride; }
+__device__ __forceinline__ int tr_pos(int r, int c4) { return r * kT + 4 * (c4 ^ ((r >> 1) & 3)); }
+// Workgroup buffer for the sums over channels: [channel][state][step] with
+// the same per-(state) swizzle; 16 x 256 floats per array.
+constexpr int kChArr = kChPerWG * kT * kT;     // 4096 floats
 
-__device__ __forceinline__ int swz(int r, int chunk4) { return r * kT + 4 * (chunk4 ^ (r >> 2)); }
-
-template <typename IT, int SPL>
+// kVarBC: B and C are both variable (the common case, no runtime switches).
+template <typename IT, int SPL, bool kVarBC>
 __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) {
-    // [wave][array: s1, s2, dB, dC][kArr]
-    __shared__ __attribute__((aligned(16))) float trb[kWaves * 4 * kArr];
-    // [array: dB, dC][wave][state n][16 steps] (swizzled like trb rows)
-    __shared__ __attribute__((aligned(16))) float wgb[2 * kWaves * kT * kT];
+    __shared__ __attribute__((aligned(16))) float trb[kWaves * 2 * kTrArr];   // [wave][s1, s2]
+    __shared__ __attribute__((aligned(16))) float chb[2 * kChArr];           // [dB, dC]
     const FwdParams& p = q.f;
 
     const int lane = threadIdx.x & 63;
@@ -55,23 +62,24 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     const int64_t g = c / p.dpg;
     const int N = int(p.dstate);
     const int64_t L = p.seqlen;
+    const bool var_B = kVarBC || p.var_B;
+    const bool var_C = kVarBC || p.var_C;
 
-    float* tr_s1 = trb + (w * 4 + 0) * kArr;
-    float* tr_s2 = trb + (w * 4 + 1) * kArr;
-    float* tr_dB = trb + (w * 4 + 2) * kArr;
-    float* tr_dC = trb + (w * 4 + 3) * kArr;
-    // streaming write position of this lane (chunk4 added per group)
-    const int wrow = j * kT * kT;
-    // in-row transposed sum: element (lane r', step r) of row j lives at
-    // wrow + r' * 16 + 4 * ((r >> 2) ^ (r' >> 2)) + (r & 3)
+    float* tr_s1 = trb + (w * 2 + 0) * kTrArr + tr_row(j);
+    float* tr_s2 = trb + (w * 2 + 1) * kTrArr + tr_row(j);
+    float* ch_dB = chb + (w * kRows + j) * kT * kT;
+    float* ch_dC = chb + kChArr + (w * kRows + j) * kT * kT;
+    // in-row transposed sum: element (lane r', step r) of the row lives at
+    // r' * 16 + 4 * ((r >> 2) ^ ((r' >> 1) & 3)) + (r & 3) from the row base
     int toff[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) toff[m] = wrow + 4 * ((r >> 2) ^ m) + (r & 3);
+    for (int m = 0; m < 4; ++m) toff[m] = 4 * ((r >> 2) ^ m) + (r & 3);
 
     const IT* u = static_cast<const IT*>(p.u) + b * p.u_bs + c * p.u_ds;
     const IT* dl = static_cast<const IT*>(p.delta) + b * p.dl_bs + c * p.dl_ds;
-    const IT* zp = p.has_z ? static_cast<const IT*>(p.z) + b * p.z_bs + c * p.z_ds : nullptr;
-    const IT* yp = p.has_z ? static_cast<const IT*>(p.y) + b * p.y_bs + c * p.y_ds : nullptr;
+    // without a z gate zp / yp alias u so that their (unused) loads stay unconditional
+    const IT* zp = p.has_z ? static_cast<const IT*>(p.z) + b * p.z_bs + c * p.z_ds : u;
+    const IT* yp = p.has_z ? static_cast<const IT*>(p.y) + b * p.y_bs + c * p.y_ds : u;
     const IT* dop = static_cast<const IT*>(q.dout) + b * q.do_bs + c * q.do_ds;
     IT* dup = static_cast<IT*>(q.du) + b * q.du_bs + c * q.du_ds;
     IT* ddp = static_cast<IT*>(q.ddelta) + b * q.dd_bs + c * q.dd_ds;
@@ -88,6 +96,7 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
+    const bool pad_states = (N % 16) != 0;
 
     float A2[SPL], Av[SPL], Bc[SPL], Cc[SPL];
     float gcar[SPL], acar[SPL], dA_acc[SPL], dBc_acc[SPL], dCc_acc[SPL];
@@ -97,8 +106,8 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
         const bool nv = n < N;
         Av[s] = nv ? p.A[c * p.A_ds + n * p.A_ns] : 0.f;
         A2[s] = Av[s] * kLog2e;
-        Bc[s] = (!p.var_B && nv) ? Bc_base[n * p.B_ns] : 0.f;
-        Cc[s] = (!p.var_C && nv) ? Cc_base[n * p.C_ns] : 0.f;
+        Bc[s] = (!var_B && nv) ? Bc_base[n * p.B_ns] : 0.f;
+        Cc[s] = (!var_C && nv) ? Cc_base[n * p.C_ns] : 0.f;
         gcar[s] = 0.f;      // g_{t+1} entering the chunk from the right
         acar[s] = 1.f;      // a_{t+1} entering the chunk from the right
         dA_acc[s] = 0.f;
@@ -107,199 +116,222 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     }
     float dD_acc = 0.f, db_acc = 0.f;
 
-    for (int64_t ck = p.n_chunks - 1; ck >= 0; --ck) {
-        const int64_t tb = ck * kChunk;
-        // per-step inputs of step tb + 16 qq + r, one per tile of the chunk
-        float uu[kTiles], dt[kTiles], dtu[kTiles], dy[kTiles], pre[kTiles], dov[kTiles], zz[kTiles];
-        bool tv[kTiles];
-        int nval[kTiles];
+    // B / C rows of state group s for the chunk at t0; padding states get
+    // C = 0 so that their adjoint g stays 0.
+    auto load_bc = [&](int64_t t0, int s, float (&Bo)[kT], float (&Co)[kT]) {
+        const int n = 16 * s + r;
+        const bool nv = n < N;
+        const int nn = nv ? n : N - 1;
+        if (var_B) load_tile16<IT>(Bv_base + nn * p.B_ns, t0, L, p.vec_B != 0, Bo);
+        else {
 #pragma unroll
-        for (int qq = 0; qq < kTiles; ++qq) {
-            const int64_t t = tb + kT * qq + r;
-            tv[qq] = t < L;
-            const int64_t rem = L - (tb + kT * qq);
-            nval[qq] = int(rem <= 0 ? 0 : (rem < kT ? rem : kT));
-            uu[qq] = tv[qq] ? io<IT>::load(u + t) : 0.f;
-            pre[qq] = (tv[qq] ? io<IT>::load(dl + t) : 0.f) + bias;
-            dt[qq] = p.softplus ? softplus20(pre[qq]) : pre[qq];
-            if (!tv[qq]) dt[qq] = 0.f;
-            dtu[qq] = dt[qq] * uu[qq];
-            dov[qq] = tv[qq] ? io<IT>::load(dop + t) : 0.f;
-            zz[qq] = (p.has_z && tv[qq]) ? io<IT>::load(zp + t) : 0.f;
-            dy[qq] = p.has_z ? dov[qq] * zz[qq] * sigmoidf_(zz[qq]) : dov[qq];
-            if (!cval) dy[qq] = 0.f;     // padding channels contribute nothing
+            for (int k = 0; k < kT; ++k) Bo[k] = Bc[s];
         }
-        float s1_red[kTiles], s2_red[kTiles];
+        if (var_C) load_tile16<IT>(Cv_base + nn * p.C_ns, t0, L, p.vec_C != 0, Co);
+        else {
 #pragma unroll
-        for (int qq = 0; qq < kTiles; ++qq) { s1_red[qq] = 0.f; s2_red[qq] = 0.f; }
+            for (int k = 0; k < kT; ++k) Co[k] = Cc[s];
+        }
+        if (pad_states && !nv) {
+#pragma unroll
+            for (int k = 0; k < kT; ++k) Co[k] = 0.f;
+        }
+    };
+    // checkpoint h at the end of chunk ck - 1 (0 before the first chunk)
+    auto load_h0 = [&](int64_t ck, int s) {
+        const int n = 16 * s + r;
+        const int nn = n < N ? n : N - 1;
+        const float v = xrow[(ck > 0 ? ck - 1 : 0) * N + nn];
+        return ck > 0 ? v : 0.f;
+    };
+
+    // Per-step inputs of step 16 ck + r (streams from HBM), loaded two chunks
+    // ahead and shifted along; chunk indices below 0 re-read chunk 0.
+    struct Step { float u, dl, dout, z, y; };
+    auto load_step = [&](int64_t ck, Step& S) {
+        const int64_t t = (ck >= 0 ? ck : 0) * kT + r;
+        if (t - r + kT <= L) {
+            S.u = load_at(u, t); S.dl = load_at(dl, t); S.dout = load_at(dop, t);
+            S.z = load_at(zp, t); S.y = load_at(yp, t);
+        } else {
+            S.u = load_or0(u, t, L); S.dl = load_or0(dl, t, L); S.dout = load_or0(dop, t, L);
+            S.z = load_or0(zp, t, L); S.y = load_or0(yp, t, L);
+        }
+    };
+    // B / C rows and checkpoint of the chunk (single state group), one chunk ahead.
+    struct Rows { float h0; float B[kT], C[kT]; };
+    auto load_rows = [&](int64_t ck, Rows& R) {
+        if constexpr (SPL == 1) {
+            const int64_t ckc = ck >= 0 ? ck : 0;
+            load_bc(ckc * kT, 0, R.B, R.C);
+            R.h0 = load_h0(ckc, 0);
+        }
+    };
+
+    auto compute_chunk = [&](int64_t ck, const Step& S, Rows& R) {
+        const int64_t t0 = ck * kT;
+        const int64_t t = t0 + r;
+        const bool tv = t < L;
+        const int nval = int(L - t0 < kT ? L - t0 : kT);
+        const float pre = S.dl + bias;
+        float dt = p.softplus ? softplus20(pre) : pre;
+        if (!tv) dt = 0.f;
+        const float dtu = dt * S.u;
+        const float sgz = sigmoidf_(S.z);
+        float dy = p.has_z ? S.dout * S.z * sgz : S.dout;
+        if (!cval) dy = 0.f;     // padding channels contribute nothing
+        float s1_red = 0.f, s2_red = 0.f;
 
 #pragma unroll
         for (int s = 0; s < SPL; ++s) {
             const int n = 16 * s + r;
             const bool nv = n < N;
-            const float h0 = (ck > 0 && nv) ? xrow[(ck - 1) * N + n] : 0.f;
+            float Bl[kT], Cl[kT];
+            float h0 = 0.f;
+            if constexpr (SPL > 1) {
+                load_bc(t0, s, Bl, Cl);
+                h0 = load_h0(ck, s);
+            } else {
+                h0 = R.h0;
+            }
+            const float (&Bt)[kT] = (SPL == 1) ? R.B : Bl;
+            const float (&Ct)[kT] = (SPL == 1) ? R.C : Cl;
 
             // ---- recompute a_t and h_t of the chunk from the checkpoint
-            float Bt[kChunk], as[kChunk], hs[kChunk];
+            float as[kT], hs[kT];
             float hcur = h0;
             const float a2 = A2[s];
-            static_for<kTiles>([&](auto QQ) {
-                constexpr int qq = decltype(QQ)::value;
-                float tmp[kT];
-                if (p.var_B) {
-                    load16<IT>(Bv_base + n * p.B_ns + tb + kT * qq, nv ? nval[qq] : 0, p.vec_B != 0, tmp);
-                } else {
-#pragma unroll
-                    for (int k = 0; k < kT; ++k) tmp[k] = Bc[s];
-                }
-                static_for<kT>([&](auto K) {
-                    constexpr int k = decltype(K)::value;
-                    Bt[kT * qq + k] = tmp[k];
-                    const float a = __builtin_amdgcn_exp2f(row_bcast<k>(dt[qq]) * a2);
-                    hcur = __builtin_fmaf(a, hcur, row_bcast<k>(dtu[qq]) * tmp[k]);
-                    as[kT * qq + k] = a;
-                    hs[kT * qq + k] = hcur;
-                });
+            static_for<kT>([&](auto K) {
+                constexpr int k = decltype(K)::value;
+                const float a = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
+                hcur = __builtin_fmaf(a, hcur, row_bcast<k>(dtu) * Bt[k]);
+                as[k] = a;
+                hs[k] = hcur;
             });
 
-            // ---- adjoint, last step of the chunk first
+            // ---- adjoint, last step of the chunk first, streamed to LDS four steps at a time
             float gv = gcar[s];
             float anext = acar[s];
             const float av = Av[s];
-            static_for<kTiles>([&](auto QQ) {
-                constexpr int qq = kTiles - 1 - decltype(QQ)::value;
-                const int64_t t0 = tb + kT * qq;
-                float Ct[kT];
-                if (p.var_C) {
-                    load16<IT>(Cv_base + n * p.C_ns + t0, nv ? nval[qq] : 0, p.vec_C != 0, Ct);
-                } else {
-#pragma unroll
-                    for (int k = 0; k < kT; ++k) Ct[k] = Cc[s];
-                }
-                float dAq = 0.f, dBq = 0.f, dCq = 0.f;
-                static_for<4>([&](auto KG) {
-                    constexpr int kg = 3 - decltype(KG)::value;
-                    float s1p[4], s2p[4], dBp[4], dCp[4];
-                    static_for<4>([&](auto KI) {
-                        constexpr int ki = 3 - decltype(KI)::value;
-                        constexpr int k = 4 * kg + ki;
-                        constexpr int ii = kT * qq + k;
-                        const float dyk = row_bcast<k>(dy[qq]);
-                        gv = __builtin_fmaf(anext, gv, dyk * Ct[k]);
-                        float hprev;
-                        if constexpr (ii == 0) hprev = h0;
-                        else hprev = hs[ii - 1];
-                        const float gah = gv * (as[ii] * hprev);
-                        dAq = __builtin_fmaf(row_bcast<k>(dt[qq]), gah, dAq);
-                        s2p[ki] = av * gah;
-                        s1p[ki] = gv * Bt[ii];
-                        dBp[ki] = gv * row_bcast<k>(dtu[qq]);
-                        dCp[ki] = dyk * hs[ii];
-                        anext = as[ii];
-                    });
-                    const int o = wrow + swz(r, kg);
-                    *reinterpret_cast<float4*>(tr_s1 + o) = make_float4(s1p[0], s1p[1], s1p[2], s1p[3]);
-                    *reinterpret_cast<float4*>(tr_s2 + o) = make_float4(s2p[0], s2p[1], s2p[2], s2p[3]);
-                    if (p.var_B) {
-                        if (q.wg_reduce) {
-                            *reinterpret_cast<float4*>(tr_dB + o) = make_float4(dBp[0], dBp[1], dBp[2], dBp[3]);
-                        } else if (cval && nv) {
-#pragma unroll
-                            for (int ki = 0; ki < 4; ++ki)
-                                if (4 * kg + ki < nval[qq]) atomicAdd(dBrow + n * L + t0 + 4 * kg + ki, dBp[ki]);
-                        }
-                    } else {
-                        dBq += (dBp[0] + dBp[1]) + (dBp[2] + dBp[3]);
-                    }
-                    if (p.var_C) {
-                        if (q.wg_reduce) {
-                            *reinterpret_cast<float4*>(tr_dC + o) = make_float4(dCp[0], dCp[1], dCp[2], dCp[3]);
-                        } else if (cval && nv) {
-#pragma unroll
-                            for (int ki = 0; ki < 4; ++ki)
-                                if (4 * kg + ki < nval[qq]) atomicAdd(dCrow + n * L + t0 + 4 * kg + ki, dCp[ki]);
-                        }
-                    } else {
-                        dCq += (dCp[0] + dCp[1]) + (dCp[2] + dCp[3]);
-                    }
+            float dAq = 0.f, dBq = 0.f, dCq = 0.f;
+            static_for<4>([&](auto KG) {
+                constexpr int kg = 3 - decltype(KG)::value;
+                float s1p[4], s2p[4], dBp[4], dCp[4];
+                static_for<4>([&](auto KI) {
+                    constexpr int ki = 3 - decltype(KI)::value;
+                    constexpr int k = 4 * kg + ki;
+                    const float dyk = row_bcast<k>(dy);
+                    gv = __builtin_fmaf(anext, gv, dyk * Ct[k]);
+                    float hprev;
+                    if constexpr (k == 0) hprev = h0;
+                    else hprev = hs[k - 1];
+                    const float gah = gv * (as[k] * hprev);
+                    dAq = __builtin_fmaf(row_bcast<k>(dt), gah, dAq);
+                    s2p[ki] = av * gah;
+                    s1p[ki] = gv * Bt[k];
+                    dBp[ki] = gv * row_bcast<k>(dtu);
+                    dCp[ki] = dyk * hs[k];
+                    anext = as[k];
                 });
-                dA_acc[s] += dAq;
-                dBc_acc[s] += dBq;
-                dCc_acc[s] += dCq;
-
-                // in-row transposed sums over states
-                float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+                const int o = tr_pos(r, kg);
+                *reinterpret_cast<float4*>(tr_s1 + o) = make_float4(s1p[0], s1p[1], s1p[2], s1p[3]);
+                *reinterpret_cast<float4*>(tr_s2 + o) = make_float4(s2p[0], s2p[1], s2p[2], s2p[3]);
+                if (var_B) {
+                    if (q.wg_reduce) {
+                        *reinterpret_cast<float4*>(ch_dB + o) = make_float4(dBp[0], dBp[1], dBp[2], dBp[3]);
+                    } else if (cval && nv) {
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-#pragma unroll
-                    for (int i = 0; i < 4; i += 2) {
-                        a0 += tr_s1[toff[m] + (4 * m + i) * kT];
-                        a1 += tr_s1[toff[m] + (4 * m + i + 1) * kT];
-                        b0 += tr_s2[toff[m] + (4 * m + i) * kT];
-                        b1 += tr_s2[toff[m] + (4 * m + i + 1) * kT];
+                        for (int ki = 0; ki < 4; ++ki)
+                            if (4 * kg + ki < nval) atomicAdd(dBrow + n * L + t0 + 4 * kg + ki, dBp[ki]);
                     }
+                } else {
+                    dBq += (dBp[0] + dBp[1]) + (dBp[2] + dBp[3]);
                 }
-                s1_red[qq] += a0 + a1;
-                s2_red[qq] += b0 + b1;
-
-                // sums over channels: the wave's 4 rows, then the workgroup's waves
-                if (q.wg_reduce && (p.var_B || p.var_C)) {
-                    const int ro = swz(r, j);   // this lane sums steps 4j..4j+3 of state r
+                if (var_C) {
+                    if (q.wg_reduce) {
+                        *reinterpret_cast<float4*>(ch_dC + o) = make_float4(dCp[0], dCp[1], dCp[2], dCp[3]);
+                    } else if (cval && nv) {
 #pragma unroll
-                    for (int arr = 0; arr < 2; ++arr) {
-                        const bool use = arr == 0 ? p.var_B : p.var_C;
-                        if (!use) continue;
-                        const float* src = arr == 0 ? tr_dB : tr_dC;
-                        float4 acc = *reinterpret_cast<const float4*>(src + ro);
-#pragma unroll
-                        for (int jj = 1; jj < kRows; ++jj) {
-                            const float4 v = *reinterpret_cast<const float4*>(src + jj * kT * kT + ro);
-                            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-                        }
-                        *reinterpret_cast<float4*>(wgb + (arr * kWaves + w) * kT * kT + ro) = acc;
+                        for (int ki = 0; ki < 4; ++ki)
+                            if (4 * kg + ki < nval) atomicAdd(dCrow + n * L + t0 + 4 * kg + ki, dCp[ki]);
                     }
-                    __syncthreads();
-                    const int tid = threadIdx.x;
-                    const int nl = tid >> 4, k = tid & 15;
-                    const int ridx = nl * kT + 4 * ((k >> 2) ^ (nl >> 2)) + (k & 3);
-                    const int ng = 16 * s + nl;
-#pragma unroll
-                    for (int arr = 0; arr < 2; ++arr) {
-                        const bool use = arr == 0 ? p.var_B : p.var_C;
-                        if (!use) continue;
-                        float sum = 0.f;
-#pragma unroll
-                        for (int ww = 0; ww < kWaves; ++ww) sum += wgb[(arr * kWaves + ww) * kT * kT + ridx];
-                        float* dst = arr == 0 ? dBrow : dCrow;
-                        if (ng < N && k < nval[qq]) atomicAdd(dst + ng * L + t0 + k, sum);
-                    }
-                    __syncthreads();
+                } else {
+                    dCq += (dCp[0] + dCp[1]) + (dCp[2] + dCp[3]);
                 }
             });
             gcar[s] = gv;
             acar[s] = anext;
-        }
+            dA_acc[s] += dAq;
+            dBc_acc[s] += dBq;
+            dCc_acc[s] += dCq;
 
-        // ---- per-step outputs of steps tb + 16 qq + r
+            // in-row transposed sums over states
+            float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
 #pragma unroll
-        for (int qq = 0; qq < kTiles; ++qq) {
-            const int64_t t = tb + kT * qq + r;
-            const float s1 = s1_red[qq], s2 = s2_red[qq];
-            const float du = Dv * dy[qq] + dt[qq] * s1;
-            const float ddt = uu[qq] * s1 + s2;
-            const float dd = (p.softplus && pre[qq] <= 20.f) ? ddt * sigmoidf_(pre[qq]) : ddt;
-            if (tv[qq] && cval) {
-                io<IT>::store(dup + t, du);
-                io<IT>::store(ddp + t, dd);
-                if (p.has_z) {
-                    const float sg = sigmoidf_(zz[qq]);
-                    const float yv = io<IT>::load(yp + t);
-                    io<IT>::store(dzp + t, dov[qq] * yv * sg * (1.f + zz[qq] * (1.f - sg)));
+            for (int rr = 0; rr < kT; rr += 2) {
+                a0 += tr_s1[toff[(rr >> 1) & 3] + rr * kT];
+                a1 += tr_s1[toff[((rr + 1) >> 1) & 3] + (rr + 1) * kT];
+                b0 += tr_s2[toff[(rr >> 1) & 3] + rr * kT];
+                b1 += tr_s2[toff[((rr + 1) >> 1) & 3] + (rr + 1) * kT];
+            }
+            s1_red += a0 + a1;
+            s2_red += b0 + b1;
+
+            // sums over the workgroup's 16 channels, one global add per (state, step)
+            if (q.wg_reduce && (var_B || var_C)) {
+                __syncthreads();
+                const int tid = threadIdx.x;
+                const int nl = tid >> 4, k = tid & 15;
+                const int ridx = nl * kT + 4 * ((k >> 2) ^ ((nl >> 1) & 3)) + (k & 3);
+                const int ng = 16 * s + nl;
+#pragma unroll
+                for (int arr = 0; arr < 2; ++arr) {
+                    const bool use = arr == 0 ? var_B : var_C;
+                    if (!use) continue;
+                    const float* src = chb + arr * kChArr + ridx;
+                    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                    for (int ch = 0; ch < kChPerWG; ch += 2) {
+                        s0 += src[ch * kT * kT];
+                        s1 += src[(ch + 1) * kT * kT];
+                    }
+                    float* dst = arr == 0 ? dBrow : dCrow;
+                    if (ng < N && k < nval) atomicAdd(dst + ng * L + t0 + k, s0 + s1);
                 }
-                dD_acc += dy[qq] * uu[qq];
-                db_acc += dd;
+                __syncthreads();
             }
         }
+
+        // ---- per-step outputs of step t0 + r
+        const float du = Dv * dy + dt * s1_red;
+        const float ddt = S.u * s1_red + s2_red;
+        const float dd = p.softplus ? ddt * sigmoidf_(pre) : ddt;
+        if (tv && cval) {
+            io<IT>::store(dup + t, du);
+            io<IT>::store(ddp + t, dd);
+            if (p.has_z) io<IT>::store(dzp + t, S.dout * S.y * sgz * (1.f + S.z * (1.f - sgz)));
+            dD_acc += dy * S.u;
+            db_acc += dd;
+        }
+    };
+
+    // per-step inputs: three chunks in flight (shifted by register moves);
+    // B / C rows: two buffers alternated by unrolling the chunk loop twice
+    const int64_t nck = p.n_chunks;
+    Step S0, S1, S2;
+    Rows R0, R1;
+    load_step(nck - 1, S0);
+    load_step(nck - 2, S1);
+    load_rows(nck - 1, R0);
+    for (int64_t ck = nck - 1; ck >= 0; ck -= 2) {
+        load_step(ck - 2, S2);
+        load_rows(ck - 1, R1);
+        compute_chunk(ck, S0, R0);
+        S0 = S1; S1 = S2;
+        load_step(ck - 3, S2);
+        load_rows(ck - 2, R0);
+        if (ck - 1 >= 0) compute_chunk(ck - 1, S0, R1);
+        S0 = S1; S1 = S2;
     }
 
     // ---- per-channel and per-(channel, state) sums over time and batch
@@ -315,8 +347,8 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
             const int n = 16 * s + r;
             if (n < N) {
                 atomicAdd(q.dA + c * N + n, dA_acc[s]);
-                if (!p.var_B) atomicAdd(q.dB + c * N + n, dBc_acc[s]);
-                if (!p.var_C) atomicAdd(q.dC + c * N + n, dCc_acc[s]);
+                if (!var_B) atomicAdd(q.dB + c * N + n, dBc_acc[s]);
+                if (!var_C) atomicAdd(q.dC + c * N + n, dCc_acc[s]);
             }
         }
     }
@@ -328,11 +360,14 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     const dim3 grid(unsigned(nblk * p.f.batch));
     const dim3 block(kThreads);
     const int spl = int((p.f.dstate + 15) / 16);
-    if (spl <= 1) hipLaunchKernelGGL((ss_bwd_kernel<IT, 1>), grid, block, 0, stream, p);
-    else if (spl <= 2) hipLaunchKernelGGL((ss_bwd_kernel<IT, 2>), grid, block, 0, stream, p);
-    else if (spl <= 4) hipLaunchKernelGGL((ss_bwd_kernel<IT, 4>), grid, block, 0, stream, p);
-    else if (spl <= 8) hipLaunchKernelGGL((ss_bwd_kernel<IT, 8>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((ss_bwd_kernel<IT, 16>), grid, block, 0, stream, p);
+    const bool vbc = p.f.var_B && p.f.var_C;
+    if (spl <= 1) {
+        if (vbc) hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, false>), grid, block, 0, stream, p);
+    } else if (spl <= 2) hipLaunchKernelGGL((ss_bwd_kernel<IT, 2, false>), grid, block, 0, stream, p);
+    else if (spl <= 4) hipLaunchKernelGGL((ss_bwd_kernel<IT, 4, false>), grid, block, 0, stream, p);
+    else if (spl <= 8) hipLaunchKernelGGL((ss_bwd_kernel<IT, 8, false>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((ss_bwd_kernel<IT, 16, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 

@@ -19,7 +19,7 @@ constexpr int kRows = 4;          // channels per wave
 constexpr int kWaves = 4;         // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kChPerWG = kRows * kWaves;
-constexpr int kChunk = 32;        // steps per checkpoint of the state h
+constexpr int kChunk = 16;        // steps per checkpoint of the state h
 constexpr int kMaxSPL = 16;       // state groups: dstate <= 16 * kMaxSPL = 256
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -56,27 +56,42 @@ template <> struct io<_Float16> {
     static __device__ __forceinline__ void store(_Float16* p, float v) { *p = _Float16(v); }
 };
 
-// Loads 16 consecutive elements p[0..15] as float; positions >= nvalid read
-// as 0.  `vec` says p is 16-byte aligned (then full tiles use 16-byte loads).
+// Element p[t] as float (t known to be in range).
 template <typename T>
-__device__ __forceinline__ void load16(const T* __restrict__ p, int nvalid, bool vec, float (&o)[16]) {
-    if (nvalid >= 16 && vec) {
+__device__ __forceinline__ float load_at(const T* __restrict__ p, int64_t t) { return io<T>::load(p + t); }
+
+// Element p[t] as float, or 0 when t >= L.  The address is clamped to the
+// last element so the load is unconditional (no branch, no divergence).
+template <typename T>
+__device__ __forceinline__ float load_or0(const T* __restrict__ p, int64_t t, int64_t L) {
+    const float v = io<T>::load(p + (t < L ? t : L - 1));
+    return t < L ? v : 0.f;
+}
+
+// Loads row[t0 .. t0+15] as float; steps >= L read as 0.  `vec` says
+// row + t0 is 16-byte aligned; full tiles then use 16-byte loads.  The
+// branch depends only on uniform values, so no lane waits on another.
+template <typename T>
+__device__ __forceinline__ void load_tile16(const T* __restrict__ row, int64_t t0, int64_t L, bool vec,
+                                            float (&o)[16]) {
+    const T* p = row + t0;
+    if (vec && t0 + 16 <= L) {
         if constexpr (sizeof(T) == 4) {
             const float4* q = reinterpret_cast<const float4*>(p);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float4 v = q[i];
+                const float4 v = q[i];
                 o[4 * i] = v.x; o[4 * i + 1] = v.y; o[4 * i + 2] = v.z; o[4 * i + 3] = v.w;
             }
         } else {
             const uint4* q = reinterpret_cast<const uint4*>(p);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                uint4 v = q[i];
-                uint32_t w[4] = {v.x, v.y, v.z, v.w};
+                const uint4 v = q[i];
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    if constexpr (sizeof(T) == 2 && __is_same(T, bf16_t)) {
+                    if constexpr (__is_same(T, bf16_t)) {
                         o[8 * i + 2 * k] = __uint_as_float(w[k] << 16);
                         o[8 * i + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
                     } else {
@@ -88,8 +103,83 @@ __device__ __forceinline__ void load16(const T* __restrict__ p, int nvalid, bool
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] = i < nvalid ? io<T>::load(p + i) : 0.f;
+        for (int i = 0; i < 16; ++i) o[i] = load_or0(row, t0 + i, L);
     }
+}
+
+// row[t0 .. t0+15] as float with 16-byte loads (row + t0 16-byte aligned,
+// whole tile in range).
+template <typename T>
+__device__ __forceinline__ void load16_vec(const T* __restrict__ p, float (&o)[16]) {
+    if constexpr (sizeof(T) == 4) {
+        const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = q[i];
+            o[4 * i] = v.x; o[4 * i + 1] = v.y; o[4 * i + 2] = v.z; o[4 * i + 3] = v.w;
+        }
+    } else {
+        const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint4 v = q[i];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if constexpr (__is_same(T, bf16_t)) {
+                    o[8 * i + 2 * k] = __uint_as_float(w[k] << 16);
+                    o[8 * i + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+                } else {
+                    o[8 * i + 2 * k] = float(__builtin_bit_cast(_Float16, uint16_t(w[k] & 0xffffu)));
+                    o[8 * i + 2 * k + 1] = float(__builtin_bit_cast(_Float16, uint16_t(w[k] >> 16)));
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------- B / C tile staging --
+// A 16-state x 16-step tile of B (or C) is staged in LDS as 16-byte chunks:
+// chunk i (steps 4i..4i+3 for fp32, 8i..8i+7 for 16-bit types) of state row
+// n goes to chunk slot tile_slot(n, i), chosen so that 8 lanes reading chunk
+// i of rows 0..7 with ds_read_b128 hit 8 distinct groups of 4 banks.
+//   fp32 : 4 chunks per row, slot 4 n + ((i + (n >> 1)) & 3)       (64 slots)
+//   16-bit: 2 chunks per row, slot 2 n + ((i + (n >> 2)) & 1)      (32 slots)
+template <int kChunksPerRow>
+__device__ __forceinline__ int tile_slot(int n, int i) {
+    if constexpr (kChunksPerRow == 4) return 4 * n + ((i + (n >> 1)) & 3);
+    else return 2 * n + ((i + (n >> 2)) & 1);
+}
+// Inverse: the (row, chunk) stored in slot p.
+template <int kChunksPerRow>
+__device__ __forceinline__ void tile_slot_inv(int p, int& n, int& i) {
+    if constexpr (kChunksPerRow == 4) { n = p >> 2; i = ((p & 3) - (n >> 1)) & 3; }
+    else { n = p >> 1; i = ((p & 1) - (n >> 2)) & 1; }
+}
+
+// Eight 16-bit values (bf16 or fp16, 16-byte aligned) as float.
+template <typename T>
+__device__ __forceinline__ void load8_16(const T* p, float (&o)[8]) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if constexpr (__is_same(T, bf16_t)) {
+            o[2 * k] = __uint_as_float(w[k] << 16);
+            o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+        } else {
+            o[2 * k] = float(__builtin_bit_cast(_Float16, uint16_t(w[k] & 0xffffu)));
+            o[2 * k + 1] = float(__builtin_bit_cast(_Float16, uint16_t(w[k] >> 16)));
+        }
+    }
+}
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load and store of the wave (vmcnt(0)), which
+// would drain the loads prefetched for the next tile; the kernels here only
+// exchange data through LDS across a barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // ------------------------------------------------------- cross-lane ops --
@@ -113,24 +203,30 @@ __device__ __forceinline__ float row_allsum(float v) {
 }
 
 // In-row transposed sum: lane r of row j passes v[0..15]; the result in lane
-// r is sum over the row's lanes r' of v_{r'}[r].  `wbuf` is this wave's
-// private scratch of kTrWave floats.  Only lanes of the calling wave touch
-// it and a wave executes its LDS operations in order, so no barrier is
-// needed; the compiler cannot reorder the accesses because their offsets
-// depend on the lane index.
-__device__ __forceinline__ float row_transpose_sum(float* wbuf, const float (&v)[16], int j, int r) {
+// r is sum over the row's lanes r' of v_{r'}[r].  `wbuf` is a per-wave
+// scratch of kTrWave floats.  Only lanes of the calling wave touch it and a
+// wave executes its LDS operations in order, so no barrier is needed; the
+// compiler cannot reorder the accesses because their offsets depend on the
+// lane index.  Split in a write and a read so that other work can be placed
+// between them.
+__device__ __forceinline__ void row_transpose_write(float* wbuf, const float (&v)[16], int j, int r) {
     float* wp = wbuf + j * kTrRow + r * kTrStride;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         *reinterpret_cast<float4*>(wp + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+__device__ __forceinline__ float row_transpose_read(const float* wbuf, int j, int r) {
     const float* rp = wbuf + j * kTrRow + r;
-    float s0 = 0.f, s1 = 0.f;
+    // all 16 reads are issued before the first add (one LDS round trip)
+    float v[16];
 #pragma unroll
-    for (int k = 0; k < 16; k += 2) {
-        s0 += rp[k * kTrStride];
-        s1 += rp[(k + 1) * kTrStride];
+    for (int k = 0; k < 16; ++k) v[k] = rp[k * kTrStride];
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int k = 0; k < w; ++k) v[k] += v[k + w];
     }
-    return s0 + s1;
+    return v[0];
 }
 
 // ------------------------------------------------------------ unrolling --
@@ -145,10 +241,26 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // ----------------------------------------------------------------- math --
-__device__ __forceinline__ float softplus20(float x) {
-    // log1p(exp(x)) below the threshold 20, x above (forward_kernel.cu:217-221)
-    return x <= 20.f ? log1pf(__expf(x)) : x;
+// All branch-free: a per-lane branch would make the compiler wait for every
+// outstanding load, including the prefetch of the next tile.
+
+// log(1 + e) for e >= 0, accurate for small e: log(u) * e / (u - 1) with
+// u = 1 + e rounded (Goldberg's compensation), and e itself when u == 1.
+__device__ __forceinline__ float log1p_pos(float e) {
+    const float u = 1.f + e;   // in [1, 2]: no denormal or range handling needed
+    const float l = (__builtin_amdgcn_logf(u) * 0.69314718055994531f) * __builtin_amdgcn_rcpf(u - 1.f) * e;
+    return u == 1.f ? e : l;
 }
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// softplus with the reference's threshold rule, log1p(exp(x)) for x <= 20
+// and x above (forward_kernel.cu:217-221), computed as the identity
+// max(x, 0) + log1p(exp(-|x|)); for x > 20 the second term (< 2.1e-9) is
+// below half an ulp of x, so the result is exactly x as in the reference.
+__device__ __forceinline__ float softplus20(float x) {
+    return fmaxf(x, 0.f) + log1p_pos(__expf(-fabsf(x)));
+}
+
+// 1 / (1 + exp(-x)); exp overflow gives 1 / inf = 0.
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 }  // namespace ss

@@ -120,49 +120,64 @@ def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
+    """Forward into caller-allocated ``out`` (delta's dtype), ``x`` (fp32
+    (batch, dim, n_chunks, dstate) contiguous) and, with ``z``, ``y``."""
+    lib = nat.load()
+    _require(out is not None and x is not None, "out and x are required")
+    _check_seq_tensor("out", out, u.shape, delta.dtype, u.device)
+    batch, dim, seqlen = u.shape
+    _require(x.dtype == torch.float32 and x.is_contiguous() and x.device == u.device
+             and tuple(x.shape) == (batch, dim, n_chunks(seqlen), A.shape[1]),
+             "x must be a contiguous fp32 (batch, dim, n_chunks, dstate) tensor")
+    if y is not None:
+        _check_seq_tensor("y", y, u.shape, delta.dtype, u.device)
+    a = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
+    with torch.cuda.device(u.device):
+        nat.check(lib.ss_fwd(ctypes.byref(a), _stream(u.device)), "selective_scan.forward")
+
+
 def forward(u, delta, A, B, C, D=None, delta_bias=None, use_delta_softplus=True, *, z=None):
     """selective_scan.forward (selective_scan.cpp:184-244).
 
     Returns [out, x]; with ``z`` given, [out, x, y] where out = y * silu(z)
     and y is the pre-gate output saved for ``backward``.
     """
-    lib = nat.load()
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     out = torch.empty_like(delta, memory_format=torch.contiguous_format)
     x = torch.empty((batch, dim, n_chunks(seqlen), dstate), dtype=torch.float32, device=u.device)
     y = torch.empty_like(out) if z is not None else None
-    a = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
-    with torch.cuda.device(u.device):
-        nat.check(lib.ss_fwd(ctypes.byref(a), _stream(u.device)), "selective_scan.forward")
+    forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z=z, y=y)
     return [out, x] if z is None else [out, x, y]
 
 
-def backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus, *, z=None, y=None):
-    """selective_scan.backward (selective_scan.cpp:246-329).
-
-    Returns [du, ddelta, dA, dB, dC, dD, ddelta_bias]; with ``z`` (and the
-    forward's ``y``) also dz as an eighth entry.
-    """
+def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                  du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None):
+    """Backward into caller-allocated gradients.  du, ddelta (and dz) are
+    overwritten; dA, dB, dC, dD, ddelta_bias are fp32 and accumulated into,
+    so pass zeros for plain gradients."""
     lib = nat.load()
     _require(x is not None, "x (the forward's checkpoints) is required")
-    _require(z is None or y is not None, "y from the forward is required with z")
+    _require(z is None or (y is not None and dz is not None), "y from the forward and dz are required with z")
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     _require(x.dtype == torch.float32 and tuple(x.shape) == (batch, dim, n_chunks(seqlen), dstate)
              and x.is_contiguous() and x.device == u.device, "x does not come from forward")
     _check_seq_tensor("dout", dout, u.shape, delta.dtype, u.device)
+    _check_seq_tensor("du", du, u.shape, u.dtype, u.device)
+    _check_seq_tensor("ddelta", ddelta, u.shape, delta.dtype, u.device)
     if y is not None:
         _check_seq_tensor("y", y, u.shape, delta.dtype, u.device)
-    du = torch.empty_like(u, memory_format=torch.contiguous_format)
-    ddelta = torch.empty_like(delta, memory_format=torch.contiguous_format)
-    dA = torch.zeros_like(A, dtype=torch.float32, memory_format=torch.contiguous_format)
-    dB = torch.zeros(B.shape, dtype=torch.float32, device=B.device)
-    dC = torch.zeros(C.shape, dtype=torch.float32, device=C.device)
-    dD = torch.zeros_like(D, memory_format=torch.contiguous_format) if D is not None else None
-    ddelta_bias = (torch.zeros_like(delta_bias, memory_format=torch.contiguous_format)
-                   if delta_bias is not None else None)
-    dz = torch.empty_like(z, memory_format=torch.contiguous_format) if z is not None else None
+    if dz is not None:
+        _check_seq_tensor("dz", dz, u.shape, delta.dtype, u.device)
+    for name, g, ref in (("dA", dA, A), ("dB", dB, B), ("dC", dC, C), ("dD", dD, D),
+                         ("ddelta_bias", ddelta_bias, delta_bias)):
+        if ref is None:
+            continue
+        _require(g is not None and g.dtype == torch.float32 and g.is_contiguous()
+                 and tuple(g.shape) == tuple(ref.shape) and g.device == u.device,
+                 f"{name} must be a contiguous fp32 tensor of shape {tuple(ref.shape)}")
     b = nat.BwdArgs()
     b.f = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, None, x, y)
     b.dout_batch_stride, b.dout_dim_stride = dout.stride(0), dout.stride(1)
@@ -174,6 +189,25 @@ def backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus, *, z
     b.dA, b.dB, b.dC, b.dD, b.ddelta_bias = _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(ddelta_bias)
     with torch.cuda.device(u.device):
         nat.check(lib.ss_bwd(ctypes.byref(b), _stream(u.device)), "selective_scan.backward")
+
+
+def backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus, *, z=None, y=None):
+    """selective_scan.backward (selective_scan.cpp:246-329).
+
+    Returns [du, ddelta, dA, dB, dC, dD, ddelta_bias]; with ``z`` (and the
+    forward's ``y``) also dz as an eighth entry.
+    """
+    du = torch.empty_like(u, memory_format=torch.contiguous_format)
+    ddelta = torch.empty_like(delta, memory_format=torch.contiguous_format)
+    dA = torch.zeros(A.shape, dtype=torch.float32, device=A.device)
+    dB = torch.zeros(B.shape, dtype=torch.float32, device=B.device)
+    dC = torch.zeros(C.shape, dtype=torch.float32, device=C.device)
+    dD = torch.zeros(D.shape, dtype=torch.float32, device=D.device) if D is not None else None
+    ddelta_bias = (torch.zeros(delta_bias.shape, dtype=torch.float32, device=delta_bias.device)
+                   if delta_bias is not None else None)
+    dz = torch.empty_like(z, memory_format=torch.contiguous_format) if z is not None else None
+    backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                  du, ddelta, dA, dB, dC, dD, ddelta_bias, z=z, y=y, dz=dz)
     res = [du, ddelta, dA, dB, dC, dD, ddelta_bias]
     if z is not None:
         res.append(dz)

@@ -142,7 +142,7 @@ def main():
     with torch.no_grad():
         u, dl, A, B, C, D, z, bias = (g[k].detach() for k in names)
         out = torch.empty_like(dl)
-        xck = torch.empty((batch, dim, ss.n_chunks(seqlen), dstate), dtype=torch.float32, device=dev)
+        xck = torch.empty((batch, ss.n_chunks(seqlen), dim, dstate), dtype=torch.float32, device=dev)
         y = torch.empty_like(dl)
         du, dd, dz = torch.empty_like(u), torch.empty_like(dl), torch.empty_like(z)
         dA = torch.zeros(A.shape, dtype=torch.float32, device=dev)

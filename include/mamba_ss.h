@@ -23,7 +23,7 @@
  * with unit stride along seqlen; A is (dim, dstate) fp32; variable B/C are
  * (batch, n_groups, dstate, seqlen) with unit stride along seqlen; constant
  * B/C are (dim, dstate) fp32; D and delta_bias are (dim) fp32 contiguous.
- * x is fp32 (batch, dim, n_chunks, dstate) contiguous: the state h at the
+ * x is fp32 (batch, n_chunks, dim, dstate) contiguous: the state h at the
  * end of every chunk of ss_chunk_size() steps (the last chunk holds the
  * final state).  It plays the role of the reference's x
  * (selective_scan.cpp:207-212) and is consumed only by ss_bwd.

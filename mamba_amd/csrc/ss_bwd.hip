@@ -88,7 +88,9 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     const IT* Cv_base = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
     const float* Bc_base = static_cast<const float*>(p.B) + c * p.B_gs;
     const float* Cc_base = static_cast<const float*>(p.C) + c * p.C_gs;
-    const float* xrow = p.x + (b * p.dim + c) * p.n_chunks * N;
+    // x: (batch, chunk, dim, dstate)
+    const float* xrow = p.x + (b * p.n_chunks * p.dim + c) * N;
+    const int64_t x_chunk_stride = p.dim * N;
     // fp32 gradient rows of variable B / C for this (batch, group): (dstate, seqlen)
     const int64_t G = p.dim / p.dpg;
     float* dBrow = q.dB + (b * G + g) * int64_t(N) * L;
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     auto load_h0 = [&](int64_t ck, int s) {
         const int n = 16 * s + r;
         const int nn = n < N ? n : N - 1;
-        const float v = xrow[(ck > 0 ? ck - 1 : 0) * N + nn];
+        const float v = xrow[(ck > 0 ? ck - 1 : 0) * x_chunk_stride + nn];
         return ck > 0 ? v : 0.f;
     };
 
@@ -354,6 +356,305 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     }
 }
 
+// ------------------------------------------------------------ fast path --
+// dstate 16, variable B and C, seqlen a multiple of 32, dim and channels per
+// group multiples of 16, z gate fixed at compile time: no branch around a
+// memory access in the loop (see the forward fast path).  Global traffic is
+// workgroup-cooperative per 32-step super-tile (two checkpoint chunks):
+// every thread moves one 2-element piece of each of u, delta, dout, z, y, B
+// and C, prefetched one super-tile ahead and staged in LDS; du, ddelta and
+// dz go back the same way.  Sums over states use 8-step transposition
+// halves; dB / dC are first summed over the wave's 4 channel rows with
+// v_permlane32_swap / v_permlane16_swap, then over the 4 waves in LDS, and
+// added to global memory once per workgroup, state and step.
+constexpr int kSB = 32;                 // steps per backward super-tile
+constexpr int kQB = kSB / kT;           // chunks per super-tile
+constexpr int kStrB = kSB + 16;         // LDS row stride of stream tiles (floats)
+constexpr int kBCB = kSB + 4;           // LDS row stride of B / C tiles (floats)
+constexpr int kHRow = 8 * kT + 16;      // half-chunk transposition row stride (144 floats)
+constexpr int kHArr = 3 * kHRow + 8 * kT;   // 560 floats per array per wave
+constexpr int kWgN = 17;                // padded step stride of the dB / dC wave partials
+
+template <typename IT>
+struct Piece2 {                         // 2 consecutive elements of one row
+    using raw = typename std::conditional<sizeof(IT) == 4, uint2, uint32_t>::type;
+    raw v;
+    __device__ __forceinline__ void load(const IT* p) { v = *reinterpret_cast<const raw*>(p); }
+    __device__ __forceinline__ float2 f() const {
+        if constexpr (sizeof(IT) == 4) {
+            return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
+        } else if constexpr (__is_same(IT, bf16_t)) {
+            return make_float2(__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u));
+        } else {
+            return make_float2(float(__builtin_bit_cast(_Float16, uint16_t(v & 0xffffu))),
+                               float(__builtin_bit_cast(_Float16, uint16_t(v >> 16))));
+        }
+    }
+};
+
+template <typename IT>
+__device__ __forceinline__ void store2(IT* p, float2 v) {
+    if constexpr (sizeof(IT) == 4) {
+        *reinterpret_cast<float2*>(p) = v;
+    } else if constexpr (__is_same(IT, bf16_t)) {
+        *reinterpret_cast<uint32_t*>(p) = uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16);
+    } else {
+        *reinterpret_cast<uint32_t*>(p) = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) |
+                                          (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16);
+    }
+}
+
+// Sum of v0..v3 (steps 4kg + 0..3 of one state) over the wave's 4 rows; row
+// j of the result holds the sum for step 4kg + j.
+__device__ __forceinline__ float rows4_sum(float v0, float v1, float v2, float v3) {
+    auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v0), __float_as_uint(v2), false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v1), __float_as_uint(v3), false, false);
+    // rows 0, 1: steps 0 / 1 over rows {j, j + 2}; rows 2, 3: steps 2 / 3
+    const float a = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);
+    const float c = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);
+    auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(c), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+
+template <typename IT, bool kZ>
+__global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
+    // streams u, delta, dout, z, y; the first three hold du, ddelta, dz afterwards
+    __shared__ __attribute__((aligned(16))) float s_in[5 * kChPerWG * kStrB];
+    __shared__ __attribute__((aligned(16))) float s_B[16 * kBCB];
+    __shared__ __attribute__((aligned(16))) float s_C[16 * kBCB];
+    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * 2 * kHArr];       // [wave][s1, s2]
+    __shared__ __attribute__((aligned(16))) float s_wg[2 * kWaves * 16 * kWgN];   // [dB, dC][wave][n][t]
+    const FwdParams& p = q.f;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane & 15;
+    const int j = lane >> 4;
+    const int row = w * kRows + j;
+    const int64_t nblk = p.dim / kChPerWG;
+    const int64_t b = blockIdx.x / nblk;
+    const int64_t c0 = (blockIdx.x % nblk) * kChPerWG;
+    const int64_t c = c0 + row;
+    const int64_t g = c0 / p.dpg;
+    const int64_t L = p.seqlen;
+    const int64_t G = p.dim / p.dpg;
+
+    // cooperative piece of this thread: row prow, steps 2 pc, 2 pc + 1
+    const int prow = tid >> 4, pc = tid & 15;
+    const IT* gsrc[5] = {
+        static_cast<const IT*>(p.u) + b * p.u_bs + (c0 + prow) * p.u_ds + 2 * pc,
+        static_cast<const IT*>(p.delta) + b * p.dl_bs + (c0 + prow) * p.dl_ds + 2 * pc,
+        static_cast<const IT*>(q.dout) + b * q.do_bs + (c0 + prow) * q.do_ds + 2 * pc,
+        kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + (c0 + prow) * p.z_ds + 2 * pc : nullptr,
+        kZ ? static_cast<const IT*>(p.y) + b * p.y_bs + (c0 + prow) * p.y_ds + 2 * pc : nullptr,
+    };
+    const IT* gB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs + prow * p.B_ns + 2 * pc;
+    const IT* gC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs + prow * p.C_ns + 2 * pc;
+    IT* gdu = static_cast<IT*>(q.du) + b * q.du_bs + (c0 + prow) * q.du_ds + 2 * pc;
+    IT* gdd = static_cast<IT*>(q.ddelta) + b * q.dd_bs + (c0 + prow) * q.dd_ds + 2 * pc;
+    IT* gdz = kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + (c0 + prow) * q.dz_ds + 2 * pc : gdu;
+    const int spos = prow * kStrB + 2 * pc;
+    const int bpos = prow * kBCB + 2 * pc;
+    constexpr int kNin = kZ ? 5 : 3;
+    // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
+    const float* gx = p.x + (b * p.n_chunks * p.dim + c) * kT + r;
+    const int64_t x_chunk_stride = p.dim * kT;
+    float* dBrow = q.dB + (b * G + g) * int64_t(kT) * L;
+    float* dCrow = q.dC + (b * G + g) * int64_t(kT) * L;
+
+    const float Dv = p.D ? p.D[c] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
+    const float av = p.A[c * p.A_ds + r * p.A_ns];
+    const float a2 = av * kLog2e;
+    const bool softplus = p.softplus != 0;
+
+    float* tr1 = s_tr + (w * 2 + 0) * kHArr + j * kHRow;
+    float* tr2 = s_tr + (w * 2 + 1) * kHArr + j * kHRow;
+    // half-chunk transposition: lane r writes steps 4c..4c+3 of the half at
+    // r * 8 + 4 * (c ^ ((r >> 2) & 1)); element (lane r', step s) is read at
+    // r' * 8 + 4 * ((s >> 2) ^ ((r' >> 2) & 1)) + (s & 3)
+    const int hs_ = r & 7;                           // this lane's step inside its half
+    const int hoff0 = 4 * ((hs_ >> 2) ^ 0) + (hs_ & 3);
+    const int hoff1 = 4 * ((hs_ >> 2) ^ 1) + (hs_ & 3);
+
+    struct Pieces {
+        Piece2<IT> in[5], B, C;
+        float x[kQB];
+    };
+    auto fetch = [&](int64_t st, Pieces& P) {     // st clamped by the caller
+        const int64_t t0 = st * kSB;
+#pragma unroll
+        for (int a = 0; a < kNin; ++a) P.in[a].load(gsrc[a] + t0);
+        P.B.load(gB + t0);
+        P.C.load(gC + t0);
+#pragma unroll
+        for (int qq = 0; qq < kQB; ++qq) {
+            const int64_t ck = st * kQB + qq;
+            const float v = gx[(ck > 0 ? ck - 1 : 0) * x_chunk_stride];
+            P.x[qq] = ck > 0 ? v : 0.f;
+        }
+    };
+    auto stage = [&](const Pieces& P) {
+#pragma unroll
+        for (int a = 0; a < kNin; ++a)
+            *reinterpret_cast<float2*>(s_in + a * kChPerWG * kStrB + spos) = P.in[a].f();
+        *reinterpret_cast<float2*>(s_B + bpos) = P.B.f();
+        *reinterpret_cast<float2*>(s_C + bpos) = P.C.f();
+    };
+
+    float gcar = 0.f, acar = 1.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
+    const int64_t nst = L / kSB;
+    Pieces P;
+    fetch(nst - 1, P);
+    for (int64_t st = nst - 1; st >= 0; --st) {
+        const int64_t t0 = st * kSB;
+        lds_barrier();                 // previous super-tile's outputs have been stored
+        stage(P);
+        float h0s[kQB];
+#pragma unroll
+        for (int qq = 0; qq < kQB; ++qq) h0s[qq] = P.x[qq];
+        lds_barrier();
+        fetch(st > 0 ? st - 1 : 0, P);              // prefetch the previous super-tile
+
+        float in_v[5][kQB];
+#pragma unroll
+        for (int a = 0; a < 5; ++a)
+#pragma unroll
+            for (int qq = 0; qq < kQB; ++qq)
+                in_v[a][qq] = a < kNin ? s_in[a * kChPerWG * kStrB + row * kStrB + kT * qq + r] : 0.f;
+        lds_barrier();                 // s_in is reused for the outputs below
+
+#pragma unroll
+        for (int qi = kQB - 1; qi >= 0; --qi) {
+            const int64_t tc = t0 + kT * qi;       // first step of this chunk
+            const float uu = in_v[0][qi], pre = in_v[1][qi] + bias, dout = in_v[2][qi];
+            const float zz = in_v[3][qi], yv = in_v[4][qi];
+            const float dt = softplus ? softplus20(pre) : pre;
+            const float dtu = dt * uu;
+            const float sgz = kZ ? sigmoidf_(zz) : 1.f;
+            const float dy = kZ ? dout * zz * sgz : dout;
+            float Bt[kT], Ct[kT];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 vb = *reinterpret_cast<const float4*>(s_B + r * kBCB + kT * qi + 4 * i);
+                const float4 vc = *reinterpret_cast<const float4*>(s_C + r * kBCB + kT * qi + 4 * i);
+                Bt[4 * i] = vb.x; Bt[4 * i + 1] = vb.y; Bt[4 * i + 2] = vb.z; Bt[4 * i + 3] = vb.w;
+                Ct[4 * i] = vc.x; Ct[4 * i + 1] = vc.y; Ct[4 * i + 2] = vc.z; Ct[4 * i + 3] = vc.w;
+            }
+            const float h0 = h0s[qi];
+
+            // ---- recompute a_t and h_t of the chunk from the checkpoint
+            float as[kT], hs[kT];
+            static_for<kT>([&](auto K) {
+                constexpr int k = decltype(K)::value;
+                as[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
+            });
+            float hcur = h0;
+            static_for<kT>([&](auto K) {
+                constexpr int k = decltype(K)::value;
+                hcur = __builtin_fmaf(as[k], hcur, row_bcast<k>(dtu) * Bt[k]);
+                hs[k] = hcur;
+            });
+
+            // ---- adjoint, last step first, in two halves of 8 steps
+            float gv = gcar, anext = acar;
+            float s1r = 0.f, s2r = 0.f;
+            static_for<2>([&](auto HH) {
+                constexpr int hh = 1 - decltype(HH)::value;        // half 1 (steps 8..15) first
+                static_for<2>([&](auto CC) {
+                    constexpr int cc = 1 - decltype(CC)::value;
+                    constexpr int kg = 2 * hh + cc;
+                    float s1p[4], s2p[4], dBp[4], dCp[4];
+                    static_for<4>([&](auto KI) {
+                        constexpr int ki = 3 - decltype(KI)::value;
+                        constexpr int k = 4 * kg + ki;
+                        const float dyk = row_bcast<k>(dy);
+                        gv = __builtin_fmaf(anext, gv, dyk * Ct[k]);
+                        float hprev;
+                        if constexpr (k == 0) hprev = h0;
+                        else hprev = hs[k - 1];
+                        const float gah = gv * (as[k] * hprev);
+                        dA_acc = __builtin_fmaf(row_bcast<k>(dt), gah, dA_acc);
+                        s2p[ki] = av * gah;
+                        s1p[ki] = gv * Bt[k];
+                        dBp[ki] = gv * row_bcast<k>(dtu);
+                        dCp[ki] = dyk * hs[k];
+                        anext = as[k];
+                    });
+                    const int o = r * 8 + 4 * (cc ^ ((r >> 2) & 1));
+                    *reinterpret_cast<float4*>(tr1 + o) = make_float4(s1p[0], s1p[1], s1p[2], s1p[3]);
+                    *reinterpret_cast<float4*>(tr2 + o) = make_float4(s2p[0], s2p[1], s2p[2], s2p[3]);
+                    // dB / dC of steps 4kg..4kg+3 summed over the wave's rows:
+                    // row j holds step 4kg + j
+                    const float dBs = rows4_sum(dBp[0], dBp[1], dBp[2], dBp[3]);
+                    const float dCs = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
+                    s_wg[((0 * kWaves + w) * 16 + r) * kWgN + 4 * kg + j] = dBs;
+                    s_wg[((1 * kWaves + w) * 16 + r) * kWgN + 4 * kg + j] = dCs;
+                });
+                // transposed sums of this half: lanes 8 hh .. 8 hh + 7 own its steps
+                float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+                for (int rr = 0; rr < kT; rr += 2) {
+                    const int o0 = rr * 8 + (((rr >> 2) & 1) ? hoff1 : hoff0);
+                    const int o1 = (rr + 1) * 8 + ((((rr + 1) >> 2) & 1) ? hoff1 : hoff0);
+                    a0 += tr1[o0]; a1 += tr1[o1];
+                    b0 += tr2[o0]; b1 += tr2[o1];
+                }
+                if ((r >> 3) == hh) { s1r = a0 + a1; s2r = b0 + b1; }
+            });
+            gcar = gv;
+            acar = anext;
+
+            // ---- dB / dC: sum the 4 wave partials, one global add per (state, step)
+            lds_barrier();
+            {
+                const int nl = tid >> 4, k = tid & 15;
+                float sB = 0.f, sC = 0.f;
+#pragma unroll
+                for (int ww = 0; ww < kWaves; ++ww) {
+                    sB += s_wg[((0 * kWaves + ww) * 16 + nl) * kWgN + k];
+                    sC += s_wg[((1 * kWaves + ww) * 16 + nl) * kWgN + k];
+                }
+                atomicAdd(dBrow + nl * L + tc + k, sB);
+                atomicAdd(dCrow + nl * L + tc + k, sC);
+            }
+            lds_barrier();
+
+            // ---- per-step outputs of step tc + r into the output tiles
+            const float du = Dv * dy + dt * s1r;
+            const float ddt = uu * s1r + s2r;
+            const float dd = softplus ? ddt * sigmoidf_(pre) : ddt;
+            const int opos = row * kStrB + kT * qi + r;
+            s_in[0 * kChPerWG * kStrB + opos] = du;
+            s_in[1 * kChPerWG * kStrB + opos] = dd;
+            if constexpr (kZ) s_in[2 * kChPerWG * kStrB + opos] = dout * yv * sgz * (1.f + zz * (1.f - sgz));
+            dD_acc += dy * uu;
+            db_acc += dd;
+        }
+        lds_barrier();
+        store2<IT>(gdu + t0, *reinterpret_cast<const float2*>(s_in + 0 * kChPerWG * kStrB + spos));
+        store2<IT>(gdd + t0, *reinterpret_cast<const float2*>(s_in + 1 * kChPerWG * kStrB + spos));
+        if constexpr (kZ) store2<IT>(gdz + t0, *reinterpret_cast<const float2*>(s_in + 2 * kChPerWG * kStrB + spos));
+    }
+
+    // ---- per-channel and per-(channel, state) sums over time and batch
+    dD_acc = row_allsum(dD_acc);
+    db_acc = row_allsum(db_acc);
+    if (r == 0) {
+        if (q.dD) atomicAdd(q.dD + c, dD_acc);
+        if (q.ddelta_bias) atomicAdd(q.ddelta_bias + c, db_acc);
+    }
+    atomicAdd(q.dA + c * kT + r, dA_acc);
+}
+
+bool bwd_fast_ok(const BwdParams& q) {
+    const FwdParams& p = q.f;
+    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kSB && p.seqlen % kSB == 0 &&
+           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && q.stream_vec_bwd &&
+           (!p.has_z || p.y != nullptr);
+}
+
 template <typename IT>
 static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     const int64_t nblk = (p.f.dim + kChPerWG - 1) / kChPerWG;
@@ -361,7 +662,10 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     const dim3 block(kThreads);
     const int spl = int((p.f.dstate + 15) / 16);
     const bool vbc = p.f.var_B && p.f.var_C;
-    if (spl <= 1) {
+    if (bwd_fast_ok(p)) {
+        if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((ss_bwd_fast<IT, false>), grid, block, 0, stream, p);
+    } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, false>), grid, block, 0, stream, p);
     } else if (spl <= 2) hipLaunchKernelGGL((ss_bwd_kernel<IT, 2, false>), grid, block, 0, stream, p);

@@ -49,7 +49,9 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
     const IT* Cv_base = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
     const float* Bc_base = static_cast<const float*>(p.B) + c * p.B_gs;  // constant B: (dim, dstate)
     const float* Cc_base = static_cast<const float*>(p.C) + c * p.C_gs;
-    float* xrow = p.x + (b * p.dim + c) * p.n_chunks * N;
+    // x: (batch, chunk, dim, dstate)
+    float* xrow = p.x + (b * p.n_chunks * p.dim + c) * N;
+    const int64_t x_chunk_stride = p.dim * N;
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
             });
             h[s] = hs;
             const bool chunk_end = ((t0 + kT) % kChunk == 0) || (t0 + kT >= L);
-            if (chunk_end && cval && n < N) xrow[(t0 / kChunk) * N + n] = hs;
+            if (chunk_end && cval && n < N) xrow[(t0 / kChunk) * x_chunk_stride + n] = hs;
         }
         row_transpose_write(wbuf + slot * kTrWave, yp, j, r);
         pend_t = t0 + r;
@@ -186,158 +188,186 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
     finish_pending(slot ^ 1);
 }
 
-// Fast path: dstate 16, variable B and C with 16-byte aligned rows, seqlen a
-// multiple of 32, dim a multiple of 16, z gate fixed at compile time.  Every
-// step, state and channel is real, so the loop body has no branch around a
-// memory access.  That matters on gfx950: loads and stores share one
-// in-order counter (vmcnt), and after a branch that contains memory accesses
-// the compiler waits for all of them (vmcnt(0)), which would also wait for
-// the loads prefetched for the next tile.
-template <typename IT, bool kZ>
-__global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
-    // 16-byte chunks per 16-step row of B / C: 4 for fp32, 2 for 16-bit types
-    constexpr int CPR = (kT * int(sizeof(IT))) / 16;
-    __shared__ __attribute__((aligned(16))) float tr_buf[kWaves * kTrWave];
-    // per wave: one staged tile of B and C, 1 KB each
-    __shared__ __attribute__((aligned(16))) float bc_buf[kWaves * 2 * 256];
+// Fast path: dstate 16, variable B and C, seqlen a multiple of 64, dim a
+// multiple of 16, z gate fixed at compile time.  Every step, state and
+// channel is real, so the loop body has no branch around a memory access
+// (loads and stores share one in-order counter, vmcnt; after a branch that
+// contains memory accesses the compiler waits for all of them, which would
+// also wait for the prefetch of the next super-tile).
+//
+// Global traffic is workgroup-cooperative: per 64-step super-tile, each of
+// the 256 threads moves one 16-byte piece of each of u, delta, z, B and C
+// (16 rows x 256 contiguous bytes per array for fp32), prefetched one
+// super-tile ahead in registers and staged in LDS; outputs go back the same
+// way.  Lanes then read their per-step values and B / C rows from LDS.  A
+// wave's checkpoint store is 4 channels x 16 states = 256 contiguous bytes.
+constexpr int kS = 64;                       // steps per super-tile
+constexpr int kSq = kS / kT;                 // 16-step sub-tiles per super-tile
+constexpr int kStrm = kS + 16;               // LDS row stride of stream tiles (floats)
+constexpr int kBCs = kS + 4;                 // LDS row stride of B / C tiles (floats)
 
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int r = lane & 15;
-    const int j = lane >> 4;
-    const int64_t nblk = p.dim / kChPerWG;
-    const int64_t b = blockIdx.x / nblk;
-    const int64_t c = (blockIdx.x % nblk) * kChPerWG + w * kRows + j;
-    const int64_t g = c / p.dpg;
-    const int64_t L = p.seqlen;
-    float* wbuf = tr_buf + w * kTrWave;
-    float* bcw = bc_buf + w * 2 * 256;
-
-    const IT* u = static_cast<const IT*>(p.u) + b * p.u_bs + c * p.u_ds;
-    const IT* dl = static_cast<const IT*>(p.delta) + b * p.dl_bs + c * p.dl_ds;
-    const IT* zp = kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c * p.z_ds : u;
-    IT* out = static_cast<IT*>(p.out) + b * p.o_bs + c * p.o_ds;
-    IT* ysave = kZ ? static_cast<IT*>(p.y) + b * p.y_bs + c * p.y_ds : out;
-    float* xrow = p.x + (b * p.dim + c) * p.n_chunks * kT;
-
-    // B / C tiles are staged through LDS: every lane fetches the 16-byte chunk
-    // of its LDS slot (see tile_slot) with a coalesced load, 4 lanes per
-    // 64-byte state row segment; for 16-bit types lanes 0-31 fetch B and lanes
-    // 32-63 fetch C.  Each lane then reads its own state row from LDS.
-    const IT* Bbase = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs;
-    const IT* Cbase = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
-    const IT* stage_src_B;
-    const IT* stage_src_C;
-    {
-        int n, i;
-        if constexpr (CPR == 4) {
-            tile_slot_inv<4>(lane, n, i);
-            stage_src_B = Bbase + n * p.B_ns + 4 * i;
-            stage_src_C = Cbase + n * p.C_ns + 4 * i;
+template <typename IT>
+struct Piece4 {                              // 4 consecutive elements of one row
+    using raw = typename std::conditional<sizeof(IT) == 4, uint4, uint2>::type;
+    raw v;
+    __device__ __forceinline__ void load(const IT* p) { v = *reinterpret_cast<const raw*>(p); }
+    __device__ __forceinline__ float4 f() const {
+        if constexpr (sizeof(IT) == 4) {
+            return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+        } else if constexpr (__is_same(IT, bf16_t)) {
+            return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
+                               __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
         } else {
-            tile_slot_inv<2>(lane & 31, n, i);
-            stage_src_B = lane < 32 ? Bbase + n * p.B_ns + 8 * i : Cbase + n * p.C_ns + 8 * i;
-            stage_src_C = stage_src_B;
+            return make_float4(float(__builtin_bit_cast(_Float16, uint16_t(v.x & 0xffffu))),
+                               float(__builtin_bit_cast(_Float16, uint16_t(v.x >> 16))),
+                               float(__builtin_bit_cast(_Float16, uint16_t(v.y & 0xffffu))),
+                               float(__builtin_bit_cast(_Float16, uint16_t(v.y >> 16))));
         }
     }
-    // coalesced fetch of this lane's 16-byte chunk of the tile (kept in
-    // registers until the tile is computed), then a float4 write to its LDS slot
-    struct Chunks { uint4 b, c; };
-    auto fetch_bc = [&](int64_t t0, Chunks& F) {
-        F.b = *reinterpret_cast<const uint4*>(stage_src_B + t0);
-        if constexpr (CPR == 4) F.c = *reinterpret_cast<const uint4*>(stage_src_C + t0);
-    };
-    auto stage_bc = [&](const Chunks& F) {
-        uint4* dst = reinterpret_cast<uint4*>(bcw);
-        dst[lane] = F.b;
-        if constexpr (CPR == 4) dst[64 + lane] = F.c;
-    };
-    // this lane's state row r of the staged tile, as float
-    auto read_bc = [&](float (&Bo)[kT], float (&Co)[kT]) {
-        const float* src = bcw;
-        if constexpr (CPR == 4) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 vb = *reinterpret_cast<const float4*>(src + 4 * tile_slot<4>(r, i));
-                const float4 vc = *reinterpret_cast<const float4*>(src + 256 + 4 * tile_slot<4>(r, i));
-                Bo[4 * i] = vb.x; Bo[4 * i + 1] = vb.y; Bo[4 * i + 2] = vb.z; Bo[4 * i + 3] = vb.w;
-                Co[4 * i] = vc.x; Co[4 * i + 1] = vc.y; Co[4 * i + 2] = vc.z; Co[4 * i + 3] = vc.w;
-            }
-        } else {
-            const IT* s16 = reinterpret_cast<const IT*>(src);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                float tb[8], tc[8];
-                load8_16(s16 + 8 * tile_slot<2>(r, i), tb);
-                load8_16(s16 + 256 + 8 * tile_slot<2>(r, i), tc);
-#pragma unroll
-                for (int k = 0; k < 8; ++k) { Bo[8 * i + k] = tb[k]; Co[8 * i + k] = tc[k]; }
-            }
-        }
-    };
+};
+
+template <typename IT>
+__device__ __forceinline__ void store4(IT* p, float4 v) {
+    if constexpr (sizeof(IT) == 4) {
+        *reinterpret_cast<float4*>(p) = v;
+    } else if constexpr (__is_same(IT, bf16_t)) {
+        uint2 o;
+        o.x = uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16);
+        o.y = uint32_t(io<bf16_t>::round(v.z)) | (uint32_t(io<bf16_t>::round(v.w)) << 16);
+        *reinterpret_cast<uint2*>(p) = o;
+    } else {
+        uint2 o;
+        o.x = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16);
+        o.y = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.z))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.w))) << 16);
+        *reinterpret_cast<uint2*>(p) = o;
+    }
+}
+
+template <typename IT, bool kZ>
+__global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
+    __shared__ __attribute__((aligned(16))) float tr_buf[kWaves * kTrWave];
+    // stream tiles [16 channels][64 steps] of u, delta, z; u and delta hold
+    // the outputs (out, y) once every lane has read its inputs
+    __shared__ __attribute__((aligned(16))) float s_u[kChPerWG * kStrm];
+    __shared__ __attribute__((aligned(16))) float s_d[kChPerWG * kStrm];
+    __shared__ __attribute__((aligned(16))) float s_z[kZ ? kChPerWG * kStrm : 4];
+    // B / C tiles [16 states][64 steps]
+    __shared__ __attribute__((aligned(16))) float s_B[16 * kBCs];
+    __shared__ __attribute__((aligned(16))) float s_C[16 * kBCs];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane & 15;
+    const int j = lane >> 4;
+    const int row = w * kRows + j;                 // this lane's channel row in the workgroup
+    const int64_t nblk = p.dim / kChPerWG;
+    const int64_t b = blockIdx.x / nblk;
+    const int64_t c0 = (blockIdx.x % nblk) * kChPerWG;
+    const int64_t c = c0 + row;
+    const int64_t g = c0 / p.dpg;
+    const int64_t L = p.seqlen;
+    float* wbuf = tr_buf + w * kTrWave;
+
+    // cooperative piece of this thread: row prow, steps 4 pc .. 4 pc + 3
+    const int prow = tid >> 4, pc = tid & 15;
+    const IT* gu = static_cast<const IT*>(p.u) + b * p.u_bs + (c0 + prow) * p.u_ds + 4 * pc;
+    const IT* gd = static_cast<const IT*>(p.delta) + b * p.dl_bs + (c0 + prow) * p.dl_ds + 4 * pc;
+    const IT* gz = kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + (c0 + prow) * p.z_ds + 4 * pc : gu;
+    const IT* gB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs + prow * p.B_ns + 4 * pc;
+    const IT* gC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs + prow * p.C_ns + 4 * pc;
+    IT* go = static_cast<IT*>(p.out) + b * p.o_bs + (c0 + prow) * p.o_ds + 4 * pc;
+    IT* gy = kZ ? static_cast<IT*>(p.y) + b * p.y_bs + (c0 + prow) * p.y_ds + 4 * pc : go;
+    const int spos = prow * kStrm + 4 * pc;        // this piece in a stream tile
+    const int bpos = prow * kBCs + 4 * pc;         // this piece in a B / C tile
+    // x: (batch, chunk, dim, dstate); a wave's 4 channels x 16 states are contiguous
+    float* gx = p.x + (b * p.n_chunks * p.dim + c) * kT + r;
+    const int64_t x_chunk_stride = p.dim * kT;
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
     const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
-    const int64_t t_last = L - kT;
 
-    struct Step {
-        float u, dl, z;
-        Chunks bc;
+    struct Pieces { Piece4<IT> u, d, z, B, C; };
+    auto fetch = [&](int64_t t0, Pieces& P) {   // t0 clamped by the caller
+        P.u.load(gu + t0);
+        P.d.load(gd + t0);
+        if constexpr (kZ) P.z.load(gz + t0);
+        P.B.load(gB + t0);
+        P.C.load(gC + t0);
     };
-    // the prefetch past the last tile re-reads the last tile
-    auto load_step = [&](int64_t t0, Step& S) {
-        const int64_t tc = t0 < t_last ? t0 : t_last;
-        S.u = load_at(u, tc + r);
-        S.dl = load_at(dl, tc + r);
-        S.z = kZ ? load_at(zp, tc + r) : 0.f;
-        fetch_bc(tc, S.bc);
+    auto stage = [&](const Pieces& P) {
+        *reinterpret_cast<float4*>(s_u + spos) = P.u.f();
+        *reinterpret_cast<float4*>(s_d + spos) = P.d.f();
+        if constexpr (kZ) *reinterpret_cast<float4*>(s_z + spos) = P.z.f();
+        *reinterpret_cast<float4*>(s_B + bpos) = P.B.f();
+        *reinterpret_cast<float4*>(s_C + bpos) = P.C.f();
     };
+
     float h = 0.f;
-    auto compute_tile = [&](int64_t t0, const Step& S) {
-        float Bt[kT], Ct[kT];
-        stage_bc(S.bc);
-        read_bc(Bt, Ct);
-        const float pre = S.dl + bias;
-        const float dt = softplus ? softplus20(pre) : pre;
-        const float dtu = dt * S.u;
-        // decay factors and inputs of all 16 steps first: they do not depend
-        // on h, so the exp latency stays off the h chain
-        float a[kT], bb[kT], yp[kT];
-        static_for<kT>([&](auto K) {
-            constexpr int k = decltype(K)::value;
-            a[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
-            bb[k] = row_bcast<k>(dtu) * Bt[k];
-        });
-        static_for<kT>([&](auto K) {
-            constexpr int k = decltype(K)::value;
-            h = __builtin_fmaf(a[k], h, bb[k]);
-            yp[k] = Ct[k] * h;
-        });
-        xrow[(t0 / kT) * kT + r] = h;
-        row_transpose_write(wbuf, yp, j, r);
-        float y = row_transpose_read(wbuf, j, r) + Dv * S.u;
-        if constexpr (kZ) {
-            io<IT>::store(ysave + t0 + r, y);
-            y *= S.z * sigmoidf_(S.z);
-        }
-        io<IT>::store(out + t0 + r, y);
-    };
+    Pieces P;
+    fetch(0, P);
+    for (int64_t t0 = 0; t0 < L; t0 += kS) {
+        lds_barrier();                 // previous super-tile's outputs have been stored
+        stage(P);
+        lds_barrier();
+        fetch(t0 + kS < L ? t0 + kS : t0, P);      // prefetch (re-reads the last super-tile at the end)
 
-    Step S0, S1;
-    load_step(0, S0);
-    for (int64_t t0 = 0; t0 < L; t0 += 2 * kT) {
-        load_step(t0 + kT, S1);
-        compute_tile(t0, S0);
-        load_step(t0 + 2 * kT, S0);
-        compute_tile(t0 + kT, S1);
+        // per-step inputs of steps t0 + 16 q + r of this lane's channel
+        float uq[kSq], dq[kSq], zq[kSq];
+#pragma unroll
+        for (int q = 0; q < kSq; ++q) {
+            uq[q] = s_u[row * kStrm + kT * q + r];
+            dq[q] = s_d[row * kStrm + kT * q + r];
+            zq[q] = kZ ? s_z[row * kStrm + kT * q + r] : 0.f;
+        }
+        lds_barrier();                 // s_u / s_d are reused for the outputs below
+
+#pragma unroll
+        for (int q = 0; q < kSq; ++q) {
+            float Bt[kT], Ct[kT];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 vb = *reinterpret_cast<const float4*>(s_B + r * kBCs + kT * q + 4 * i);
+                const float4 vc = *reinterpret_cast<const float4*>(s_C + r * kBCs + kT * q + 4 * i);
+                Bt[4 * i] = vb.x; Bt[4 * i + 1] = vb.y; Bt[4 * i + 2] = vb.z; Bt[4 * i + 3] = vb.w;
+                Ct[4 * i] = vc.x; Ct[4 * i + 1] = vc.y; Ct[4 * i + 2] = vc.z; Ct[4 * i + 3] = vc.w;
+            }
+            const float pre = dq[q] + bias;
+            const float dt = softplus ? softplus20(pre) : pre;
+            const float dtu = dt * uq[q];
+            // decay factors and inputs of all 16 steps first: they do not
+            // depend on h, so the exp latency stays off the h chain
+            float a[kT], bb[kT], yp[kT];
+            static_for<kT>([&](auto K) {
+                constexpr int k = decltype(K)::value;
+                a[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
+                bb[k] = row_bcast<k>(dtu) * Bt[k];
+            });
+            static_for<kT>([&](auto K) {
+                constexpr int k = decltype(K)::value;
+                h = __builtin_fmaf(a[k], h, bb[k]);
+                yp[k] = Ct[k] * h;
+            });
+            gx[((t0 + kT * q) / kT) * x_chunk_stride] = h;
+            row_transpose_write(wbuf, yp, j, r);
+            float y = row_transpose_read(wbuf, j, r) + Dv * uq[q];
+            if constexpr (kZ) {
+                s_d[row * kStrm + kT * q + r] = y;
+                y *= zq[q] * sigmoidf_(zq[q]);
+            }
+            s_u[row * kStrm + kT * q + r] = y;
+        }
+        lds_barrier();
+        store4<IT>(go + t0, *reinterpret_cast<const float4*>(s_u + spos));
+        if constexpr (kZ) store4<IT>(gy + t0, *reinterpret_cast<const float4*>(s_d + spos));
     }
 }
 
 bool fwd_fast_ok(const FwdParams& p) {
-    return p.dstate == 16 && p.var_B && p.var_C && p.vec_B && p.vec_C && p.seqlen >= 32 &&
-           p.seqlen % 32 == 0 && p.dim % kChPerWG == 0 && (!p.has_z || p.y != nullptr);
+    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kS && p.seqlen % kS == 0 &&
+           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && (!p.has_z || p.y != nullptr);
 }
 
 template <typename IT>

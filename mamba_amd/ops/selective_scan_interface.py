@@ -100,7 +100,8 @@ class SelectiveScanZFn(torch.autograd.Function):
         ctx.save_for_backward(u, delta, A, B, C, D, delta_bias, z, x, y)
         ctx.mark_non_differentiable(x)
         if return_last_state:
-            last_state = x[:, :, -1, :] if x.shape[2] > 0 else x.new_zeros(x.shape[0], x.shape[1], x.shape[3])
+            # x is (batch, n_chunks, dim, dstate); its last chunk holds h at the last step
+            last_state = x[:, -1] if x.shape[1] > 0 else x.new_zeros(x.shape[0], x.shape[2], x.shape[3])
             ctx.mark_non_differentiable(last_state)
             return out, last_state
         return out

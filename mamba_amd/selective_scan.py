@@ -122,14 +122,14 @@ def _stream(device):
 
 def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
     """Forward into caller-allocated ``out`` (delta's dtype), ``x`` (fp32
-    (batch, dim, n_chunks, dstate) contiguous) and, with ``z``, ``y``."""
+    (batch, n_chunks, dim, dstate) contiguous) and, with ``z``, ``y``."""
     lib = nat.load()
     _require(out is not None and x is not None, "out and x are required")
     _check_seq_tensor("out", out, u.shape, delta.dtype, u.device)
     batch, dim, seqlen = u.shape
     _require(x.dtype == torch.float32 and x.is_contiguous() and x.device == u.device
-             and tuple(x.shape) == (batch, dim, n_chunks(seqlen), A.shape[1]),
-             "x must be a contiguous fp32 (batch, dim, n_chunks, dstate) tensor")
+             and tuple(x.shape) == (batch, n_chunks(seqlen), dim, A.shape[1]),
+             "x must be a contiguous fp32 (batch, n_chunks, dim, dstate) tensor")
     if y is not None:
         _check_seq_tensor("y", y, u.shape, delta.dtype, u.device)
     a = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
@@ -146,7 +146,7 @@ def forward(u, delta, A, B, C, D=None, delta_bias=None, use_delta_softplus=True,
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     out = torch.empty_like(delta, memory_format=torch.contiguous_format)
-    x = torch.empty((batch, dim, n_chunks(seqlen), dstate), dtype=torch.float32, device=u.device)
+    x = torch.empty((batch, n_chunks(seqlen), dim, dstate), dtype=torch.float32, device=u.device)
     y = torch.empty_like(out) if z is not None else None
     forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z=z, y=y)
     return [out, x] if z is None else [out, x, y]
@@ -162,7 +162,7 @@ def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
     _require(z is None or (y is not None and dz is not None), "y from the forward and dz are required with z")
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
-    _require(x.dtype == torch.float32 and tuple(x.shape) == (batch, dim, n_chunks(seqlen), dstate)
+    _require(x.dtype == torch.float32 and tuple(x.shape) == (batch, n_chunks(seqlen), dim, dstate)
              and x.is_contiguous() and x.device == u.device, "x does not come from forward")
     _check_seq_tensor("dout", dout, u.shape, delta.dtype, u.device)
     _check_seq_tensor("du", du, u.shape, u.dtype, u.device)

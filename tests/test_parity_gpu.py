@@ -36,6 +36,10 @@ CASES = [
     (1, 16, 64, 40, torch.float32, 1, True, True, True, True, True, True),      # dstate 64
     (2, 64, 16, 256, torch.bfloat16, 1, True, True, True, True, True, True),    # bf16 I/O
     (1, 32, 16, 70, torch.float16, 1, True, True, True, True, True, True),      # fp16 I/O
+    # fast path: dstate 16, variable B/C, seqlen % 64 == 0, 16-channel groups
+    (1, 32, 16, 128, torch.float16, 2, True, True, True, True, True, True),     # fp16, 2 groups
+    (2, 48, 16, 192, torch.float32, 1, True, True, False, True, True, True),    # no z, 3 workgroups
+    (1, 16, 16, 64, torch.bfloat16, 1, True, True, True, False, False, True),   # one super-tile, no D / bias
 ]
 
 
@@ -110,3 +114,30 @@ def test_strided_z_and_last_state():
                                     delta_softplus=True, return_last_state=True, compute_dtype=torch.float64)
     assert_close(out.cpu(), ref, 1e-3, 1e-3, "out")
     assert_close(last.cpu(), rlast, 1e-3, 1e-3, "last_state")
+
+
+def test_fast_path_strided_z_and_last_state():
+    """Fast-path shapes with z a channel slice of a packed xz tensor."""
+    from mamba_amd.ops.selective_scan_interface import selective_scan_fn
+    print("\n[parity] fast path strided z + last state b2-d32-n16-l128", flush=True)
+    x = make_inputs(2, 32, 16, 128, seed=12)
+    dev = torch.device("cuda:0")
+    xz = torch.cat([x["u"], x["z"]], dim=1).to(dev)      # (2, 64, 128)
+    u, z = xz[:, :32], xz[:, 32:]
+    g = {k: x[k].to(dev).requires_grad_(True) for k in ("delta", "A", "B", "C", "D", "delta_bias")}
+    uu = u.detach().requires_grad_(True)
+    zz = z.detach().requires_grad_(True)
+    out, last = selective_scan_fn(uu, g["delta"], g["A"], g["B"], g["C"], g["D"], z=zz,
+                                  delta_bias=g["delta_bias"], delta_softplus=True, return_last_state=True)
+    out.backward(x["dout"].to(dev))
+    ref, rgrads = oracle_fwd_bwd(x, delta_softplus=True)
+    from oracle.selective_scan_ref import selective_scan_ref
+    _, rlast = selective_scan_ref(*(x[k].double() for k in ("u", "delta", "A", "B", "C", "D")),
+                                  z=x["z"].double(), delta_bias=x["delta_bias"].double(),
+                                  delta_softplus=True, return_last_state=True, compute_dtype=torch.float64)
+    assert_close(out.detach().cpu(), ref, 1e-3, 1e-3, "out")
+    assert_close(last.cpu(), rlast, 1e-3, 1e-3, "last_state")
+    assert_close(uu.grad.cpu(), rgrads["u"], 1e-3, 1e-3, "du")
+    assert_close(zz.grad.cpu(), rgrads["z"], 1e-3, 1e-3, "dz")
+    for k in ("delta", "A", "B", "C", "D", "delta_bias"):
+        assert_close(g[k].grad.cpu(), rgrads[k], 1e-3, 1e-3, f"d{k}")

@@ -363,17 +363,18 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
 // workgroup-cooperative per 32-step super-tile (two checkpoint chunks):
 // every thread moves one 2-element piece of each of u, delta, dout, z, y, B
 // and C, prefetched one super-tile ahead and staged in LDS; du, ddelta and
-// dz go back the same way.  Sums over states use 8-step transposition
-// halves; dB / dC are first summed over the wave's 4 channel rows with
-// v_permlane32_swap / v_permlane16_swap, then over the 4 waves in LDS, and
-// added to global memory once per workgroup, state and step.
+// dz go back the same way.  The sums over states (sum_n g B, sum_n A g a h)
+// share one float2 transposition per chunk.  dB / dC are first summed over
+// the wave's 4 channel rows with v_permlane32_swap / v_permlane16_swap, then
+// over the 4 waves in LDS once per super-tile (inside barriers the
+// super-tile needs anyway), and added to global memory once per workgroup,
+// state and step.
 constexpr int kSB = 32;                 // steps per backward super-tile
 constexpr int kQB = kSB / kT;           // chunks per super-tile
 constexpr int kStrB = kSB + 16;         // LDS row stride of stream tiles (floats)
 constexpr int kBCB = kSB + 4;           // LDS row stride of B / C tiles (floats)
-constexpr int kHRow = 8 * kT + 16;      // half-chunk transposition row stride (144 floats)
-constexpr int kHArr = 3 * kHRow + 8 * kT;   // 560 floats per array per wave
-constexpr int kWgN = 17;                // padded step stride of the dB / dC wave partials
+constexpr int kTr2Row = kT * 2 * kT;    // float2 transposition: 16 lanes x 16 steps x 2 (512 floats)
+constexpr int kWgN = kSB + 1;           // padded step stride of the dB / dC wave partials
 
 template <typename IT>
 struct Piece2 {                         // 2 consecutive elements of one row
@@ -422,8 +423,8 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     __shared__ __attribute__((aligned(16))) float s_in[5 * kChPerWG * kStrB];
     __shared__ __attribute__((aligned(16))) float s_B[16 * kBCB];
     __shared__ __attribute__((aligned(16))) float s_C[16 * kBCB];
-    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * 2 * kHArr];       // [wave][s1, s2]
-    __shared__ __attribute__((aligned(16))) float s_wg[2 * kWaves * 16 * kWgN];   // [dB, dC][wave][n][t]
+    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * kRows * kTr2Row];   // [wave][row][lane][step][2]
+    __shared__ __attribute__((aligned(16))) float s_wg[2 * kWaves * 16 * kWgN];     // [dB, dC][wave][n][t]
     const FwdParams& p = q.f;
 
     const int tid = threadIdx.x;
@@ -440,28 +441,32 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     const int64_t L = p.seqlen;
     const int64_t G = p.dim / p.dpg;
 
-    // cooperative piece of this thread: row prow, steps 2 pc, 2 pc + 1
+    // cooperative piece of this thread: row prow, steps 2 pc, 2 pc + 1.
+    // Workgroup-uniform bases plus 32-bit per-thread offsets.
     const int prow = tid >> 4, pc = tid & 15;
-    const IT* gsrc[5] = {
-        static_cast<const IT*>(p.u) + b * p.u_bs + (c0 + prow) * p.u_ds + 2 * pc,
-        static_cast<const IT*>(p.delta) + b * p.dl_bs + (c0 + prow) * p.dl_ds + 2 * pc,
-        static_cast<const IT*>(q.dout) + b * q.do_bs + (c0 + prow) * q.do_ds + 2 * pc,
-        kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + (c0 + prow) * p.z_ds + 2 * pc : nullptr,
-        kZ ? static_cast<const IT*>(p.y) + b * p.y_bs + (c0 + prow) * p.y_ds + 2 * pc : nullptr,
-    };
-    const IT* gB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs + prow * p.B_ns + 2 * pc;
-    const IT* gC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs + prow * p.C_ns + 2 * pc;
-    IT* gdu = static_cast<IT*>(q.du) + b * q.du_bs + (c0 + prow) * q.du_ds + 2 * pc;
-    IT* gdd = static_cast<IT*>(q.ddelta) + b * q.dd_bs + (c0 + prow) * q.dd_ds + 2 * pc;
-    IT* gdz = kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + (c0 + prow) * q.dz_ds + 2 * pc : gdu;
+    const IT* bu = static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds;
+    const IT* bd = static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds;
+    const IT* bo = static_cast<const IT*>(q.dout) + b * q.do_bs + c0 * q.do_ds;
+    const IT* bz = kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : bu;
+    const IT* by = kZ ? static_cast<const IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : bu;
+    const IT* bB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs;
+    const IT* bC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
+    IT* bdu = static_cast<IT*>(q.du) + b * q.du_bs + c0 * q.du_ds;
+    IT* bdd = static_cast<IT*>(q.ddelta) + b * q.dd_bs + c0 * q.dd_ds;
+    IT* bdz = kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + c0 * q.dz_ds : bdu;
+    const uint32_t ou = uint32_t(prow * p.u_ds + 2 * pc), od = uint32_t(prow * p.dl_ds + 2 * pc);
+    const uint32_t oo = uint32_t(prow * q.do_ds + 2 * pc);
+    const uint32_t oz = kZ ? uint32_t(prow * p.z_ds + 2 * pc) : ou, oy = kZ ? uint32_t(prow * p.y_ds + 2 * pc) : ou;
+    const uint32_t oB = uint32_t(prow * p.B_ns + 2 * pc), oC = uint32_t(prow * p.C_ns + 2 * pc);
+    const uint32_t odu = uint32_t(prow * q.du_ds + 2 * pc), odd = uint32_t(prow * q.dd_ds + 2 * pc);
+    const uint32_t odz = kZ ? uint32_t(prow * q.dz_ds + 2 * pc) : odu;
     const int spos = prow * kStrB + 2 * pc;
     const int bpos = prow * kBCB + 2 * pc;
-    constexpr int kNin = kZ ? 5 : 3;
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
     const float* gx = p.x + (b * p.n_chunks * p.dim + c) * kT + r;
     const int64_t x_chunk_stride = p.dim * kT;
-    float* dBrow = q.dB + (b * G + g) * int64_t(kT) * L;
-    float* dCrow = q.dC + (b * G + g) * int64_t(kT) * L;
+    float* dBb = q.dB + (b * G + g) * int64_t(kT) * L;
+    float* dCb = q.dC + (b * G + g) * int64_t(kT) * L;
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -469,25 +474,23 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     const float a2 = av * kLog2e;
     const bool softplus = p.softplus != 0;
 
-    float* tr1 = s_tr + (w * 2 + 0) * kHArr + j * kHRow;
-    float* tr2 = s_tr + (w * 2 + 1) * kHArr + j * kHRow;
-    // half-chunk transposition: lane r writes steps 4c..4c+3 of the half at
-    // r * 8 + 4 * (c ^ ((r >> 2) & 1)); element (lane r', step s) is read at
-    // r' * 8 + 4 * ((s >> 2) ^ ((r' >> 2) & 1)) + (s & 3)
-    const int hs_ = r & 7;                           // this lane's step inside its half
-    const int hoff0 = 4 * ((hs_ >> 2) ^ 0) + (hs_ & 3);
-    const int hoff1 = 4 * ((hs_ >> 2) ^ 1) + (hs_ & 3);
+    // float2 (s1, s2) transposition of one chunk: lane r writes steps 2m, 2m+1
+    // as a float4 at r * 32 + 4 * (m ^ (r & 7)); element (lane r', step s)
+    // is the float2 at r' * 32 + 4 * ((s >> 1) ^ (r' & 7)) + 2 * (s & 1)
+    float* trw = s_tr + (w * kRows + j) * kTr2Row;
 
     struct Pieces {
-        Piece2<IT> in[5], B, C;
+        Piece2<IT> u, d, o, z, y, B, C;
         float x[kQB];
     };
     auto fetch = [&](int64_t st, Pieces& P) {     // st clamped by the caller
         const int64_t t0 = st * kSB;
-#pragma unroll
-        for (int a = 0; a < kNin; ++a) P.in[a].load(gsrc[a] + t0);
-        P.B.load(gB + t0);
-        P.C.load(gC + t0);
+        P.u.load(bu + t0 + ou);
+        P.d.load(bd + t0 + od);
+        P.o.load(bo + t0 + oo);
+        if constexpr (kZ) { P.z.load(bz + t0 + oz); P.y.load(by + t0 + oy); }
+        P.B.load(bB + t0 + oB);
+        P.C.load(bC + t0 + oC);
 #pragma unroll
         for (int qq = 0; qq < kQB; ++qq) {
             const int64_t ck = st * kQB + qq;
@@ -496,11 +499,32 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
         }
     };
     auto stage = [&](const Pieces& P) {
-#pragma unroll
-        for (int a = 0; a < kNin; ++a)
-            *reinterpret_cast<float2*>(s_in + a * kChPerWG * kStrB + spos) = P.in[a].f();
+        constexpr int T = kChPerWG * kStrB;
+        *reinterpret_cast<float2*>(s_in + 0 * T + spos) = P.u.f();
+        *reinterpret_cast<float2*>(s_in + 1 * T + spos) = P.d.f();
+        *reinterpret_cast<float2*>(s_in + 2 * T + spos) = P.o.f();
+        if constexpr (kZ) {
+            *reinterpret_cast<float2*>(s_in + 3 * T + spos) = P.z.f();
+            *reinterpret_cast<float2*>(s_in + 4 * T + spos) = P.y.f();
+        }
         *reinterpret_cast<float2*>(s_B + bpos) = P.B.f();
         *reinterpret_cast<float2*>(s_C + bpos) = P.C.f();
+    };
+    // dB / dC of the super-tile at t0: sum the 4 wave partials; thread tid adds
+    // steps 2 (tid & 15), +1 of state tid >> 4
+    auto flush_dbc = [&](int64_t t0) {
+        const int nl = tid >> 4, k = 2 * (tid & 15);
+        float sB0 = 0.f, sB1 = 0.f, sC0 = 0.f, sC1 = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) {
+            const float* pb = s_wg + ((0 * kWaves + ww) * 16 + nl) * kWgN + k;
+            const float* pcc = s_wg + ((1 * kWaves + ww) * 16 + nl) * kWgN + k;
+            sB0 += pb[0]; sB1 += pb[1]; sC0 += pcc[0]; sC1 += pcc[1];
+        }
+        atomicAdd(dBb + nl * L + t0 + k, sB0);
+        atomicAdd(dBb + nl * L + t0 + k + 1, sB1);
+        atomicAdd(dCb + nl * L + t0 + k, sC0);
+        atomicAdd(dCb + nl * L + t0 + k + 1, sC1);
     };
 
     float gcar = 0.f, acar = 1.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
@@ -509,7 +533,7 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     fetch(nst - 1, P);
     for (int64_t st = nst - 1; st >= 0; --st) {
         const int64_t t0 = st * kSB;
-        lds_barrier();                 // previous super-tile's outputs have been stored
+        lds_barrier();                 // previous super-tile's outputs and dB / dC partials are consumed
         stage(P);
         float h0s[kQB];
 #pragma unroll
@@ -522,27 +546,20 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
         for (int a = 0; a < 5; ++a)
 #pragma unroll
             for (int qq = 0; qq < kQB; ++qq)
-                in_v[a][qq] = a < kNin ? s_in[a * kChPerWG * kStrB + row * kStrB + kT * qq + r] : 0.f;
+                in_v[a][qq] = (a < 3 || kZ) ? s_in[a * kChPerWG * kStrB + row * kStrB + kT * qq + r] : 0.f;
         lds_barrier();                 // s_in is reused for the outputs below
 
 #pragma unroll
         for (int qi = kQB - 1; qi >= 0; --qi) {
-            const int64_t tc = t0 + kT * qi;       // first step of this chunk
             const float uu = in_v[0][qi], pre = in_v[1][qi] + bias, dout = in_v[2][qi];
             const float zz = in_v[3][qi], yv = in_v[4][qi];
             const float dt = softplus ? softplus20(pre) : pre;
             const float dtu = dt * uu;
             const float sgz = kZ ? sigmoidf_(zz) : 1.f;
             const float dy = kZ ? dout * zz * sgz : dout;
-            float Bt[kT], Ct[kT];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 vb = *reinterpret_cast<const float4*>(s_B + r * kBCB + kT * qi + 4 * i);
-                const float4 vc = *reinterpret_cast<const float4*>(s_C + r * kBCB + kT * qi + 4 * i);
-                Bt[4 * i] = vb.x; Bt[4 * i + 1] = vb.y; Bt[4 * i + 2] = vb.z; Bt[4 * i + 3] = vb.w;
-                Ct[4 * i] = vc.x; Ct[4 * i + 1] = vc.y; Ct[4 * i + 2] = vc.z; Ct[4 * i + 3] = vc.w;
-            }
             const float h0 = h0s[qi];
+            const float* sBr = s_B + r * kBCB + kT * qi;
+            const float* sCr = s_C + r * kBCB + kT * qi;
 
             // ---- recompute a_t and h_t of the chunk from the checkpoint
             float as[kT], hs[kT];
@@ -551,77 +568,73 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
                 as[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
             });
             float hcur = h0;
-            static_for<kT>([&](auto K) {
-                constexpr int k = decltype(K)::value;
-                hcur = __builtin_fmaf(as[k], hcur, row_bcast<k>(dtu) * Bt[k]);
-                hs[k] = hcur;
+            static_for<4>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                const float4 vb = *reinterpret_cast<const float4*>(sBr + 4 * i);
+                const float bq[4] = {vb.x, vb.y, vb.z, vb.w};
+                static_for<4>([&](auto KI) {
+                    constexpr int k = 4 * i + decltype(KI)::value;
+                    hcur = __builtin_fmaf(as[k], hcur, row_bcast<k>(dtu) * bq[k & 3]);
+                    hs[k] = hcur;
+                });
             });
 
-            // ---- adjoint, last step first, in two halves of 8 steps
+            // ---- adjoint, last step first, four steps at a time
             float gv = gcar, anext = acar;
-            float s1r = 0.f, s2r = 0.f;
-            static_for<2>([&](auto HH) {
-                constexpr int hh = 1 - decltype(HH)::value;        // half 1 (steps 8..15) first
-                static_for<2>([&](auto CC) {
-                    constexpr int cc = 1 - decltype(CC)::value;
-                    constexpr int kg = 2 * hh + cc;
-                    float s1p[4], s2p[4], dBp[4], dCp[4];
-                    static_for<4>([&](auto KI) {
-                        constexpr int ki = 3 - decltype(KI)::value;
-                        constexpr int k = 4 * kg + ki;
-                        const float dyk = row_bcast<k>(dy);
-                        gv = __builtin_fmaf(anext, gv, dyk * Ct[k]);
-                        float hprev;
-                        if constexpr (k == 0) hprev = h0;
-                        else hprev = hs[k - 1];
-                        const float gah = gv * (as[k] * hprev);
-                        dA_acc = __builtin_fmaf(row_bcast<k>(dt), gah, dA_acc);
-                        s2p[ki] = av * gah;
-                        s1p[ki] = gv * Bt[k];
-                        dBp[ki] = gv * row_bcast<k>(dtu);
-                        dCp[ki] = dyk * hs[k];
-                        anext = as[k];
-                    });
-                    const int o = r * 8 + 4 * (cc ^ ((r >> 2) & 1));
-                    *reinterpret_cast<float4*>(tr1 + o) = make_float4(s1p[0], s1p[1], s1p[2], s1p[3]);
-                    *reinterpret_cast<float4*>(tr2 + o) = make_float4(s2p[0], s2p[1], s2p[2], s2p[3]);
-                    // dB / dC of steps 4kg..4kg+3 summed over the wave's rows:
-                    // row j holds step 4kg + j
-                    const float dBs = rows4_sum(dBp[0], dBp[1], dBp[2], dBp[3]);
-                    const float dCs = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
-                    s_wg[((0 * kWaves + w) * 16 + r) * kWgN + 4 * kg + j] = dBs;
-                    s_wg[((1 * kWaves + w) * 16 + r) * kWgN + 4 * kg + j] = dCs;
+            static_for<4>([&](auto KG) {
+                constexpr int kg = 3 - decltype(KG)::value;
+                const float4 vb = *reinterpret_cast<const float4*>(sBr + 4 * kg);
+                const float4 vc = *reinterpret_cast<const float4*>(sCr + 4 * kg);
+                const float bq[4] = {vb.x, vb.y, vb.z, vb.w};
+                const float cq[4] = {vc.x, vc.y, vc.z, vc.w};
+                float s1p[4], s2p[4], dBp[4], dCp[4];
+                static_for<4>([&](auto KI) {
+                    constexpr int ki = 3 - decltype(KI)::value;
+                    constexpr int k = 4 * kg + ki;
+                    const float dyk = row_bcast<k>(dy);
+                    gv = __builtin_fmaf(anext, gv, dyk * cq[ki]);
+                    float hprev;
+                    if constexpr (k == 0) hprev = h0;
+                    else hprev = hs[k - 1];
+                    const float gah = gv * (as[k] * hprev);
+                    dA_acc = __builtin_fmaf(row_bcast<k>(dt), gah, dA_acc);
+                    s2p[ki] = av * gah;
+                    s1p[ki] = gv * bq[ki];
+                    dBp[ki] = gv * row_bcast<k>(dtu);
+                    dCp[ki] = dyk * hs[k];
+                    anext = as[k];
                 });
-                // transposed sums of this half: lanes 8 hh .. 8 hh + 7 own its steps
-                float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
-#pragma unroll
-                for (int rr = 0; rr < kT; rr += 2) {
-                    const int o0 = rr * 8 + (((rr >> 2) & 1) ? hoff1 : hoff0);
-                    const int o1 = (rr + 1) * 8 + ((((rr + 1) >> 2) & 1) ? hoff1 : hoff0);
-                    a0 += tr1[o0]; a1 += tr1[o1];
-                    b0 += tr2[o0]; b1 += tr2[o1];
-                }
-                if ((r >> 3) == hh) { s1r = a0 + a1; s2r = b0 + b1; }
+                // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1)
+                *reinterpret_cast<float4*>(trw + r * 32 + 4 * ((2 * kg) ^ (r & 7))) =
+                    make_float4(s1p[0], s2p[0], s1p[1], s2p[1]);
+                *reinterpret_cast<float4*>(trw + r * 32 + 4 * ((2 * kg + 1) ^ (r & 7))) =
+                    make_float4(s1p[2], s2p[2], s1p[3], s2p[3]);
+                // dB / dC of steps 4kg..4kg+3 summed over the wave's rows:
+                // row j holds step 4kg + j
+                const float dBs = rows4_sum(dBp[0], dBp[1], dBp[2], dBp[3]);
+                const float dCs = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
+                s_wg[((0 * kWaves + w) * 16 + r) * kWgN + kT * qi + 4 * kg + j] = dBs;
+                s_wg[((1 * kWaves + w) * 16 + r) * kWgN + kT * qi + 4 * kg + j] = dCs;
             });
             gcar = gv;
             acar = anext;
 
-            // ---- dB / dC: sum the 4 wave partials, one global add per (state, step)
-            lds_barrier();
+            // transposed sums over states: this lane's step r
+            float s1r = 0.f, s2r = 0.f;
             {
-                const int nl = tid >> 4, k = tid & 15;
-                float sB = 0.f, sC = 0.f;
+                float2 v[kT];
 #pragma unroll
-                for (int ww = 0; ww < kWaves; ++ww) {
-                    sB += s_wg[((0 * kWaves + ww) * 16 + nl) * kWgN + k];
-                    sC += s_wg[((1 * kWaves + ww) * 16 + nl) * kWgN + k];
-                }
-                atomicAdd(dBrow + nl * L + tc + k, sB);
-                atomicAdd(dCrow + nl * L + tc + k, sC);
+                for (int rr = 0; rr < kT; ++rr)
+                    v[rr] = *reinterpret_cast<const float2*>(trw + rr * 32 + 4 * ((r >> 1) ^ (rr & 7)) + 2 * (r & 1));
+#pragma unroll
+                for (int wdt = 8; wdt >= 1; wdt >>= 1)
+#pragma unroll
+                    for (int i = 0; i < wdt; ++i) { v[i].x += v[i + wdt].x; v[i].y += v[i + wdt].y; }
+                s1r = v[0].x;
+                s2r = v[0].y;
             }
-            lds_barrier();
 
-            // ---- per-step outputs of step tc + r into the output tiles
+            // ---- per-step outputs of step t0 + 16 qi + r into the output tiles
             const float du = Dv * dy + dt * s1r;
             const float ddt = uu * s1r + s2r;
             const float dd = softplus ? ddt * sigmoidf_(pre) : ddt;
@@ -633,9 +646,11 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
             db_acc += dd;
         }
         lds_barrier();
-        store2<IT>(gdu + t0, *reinterpret_cast<const float2*>(s_in + 0 * kChPerWG * kStrB + spos));
-        store2<IT>(gdd + t0, *reinterpret_cast<const float2*>(s_in + 1 * kChPerWG * kStrB + spos));
-        if constexpr (kZ) store2<IT>(gdz + t0, *reinterpret_cast<const float2*>(s_in + 2 * kChPerWG * kStrB + spos));
+        flush_dbc(t0);
+        constexpr int T = kChPerWG * kStrB;
+        store2<IT>(bdu + t0 + odu, *reinterpret_cast<const float2*>(s_in + 0 * T + spos));
+        store2<IT>(bdd + t0 + odd, *reinterpret_cast<const float2*>(s_in + 1 * T + spos));
+        if constexpr (kZ) store2<IT>(bdz + t0 + odz, *reinterpret_cast<const float2*>(s_in + 2 * T + spos));
     }
 
     // ---- per-channel and per-(channel, state) sums over time and batch

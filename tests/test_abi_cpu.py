@@ -1,0 +1,306 @@
+"""CPU checks of the C ABI (libmamba_ss.so) and of the host side, no GPU.
+
+* the library loads, reports its ABI version and exports every function
+  that include/mamba_ss.h declares;
+* the ctypes structs of mamba_amd/_native.py have the sizes and field offsets
+  that a C compiler gives the header's structs (a small C program built here)
+  and that the library reports (ss_struct_sizes);
+* ss_fwd_check / ss_bwd_check (argument checks only, no device work) accept a
+  valid argument block and reject each kind of bad one with a message;
+* the Python boundary refuses CPU tensors (there is no CPU path) and fails
+  loudly when the library is missing;
+* nothing in the product package imports the oracle;
+* the benchmark's byte model gives the figures its docstring states and it
+  refuses more than one GPU.
+"""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mamba_ss.h")
+
+
+@pytest.fixture(scope="module")
+def nat():
+    from mamba_amd import _native
+    if not os.path.exists(_native.LIB_PATH):
+        from mamba_amd import build
+        build.build()
+    return _native
+
+
+@pytest.fixture(scope="module")
+def lib(nat):
+    return nat.load()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(ss_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_exported_list(nat):
+    assert header_functions() == sorted(nat.EXPORTED)
+
+
+def test_library_exports_every_declared_function(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib._name], capture_output=True, text=True, check=True).stdout
+    defined = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for name in header_functions():
+        assert name in defined, f"{name} is declared in mamba_ss.h but not exported"
+        assert getattr(lib, name) is not None
+
+
+def test_version_and_constants(lib, nat):
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 1
+    assert lib.ss_chunk_size() == 16
+    assert lib.ss_max_dstate() == 256
+    assert lib.ss_last_error() == b""
+
+
+C_PROBE = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "mamba_ss.h"
+#define F(T, m) printf(#T " " #m " %zu\n", offsetof(T, m));
+int main(void) {
+    printf("sizeof ss_fwd_args %zu\nsizeof ss_bwd_args %zu\n", sizeof(ss_fwd_args), sizeof(ss_bwd_args));
+    FIELDS
+    return 0;
+}
+"""
+
+
+def test_struct_layout_matches_c_compiler(nat, lib, tmp_path):
+    fields = [f"F(ss_fwd_args, {n})" for n, _ in nat.FwdArgs._fields_]
+    fields += [f"F(ss_bwd_args, {n})" for n, _ in nat.BwdArgs._fields_]
+    src = tmp_path / "probe.c"
+    src.write_text(C_PROBE.replace("FIELDS", "\n    ".join(fields)))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines()
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in lines}
+    assert got[("sizeof", "ss_fwd_args")] == ctypes.sizeof(nat.FwdArgs)
+    assert got[("sizeof", "ss_bwd_args")] == ctypes.sizeof(nat.BwdArgs)
+    for T, name in ((nat.FwdArgs, "ss_fwd_args"), (nat.BwdArgs, "ss_bwd_args")):
+        for n, _ in T._fields_:
+            assert got[(name, n)] == getattr(T, n).offset, f"{name}.{n}"
+    fs, bs = ctypes.c_int64(), ctypes.c_int64()
+    lib.ss_struct_sizes(ctypes.byref(fs), ctypes.byref(bs))
+    assert (fs.value, bs.value) == (ctypes.sizeof(nat.FwdArgs), ctypes.sizeof(nat.BwdArgs))
+    lib.ss_struct_sizes(None, None)   # either pointer may be NULL
+
+
+# ------------------------------------------------------------ argument checks --
+FAKE = 1 << 20   # a 16-byte aligned, never dereferenced address
+
+
+def valid_fwd(nat, batch=2, dim=32, seqlen=100, dstate=16, itype=None, has_z=True):
+    itype = nat.SS_F32 if itype is None else itype
+    a = nat.FwdArgs()
+    a.batch, a.dim, a.seqlen, a.dstate, a.n_groups = batch, dim, seqlen, dstate, 1
+    a.itype, a.is_var_B, a.is_var_C = itype, 1, 1
+    a.has_D, a.has_delta_bias, a.has_z, a.delta_softplus = 1, 1, int(has_z), 1
+    a.n_chunks = (seqlen + 15) // 16
+    for t in ("u", "delta", "z", "out", "y"):
+        setattr(a, f"{t}_batch_stride", dim * seqlen)
+        setattr(a, f"{t}_dim_stride", seqlen)
+    a.A_dim_stride, a.A_dstate_stride = dstate, 1
+    for t in ("B", "C"):
+        setattr(a, f"{t}_batch_stride", dstate * seqlen)
+        setattr(a, f"{t}_group_stride", dstate * seqlen)
+        setattr(a, f"{t}_dstate_stride", seqlen)
+    for i, p in enumerate(("u", "delta", "A", "B", "C", "D", "delta_bias", "z", "out", "x", "y")):
+        setattr(a, p, FAKE + 4096 * i)
+    return a
+
+
+def valid_bwd(nat, **kw):
+    b = nat.BwdArgs()
+    b.f = valid_fwd(nat, **kw)
+    dim, seqlen = b.f.dim, b.f.seqlen
+    for t in ("dout", "du", "ddelta", "dz"):
+        setattr(b, f"{t}_batch_stride", dim * seqlen)
+        setattr(b, f"{t}_dim_stride", seqlen)
+    for i, p in enumerate(("dout", "du", "ddelta", "dz", "dA", "dB", "dC", "dD", "ddelta_bias")):
+        setattr(b, p, FAKE + 65536 + 4096 * i)
+    return b
+
+
+def fwd_rc(lib, a):
+    return lib.ss_fwd_check(ctypes.byref(a)), lib.ss_last_error().decode()
+
+
+def bwd_rc(lib, b):
+    return lib.ss_bwd_check(ctypes.byref(b)), lib.ss_last_error().decode()
+
+
+def test_valid_blocks_pass(nat, lib):
+    for itype in (nat.SS_F32, nat.SS_BF16, nat.SS_F16):
+        assert fwd_rc(lib, valid_fwd(nat, itype=itype))[0] == nat.SS_OK
+        assert bwd_rc(lib, valid_bwd(nat, itype=itype))[0] == nat.SS_OK
+    assert fwd_rc(lib, valid_fwd(nat, dstate=256))[0] == nat.SS_OK
+    assert fwd_rc(lib, valid_fwd(nat, dstate=1))[0] == nat.SS_OK
+
+
+def test_empty_problem_needs_no_pointers(nat, lib):
+    for dims in ((0, 32, 100), (2, 0, 100), (2, 32, 0)):
+        a = valid_fwd(nat, *dims)
+        for p in ("u", "delta", "A", "B", "C", "x", "out"):
+            setattr(a, p, None)
+        assert fwd_rc(lib, a)[0] == nat.SS_OK
+
+
+FWD_BREAKS = [
+    ("negative size", lambda a: setattr(a, "seqlen", -1), "INVALID", "negative size"),
+    ("dstate 0", lambda a: setattr(a, "dstate", 0), "UNSUPPORTED", "dstate"),
+    ("dstate 257", lambda a: setattr(a, "dstate", 257), "UNSUPPORTED", "dstate"),
+    ("unknown itype", lambda a: setattr(a, "itype", 7), "INVALID", "itype"),
+    ("groups not dividing dim", lambda a: setattr(a, "n_groups", 3), "INVALID", "n_groups"),
+    ("zero groups", lambda a: setattr(a, "n_groups", 0), "INVALID", "n_groups"),
+    ("wrong n_chunks", lambda a: setattr(a, "n_chunks", 6), "INVALID", "n_chunks"),
+    ("u NULL", lambda a: setattr(a, "u", None), "INVALID", "u is NULL"),
+    ("x NULL", lambda a: setattr(a, "x", None), "INVALID", "x is NULL"),
+    ("out NULL", lambda a: setattr(a, "out", None), "INVALID", "out is NULL"),
+    ("D NULL with has_D", lambda a: setattr(a, "D", None), "INVALID", "D is NULL"),
+    ("z NULL with has_z", lambda a: setattr(a, "z", None), "INVALID", "z is NULL"),
+    ("misaligned delta", lambda a: setattr(a, "delta", FAKE + 2), "INVALID", "delta is misaligned"),
+    ("misaligned A", lambda a: setattr(a, "A", FAKE + 1), "INVALID", "A is misaligned"),
+    ("negative stride", lambda a: setattr(a, "B_dstate_stride", -1), "INVALID", "negative stride"),
+    ("huge grid", lambda a: (setattr(a, "batch", 1 << 40), setattr(a, "n_chunks", a.n_chunks)), "UNSUPPORTED",
+     "too large"),
+]
+
+
+@pytest.mark.parametrize("case", [c[0] for c in FWD_BREAKS])
+def test_fwd_check_rejects(nat, lib, case):
+    _, brk, code, msg = next(c for c in FWD_BREAKS if c[0] == case)
+    a = valid_fwd(nat)
+    brk(a)
+    rc, err = fwd_rc(lib, a)
+    assert rc == getattr(nat, f"SS_ERR_{code}"), (rc, err)
+    assert msg in err
+    # the same block inside a backward call is rejected the same way (out is not needed there)
+    if case != "out NULL":
+        b = valid_bwd(nat)
+        brk(b.f)
+        assert bwd_rc(lib, b)[0] == getattr(nat, f"SS_ERR_{code}")
+
+
+BWD_BREAKS = [
+    ("dout NULL", lambda b: setattr(b, "dout", None), "dout is NULL"),
+    ("du NULL", lambda b: setattr(b, "du", None), "du is NULL"),
+    ("dz NULL with has_z", lambda b: setattr(b, "dz", None), "dz is NULL"),
+    ("dB NULL", lambda b: setattr(b, "dB", None), "dB is NULL"),
+    ("dD NULL with has_D", lambda b: setattr(b, "dD", None), "dD is NULL"),
+    ("saved y NULL with has_z", lambda b: setattr(b.f, "y", None), "y (saved pre-gate output) is NULL"),
+    ("misaligned dA", lambda b: setattr(b, "dA", FAKE + 65536 + 2), "dA is misaligned"),
+    ("negative dout stride", lambda b: setattr(b, "dout_dim_stride", -5), "negative stride"),
+]
+
+
+@pytest.mark.parametrize("case", [c[0] for c in BWD_BREAKS])
+def test_bwd_check_rejects(nat, lib, case):
+    _, brk, msg = next(c for c in BWD_BREAKS if c[0] == case)
+    b = valid_bwd(nat)
+    brk(b)
+    rc, err = bwd_rc(lib, b)
+    assert rc == nat.SS_ERR_INVALID and msg in err, (rc, err)
+
+
+def test_optional_pointers_may_be_null_when_absent(nat, lib):
+    b = valid_bwd(nat, has_z=False)
+    b.f.has_D = b.f.has_delta_bias = 0
+    b.f.D = b.f.delta_bias = b.f.z = b.f.y = None
+    b.dz = b.dD = b.ddelta_bias = None
+    assert bwd_rc(lib, b)[0] == nat.SS_OK
+    a = valid_fwd(nat)
+    a.y = None   # has_z without y: the forward then just does not save the pre-gate output
+    assert fwd_rc(lib, a)[0] == nat.SS_OK
+
+
+def test_null_argument_block(nat, lib):
+    assert lib.ss_fwd_check(None) == nat.SS_ERR_INVALID
+    assert lib.ss_bwd_check(None) == nat.SS_ERR_INVALID
+    assert "null argument block" in lib.ss_last_error().decode()
+
+
+def test_error_message_is_per_thread(nat, lib):
+    import threading
+    a = valid_fwd(nat)
+    a.dstate = 0
+    assert fwd_rc(lib, a)[0] != nat.SS_OK
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.ss_last_error().decode()
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "dstate" in lib.ss_last_error().decode()
+
+
+def test_check_status_maps_to_exceptions(nat, lib):
+    a = valid_fwd(nat)
+    a.itype = 9
+    rc = lib.ss_fwd_check(ctypes.byref(a))
+    with pytest.raises(ValueError, match="itype"):
+        nat.check(rc, "ss_fwd")
+    nat.check(nat.SS_OK, "ss_fwd")
+
+
+# ------------------------------------------------------------------ host side --
+def test_python_boundary_refuses_cpu_tensors():
+    from mamba_amd import selective_scan as ss
+    from mamba_amd.ops.selective_scan_interface import SelectiveScanFn, selective_scan_fn
+    u = torch.randn(1, 4, 8)
+    A = -torch.ones(4, 2)
+    B = torch.randn(1, 1, 2, 8)
+    with pytest.raises(ValueError, match="no CPU path"):
+        ss.forward(u, u.clone(), A, B, B.clone(), None, None, True)
+    with pytest.raises(ValueError, match="no CPU path"):
+        selective_scan_fn(u, u.clone(), A, B, B.clone())
+    with pytest.raises(ValueError, match="no CPU path"):
+        SelectiveScanFn.apply(u, u.clone(), A, B, B.clone(), None)
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    from mamba_amd import _native
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "LIB_PATH", os.path.join(ROOT, "no_such_dir", "libmamba_ss.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.load()
+
+
+def test_product_package_does_not_import_the_oracle():
+    pkg = os.path.join(ROOT, "mamba_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M), f
+                assert "ss_oracle" not in text and "selective_scan_ref" not in text.replace(
+                    "reference's pure-PyTorch selective_scan_ref", ""), f
+
+
+def test_bench_byte_model():
+    sys.path.insert(0, ROOT)
+    import bench
+    fwd, bwd = bench.algorithmic_bytes(8, 1536, 16, 2048, 4)
+    assert (fwd, bwd) == (404_860_928, 709_058_560)
+    assert sum(bench.algorithmic_bytes(4, 5120, 16, 8192, 2)) == 3_700_482_048
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr

@@ -40,6 +40,13 @@ CASES = [
     (1, 32, 16, 128, torch.float16, 2, True, True, True, True, True, True),     # fp16, 2 groups
     (2, 48, 16, 192, torch.float32, 1, True, True, False, True, True, True),    # no z, 3 workgroups
     (1, 16, 16, 64, torch.bfloat16, 1, True, True, True, False, False, True),   # one super-tile, no D / bias
+    # chunk-boundary invariance: lengths either side of 128 and 2048 steps
+    (1, 16, 16, 127, torch.float32, 1, True, True, True, True, True, True),
+    (1, 16, 16, 128, torch.float32, 1, True, True, True, True, True, True),
+    (1, 16, 16, 129, torch.float32, 1, True, True, True, True, True, True),
+    (1, 16, 16, 2047, torch.float32, 1, True, True, True, True, True, True),
+    (1, 16, 16, 2048, torch.float32, 1, True, True, True, True, True, True),
+    (1, 16, 16, 2049, torch.float32, 1, True, True, True, True, True, True),
 ]
 
 

@@ -12,7 +12,13 @@ describes the dominant kernel, timed with HIP events on the stream it runs
 on; ``cpu_baseline`` times the CPU oracle (pure-PyTorch selective_scan_ref)
 on a bounded slice of the same workload on this host's cores.
 
+``--calibrate-copy MIB`` instead times a plain device-to-device copy of MIB
+MiB (torch's copy kernel); under ``rocprofv3 --pmc FETCH_SIZE`` /
+``WRITE_SIZE`` it gives the factor between those counters and bytes actually
+read / written, which scales the scan kernels' counters into ``traffic``.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--no-cpu]
+       python bench.py --calibrate-copy 1024
 """
 import argparse
 import json
@@ -50,7 +56,7 @@ def algorithmic_bytes(batch, dim, dstate, seqlen, s, groups=1):
     return fwd, bwd
 
 
-def cpu_baseline(dtype_name, seqlen, dstate, min_seconds=5.0, max_dim=1536):
+def cpu_baseline(dtype_name, seqlen, dstate, min_seconds=10.0, max_dim=1536):
     """Times the CPU oracle (fwd + autograd bwd) on 1 batch row x `d` channels
     at the full sequence length, on this host's cores.  `d` starts at 192 and
     is doubled until one run takes at least `min_seconds` (bounded by
@@ -87,6 +93,26 @@ def cpu_baseline(dtype_name, seqlen, dstate, min_seconds=5.0, max_dim=1536):
     }
 
 
+def calibrate_copy(mib, reps=5):
+    """Copies `mib` MiB device to device `reps` times; prints one JSON line."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = n * 4
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "ms": round(ms, 5),
+                      "GB/s (read + write)": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,6 +121,8 @@ def main():
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only time a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -102,6 +130,9 @@ def main():
               f"WORLD_SIZE {world}); the selective scan would shard by batch or channel "
               "(see DESIGN.md), which is not built here.", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     import torch
     from mamba_amd import selective_scan as ss
@@ -158,8 +189,13 @@ def main():
             ss.backward_into(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
                              z=z, y=y, dz=dz)
 
+        tname = {torch.float32: "float", torch.bfloat16: "bf16", torch.float16: "half"}[dtype]
+        fname = ss.forward_kernel_name(u, dl, A, B, C, D, bias, True, out, xck, z=z, y=y)
+        bname = ss.backward_kernel_name(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
+                                        z=z, y=y, dz=dz)
+        fname, bname = f"{fname}<{tname}, z>", f"{bname}<{tname}, z>"
         kernel_ms = {}
-        for name, fn in (("ss_fwd_kernel", fwd), ("ss_bwd_kernel", bwd)):
+        for name, fn in ((fname, fwd), (bname, bwd)):
             fn()
             torch.cuda.synchronize()
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -177,7 +213,7 @@ def main():
     total = fwd_bytes + bwd_bytes
     gbs = total / (ms_per_step * 1e-3) / 1e9
     dom = max(kernel_ms, key=kernel_ms.get)
-    dom_bytes = fwd_bytes if dom == "ss_fwd_kernel" else bwd_bytes
+    dom_bytes = fwd_bytes if dom == fname else bwd_bytes
     achieved = dom_bytes / (kernel_ms[dom] * 1e-3) / 1e9
 
     traffic = None

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 1
+#define SS_ABI_VERSION 2
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -103,6 +103,15 @@ typedef struct ss_bwd_args {
     float* dC;               /* accumulated into, fp32, shape of C, contiguous */
     float* dD;               /* accumulated into; may be NULL iff !has_D */
     float* ddelta_bias;      /* accumulated into; may be NULL iff !has_delta_bias */
+    /* optional device scratch of at least ss_bwd_workspace_bytes() bytes,
+       16-byte aligned, contents ignored (the call clears what it uses).  With
+       it, the dB / dC sums over channels are spread over several copies and
+       added up at the end, instead of every channel block adding into the
+       same dB / dC addresses; NULL gives the same results, more slowly when
+       many channel blocks share a group.  Calls that overlap in time must not
+       share a workspace. */
+    void* workspace;
+    int64_t workspace_bytes;
 } ss_bwd_args;
 
 /* ABI version (SS_ABI_VERSION of the built library). */
@@ -127,6 +136,20 @@ const char* ss_last_error(void);
 /* Argument checks only, no device work: SS_OK or an error code. */
 int ss_fwd_check(const ss_fwd_args* a);
 int ss_bwd_check(const ss_bwd_args* a);
+
+/* Bytes of workspace ss_bwd can use for these arguments (0: none), or -1
+   (with ss_last_error set) when the arguments fail the checks.  No device
+   work.  The reference needs none: its backward adds every channel's dB / dC
+   into the output directly (backward_kernel.cu:457-479). */
+int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a);
+
+/* Base name of the kernel that ss_fwd / ss_bwd would launch for these
+   arguments ("ss_fwd_fast", "ss_fwd_kernel", "ss_bwd_fast", "ss_bwd_kernel"),
+   "" when there is no work, NULL (with ss_last_error set) when the arguments
+   fail the checks.  No device work; for profiling and tests.  No counterpart
+   in the reference, which has one kernel per direction. */
+const char* ss_fwd_kernel_name(const ss_fwd_args* a);
+const char* ss_bwd_kernel_name(const ss_bwd_args* a);
 
 /* Forward scan: writes out and x.  Replaces selective_scan.forward /
    forward_kernel_launch (selective_scan.cpp:184-244, forward_kernel.cu:313-333). */

@@ -13,11 +13,13 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
-    "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_fwd", "ss_bwd",
+    "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_bwd_workspace_bytes",
+    "ss_fwd_kernel_name", "ss_bwd_kernel_name",
+    "ss_fwd", "ss_bwd",
 )
 
 _i64, _i32, _p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
@@ -51,6 +53,7 @@ class BwdArgs(ctypes.Structure):
         ("dz_batch_stride", _i64), ("dz_dim_stride", _i64),
         ("dout", _p), ("du", _p), ("ddelta", _p), ("dz", _p),
         ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("ddelta_bias", _p),
+        ("workspace", _p), ("workspace_bytes", _i64),
     ]
 
 
@@ -81,6 +84,12 @@ def load():
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(T)]
             fn.restype = ctypes.c_int
+        for name, T in (("ss_fwd_kernel_name", FwdArgs), ("ss_bwd_kernel_name", BwdArgs)):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.POINTER(T)]
+            fn.restype = ctypes.c_char_p
+        lib.ss_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
+        lib.ss_bwd_workspace_bytes.restype = _i64
         lib.ss_fwd.argtypes = [ctypes.POINTER(FwdArgs), _p]
         lib.ss_fwd.restype = ctypes.c_int
         lib.ss_bwd.argtypes = [ctypes.POINTER(BwdArgs), _p]

@@ -175,6 +175,45 @@ int check_bwd(const ss_bwd_args* a, bool* empty) {
     return SS_OK;
 }
 
+ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
+    ss::BwdParams p{};
+    p.f = make_fwd_params(&a->f);
+    p.wg_reduce = (p.f.dpg % ss::kChPerWG) == 0;
+    {
+        const size_t a4 = 4 * elem_size(a->f.itype);
+        bool ok = aligned(a->dout, a4) && aligned(a->du, a4) && aligned(a->ddelta, a4) &&
+                  a->dout_batch_stride % 4 == 0 && a->dout_dim_stride % 4 == 0 &&
+                  a->du_batch_stride % 4 == 0 && a->du_dim_stride % 4 == 0 &&
+                  a->ddelta_batch_stride % 4 == 0 && a->ddelta_dim_stride % 4 == 0;
+        if (a->f.has_z) ok = ok && aligned(a->dz, a4) && a->dz_batch_stride % 4 == 0 && a->dz_dim_stride % 4 == 0;
+        p.stream_vec_bwd = ok;
+    }
+    p.do_bs = a->dout_batch_stride; p.do_ds = a->dout_dim_stride;
+    p.du_bs = a->du_batch_stride; p.du_ds = a->du_dim_stride;
+    p.dd_bs = a->ddelta_batch_stride; p.dd_ds = a->ddelta_dim_stride;
+    p.dz_bs = a->dz_batch_stride; p.dz_ds = a->dz_dim_stride;
+    p.dout = a->dout; p.du = a->du; p.ddelta = a->ddelta; p.dz = a->f.has_z ? a->dz : nullptr;
+    p.dA = a->dA; p.dB = a->dB; p.dC = a->dC;
+    p.dD = a->f.has_D ? a->dD : nullptr;
+    p.ddelta_bias = a->f.has_delta_bias ? a->ddelta_bias : nullptr;
+    p.ws = nullptr;
+    p.ws_slices = 1;
+    p.ws_stride = 0;
+    return p;
+}
+
+// Workspace layout for p: slices and bytes (0 when the fast backward does
+// not use one: other kernel, one slice, or dB / dC not 16-byte aligned).
+int64_t ws_bytes_for(const ss::BwdParams& p, int* slices) {
+    *slices = ss::bwd_ws_slices(p);
+    if (*slices <= 1 || !aligned(p.dB, 16) || !aligned(p.dC, 16)) {
+        *slices = 1;
+        return 0;
+    }
+    const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * p.f.seqlen;
+    return int64_t(2) * *slices * stride * int64_t(sizeof(float));
+}
+
 }  // namespace
 
 extern "C" {
@@ -215,31 +254,46 @@ int ss_fwd(const ss_fwd_args* a, void* stream) {
     return ok();
 }
 
+int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a) {
+    bool empty = false;
+    if (check_bwd(a, &empty) != SS_OK) return -1;
+    ok();
+    if (empty) return 0;
+    int slices = 1;
+    return ws_bytes_for(make_bwd_params(a), &slices);
+}
+
+const char* ss_fwd_kernel_name(const ss_fwd_args* a) {
+    bool empty = false;
+    if (check_fwd(a, &empty) != SS_OK) return nullptr;
+    ok();
+    return empty ? "" : ss::fwd_kernel_name(make_fwd_params(a));
+}
+
+const char* ss_bwd_kernel_name(const ss_bwd_args* a) {
+    bool empty = false;
+    if (check_bwd(a, &empty) != SS_OK) return nullptr;
+    ok();
+    return empty ? "" : ss::bwd_kernel_name(make_bwd_params(a));
+}
+
 int ss_bwd(const ss_bwd_args* a, void* stream) {
     bool empty = false;
     int rc = check_bwd(a, &empty);
     if (rc != SS_OK) return rc;
     if (empty) return ok();
-    ss::BwdParams p{};
-    p.f = make_fwd_params(&a->f);
-    p.wg_reduce = (p.f.dpg % ss::kChPerWG) == 0;
-    {
-        const size_t a4 = 4 * elem_size(a->f.itype);
-        bool ok = aligned(a->dout, a4) && aligned(a->du, a4) && aligned(a->ddelta, a4) &&
-                  a->dout_batch_stride % 4 == 0 && a->dout_dim_stride % 4 == 0 &&
-                  a->du_batch_stride % 4 == 0 && a->du_dim_stride % 4 == 0 &&
-                  a->ddelta_batch_stride % 4 == 0 && a->ddelta_dim_stride % 4 == 0;
-        if (a->f.has_z) ok = ok && aligned(a->dz, a4) && a->dz_batch_stride % 4 == 0 && a->dz_dim_stride % 4 == 0;
-        p.stream_vec_bwd = ok;
+    ss::BwdParams p = make_bwd_params(a);
+    int slices = 1;
+    const int64_t need = ws_bytes_for(p, &slices);
+    if (need > 0 && a->workspace) {
+        if (a->workspace_bytes < need)
+            return fail(SS_ERR_INVALID, "workspace of %lld bytes, %lld needed", (long long)a->workspace_bytes,
+                        (long long)need);
+        if (!aligned(a->workspace, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
+        p.ws = static_cast<float*>(a->workspace);
+        p.ws_slices = slices;
+        p.ws_stride = need / int64_t(sizeof(float)) / (2 * slices);
     }
-    p.do_bs = a->dout_batch_stride; p.do_ds = a->dout_dim_stride;
-    p.du_bs = a->du_batch_stride; p.du_ds = a->du_dim_stride;
-    p.dd_bs = a->ddelta_batch_stride; p.dd_ds = a->ddelta_dim_stride;
-    p.dz_bs = a->dz_batch_stride; p.dz_ds = a->dz_dim_stride;
-    p.dout = a->dout; p.du = a->du; p.ddelta = a->ddelta; p.dz = a->f.has_z ? a->dz : nullptr;
-    p.dA = a->dA; p.dB = a->dB; p.dC = a->dC;
-    p.dD = a->f.has_D ? a->dD : nullptr;
-    p.ddelta_bias = a->f.has_delta_bias ? a->ddelta_bias : nullptr;
     hipError_t e = ss::launch_bwd(p, a->f.itype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
     return ok();

@@ -55,8 +55,9 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     const int r = lane & 15;
     const int j = lane >> 4;
     const int64_t nblk = (p.dim + kChPerWG - 1) / kChPerWG;
-    const int64_t b = blockIdx.x / nblk;
-    const int64_t c_raw = (blockIdx.x % nblk) * kChPerWG + w * kRows + j;
+    const int64_t blk = xcd_block_id();
+    const int64_t b = blk / nblk;
+    const int64_t c_raw = (blk % nblk) * kChPerWG + w * kRows + j;
     const bool cval = c_raw < p.dim;
     const int64_t c = cval ? c_raw : p.dim - 1;
     const int64_t g = c / p.dpg;
@@ -434,8 +435,9 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     const int j = lane >> 4;
     const int row = w * kRows + j;
     const int64_t nblk = p.dim / kChPerWG;
-    const int64_t b = blockIdx.x / nblk;
-    const int64_t c0 = (blockIdx.x % nblk) * kChPerWG;
+    const int64_t blk = xcd_block_id();
+    const int64_t b = blk / nblk;
+    const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
     const int64_t L = p.seqlen;
@@ -465,8 +467,10 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
     const float* gx = p.x + (b * p.n_chunks * p.dim + c) * kT + r;
     const int64_t x_chunk_stride = p.dim * kT;
-    float* dBb = q.dB + (b * G + g) * int64_t(kT) * L;
-    float* dCb = q.dC + (b * G + g) * int64_t(kT) * L;
+    // dB / dC of this batch row and group, or of its slice of the workspace
+    const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
+    float* dBb = (q.ws ? q.ws + 2 * slice * q.ws_stride : q.dB) + (b * G + g) * int64_t(kT) * L;
+    float* dCb = (q.ws ? q.ws + (2 * slice + 1) * q.ws_stride : q.dC) + (b * G + g) * int64_t(kT) * L;
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -670,6 +674,40 @@ bool bwd_fast_ok(const BwdParams& q) {
            (!p.has_z || p.y != nullptr);
 }
 
+// ------------------------------------------------------- dB / dC slices --
+// Clears the workspace (a fill kernel rather than a memset, so the sequence
+// can be captured in a graph).
+__global__ __launch_bounds__(256) void ss_ws_zero(float4* __restrict__ ws, int64_t n4) {
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride)
+        ws[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// dB += sum of the dB slices, dC += sum of the dC slices (n4 float4 each).
+__global__ __launch_bounds__(256) void ss_ws_reduce(const float4* __restrict__ ws, int slices, int64_t n4,
+                                                    float4* __restrict__ dB, float4* __restrict__ dC) {
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        float4 sb = dB[i], sc = dC[i];
+        for (int k = 0; k < slices; ++k) {
+            const float4 vb = ws[(2 * k) * n4 + i], vc = ws[(2 * k + 1) * n4 + i];
+            sb.x += vb.x; sb.y += vb.y; sb.z += vb.z; sb.w += vb.w;
+            sc.x += vc.x; sc.y += vc.y; sc.z += vc.z; sc.w += vc.w;
+        }
+        dB[i] = sb;
+        dC[i] = sc;
+    }
+}
+
+int bwd_ws_slices(const BwdParams& p) {
+    if (!bwd_fast_ok(p)) return 1;
+    // about 12 channel blocks per slice; a handful of slices already removes
+    // most of the contention, more only cost reduction traffic
+    const int64_t blocks = p.f.dpg / kChPerWG;
+    const int64_t k = (blocks + 11) / 12;
+    return int(k < 1 ? 1 : (k > 16 ? 16 : k));
+}
+
 template <typename IT>
 static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     const int64_t nblk = (p.f.dim + kChPerWG - 1) / kChPerWG;
@@ -678,8 +716,19 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     const int spl = int((p.f.dstate + 15) / 16);
     const bool vbc = p.f.var_B && p.f.var_C;
     if (bwd_fast_ok(p)) {
+        const int64_t n4 = p.ws ? p.ws_stride / 4 : 0;
+        const unsigned rgrid = unsigned(n4 > 0 ? (n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048 : 1);
+        if (p.ws) {
+            hipLaunchKernelGGL(ss_ws_zero, dim3(rgrid), dim3(256), 0, stream,
+                               reinterpret_cast<float4*>(p.ws), 2 * p.ws_slices * n4);
+        }
         if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_bwd_fast<IT, false>), grid, block, 0, stream, p);
+        if (p.ws) {
+            hipLaunchKernelGGL(ss_ws_reduce, dim3(rgrid), dim3(256), 0, stream,
+                               reinterpret_cast<const float4*>(p.ws), int(p.ws_slices), n4,
+                               reinterpret_cast<float4*>(p.dB), reinterpret_cast<float4*>(p.dC));
+        }
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, false>), grid, block, 0, stream, p);
@@ -689,6 +738,8 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     else hipLaunchKernelGGL((ss_bwd_kernel<IT, 16, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
+
+const char* bwd_kernel_name(const BwdParams& p) { return bwd_fast_ok(p) ? "ss_bwd_fast" : "ss_bwd_kernel"; }
 
 hipError_t launch_bwd(const BwdParams& p, int itype, hipStream_t stream) {
     switch (itype) {

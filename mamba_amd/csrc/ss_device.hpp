@@ -22,6 +22,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kChPerWG = kRows * kWaves;
 constexpr int kChunk = 16;        // steps per checkpoint of the state h
 constexpr int kMaxSPL = 16;       // state groups: dstate <= 16 * kMaxSPL = 256
+constexpr int kXcds = 8;          // accelerator complex dies of an MI355X
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Scratch layout of the in-row transposed sum: per row, 16 lanes x 16
@@ -263,5 +264,16 @@ __device__ __forceinline__ float softplus20(float x) {
 
 // 1 / (1 + exp(-x)); exp overflow gives 1 / inf = 0.
 __device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+
+// Workgroups are dispatched round-robin over the XCDs (blockIdx.x % kXcds
+// runs on XCD blockIdx.x % kXcds).  This renumbering hands each XCD a
+// contiguous range of logical workgroup ids, so the workgroups of one batch
+// row, which read the same B / C and add into the same dB / dC, share one
+// XCD's L2.  Grids that are not a multiple of kXcds keep the plain order.
+__device__ __forceinline__ int64_t xcd_block_id() {
+    const uint32_t n = gridDim.x, i = blockIdx.x;
+    if (n % kXcds != 0) return i;
+    return int64_t(i % kXcds) * (n / kXcds) + i / kXcds;
+}
 
 }  // namespace ss

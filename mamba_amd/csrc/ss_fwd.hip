@@ -30,8 +30,9 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
     const int r = lane & 15;
     const int j = lane >> 4;
     const int64_t nblk = (p.dim + kChPerWG - 1) / kChPerWG;
-    const int64_t b = blockIdx.x / nblk;
-    const int64_t c_raw = (blockIdx.x % nblk) * kChPerWG + w * kRows + j;
+    const int64_t blk = xcd_block_id();
+    const int64_t b = blk / nblk;
+    const int64_t c_raw = (blk % nblk) * kChPerWG + w * kRows + j;
     const bool cval = c_raw < p.dim;
     const int64_t c = cval ? c_raw : p.dim - 1;
     const int64_t g = c / p.dpg;
@@ -262,8 +263,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const int j = lane >> 4;
     const int row = w * kRows + j;                 // this lane's channel row in the workgroup
     const int64_t nblk = p.dim / kChPerWG;
-    const int64_t b = blockIdx.x / nblk;
-    const int64_t c0 = (blockIdx.x % nblk) * kChPerWG;
+    const int64_t blk = xcd_block_id();
+    const int64_t b = blk / nblk;
+    const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
     const int64_t L = p.seqlen;
@@ -389,6 +391,8 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
     else hipLaunchKernelGGL((ss_fwd_kernel<IT, 16, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
+
+const char* fwd_kernel_name(const FwdParams& p) { return fwd_fast_ok(p) ? "ss_fwd_fast" : "ss_fwd_kernel"; }
 
 hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream) {
     switch (itype) {

@@ -30,10 +30,23 @@ struct BwdParams {
     int64_t do_bs, do_ds, du_bs, du_ds, dd_bs, dd_ds, dz_bs, dz_ds;
     const void* dout; void* du; void* ddelta; void* dz;
     float* dA; float* dB; float* dC; float* dD; float* ddelta_bias;
+    // dB / dC slices: when ws is set, the workgroups of channel block k add
+    // into slice k % ws_slices of ws (2 * ws_slices arrays of ws_stride
+    // floats: dB, dC of slice 0, then of slice 1, ...), summed into dB / dC
+    // by a separate pass.  Fewer workgroups per address, less contention.
+    float* ws;
+    int32_t ws_slices;
+    int64_t ws_stride;
 };
+
+// dB / dC slices the fast backward uses for p (1: add into dB / dC directly)
+int bwd_ws_slices(const BwdParams& p);
 
 // Return hipSuccess or the launch error.
 hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int itype, hipStream_t stream);
+// base name of the kernel template launch_fwd / launch_bwd picks for p
+const char* fwd_kernel_name(const FwdParams& p);
+const char* bwd_kernel_name(const BwdParams& p);
 
 }  // namespace ss

@@ -120,10 +120,7 @@ def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
-    """Forward into caller-allocated ``out`` (delta's dtype), ``x`` (fp32
-    (batch, n_chunks, dim, dstate) contiguous) and, with ``z``, ``y``."""
-    lib = nat.load()
+def _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y):
     _require(out is not None and x is not None, "out and x are required")
     _check_seq_tensor("out", out, u.shape, delta.dtype, u.device)
     batch, dim, seqlen = u.shape
@@ -132,9 +129,27 @@ def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *
              "x must be a contiguous fp32 (batch, n_chunks, dim, dstate) tensor")
     if y is not None:
         _check_seq_tensor("y", y, u.shape, delta.dtype, u.device)
-    a = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
+    return _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
+
+
+def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
+    """Forward into caller-allocated ``out`` (delta's dtype), ``x`` (fp32
+    (batch, n_chunks, dim, dstate) contiguous) and, with ``z``, ``y``."""
+    lib = nat.load()
+    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y)
     with torch.cuda.device(u.device):
         nat.check(lib.ss_fwd(ctypes.byref(a), _stream(u.device)), "selective_scan.forward")
+
+
+def forward_kernel_name(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
+    """Base name of the kernel ``forward_into`` launches for these tensors
+    ("" when there is no work).  No device work."""
+    lib = nat.load()
+    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y)
+    name = lib.ss_fwd_kernel_name(ctypes.byref(a))
+    if name is None:
+        nat.check(nat.SS_ERR_INVALID, "selective_scan.forward_kernel_name")
+    return name.decode()
 
 
 def forward(u, delta, A, B, C, D=None, delta_bias=None, use_delta_softplus=True, *, z=None):
@@ -152,12 +167,8 @@ def forward(u, delta, A, B, C, D=None, delta_bias=None, use_delta_softplus=True,
     return [out, x] if z is None else [out, x, y]
 
 
-def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
-                  du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None):
-    """Backward into caller-allocated gradients.  du, ddelta (and dz) are
-    overwritten; dA, dB, dC, dD, ddelta_bias are fp32 and accumulated into,
-    so pass zeros for plain gradients."""
-    lib = nat.load()
+def _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                   du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz):
     _require(x is not None, "x (the forward's checkpoints) is required")
     _require(z is None or (y is not None and dz is not None), "y from the forward and dz are required with z")
     batch, dim, seqlen = u.shape
@@ -187,8 +198,60 @@ def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
         b.dz_batch_stride, b.dz_dim_stride = dz.stride(0), dz.stride(1)
     b.dout, b.du, b.ddelta, b.dz = _ptr(dout), _ptr(du), _ptr(ddelta), _ptr(dz)
     b.dA, b.dB, b.dC, b.dD, b.ddelta_bias = _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(ddelta_bias)
+    return b
+
+
+def workspace_bytes(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                    du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None):
+    """Bytes of scratch ``backward_into`` can use for these tensors (0: none)."""
+    lib = nat.load()
+    b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                       du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
+    n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))
+    if n < 0:
+        nat.check(nat.SS_ERR_INVALID, "selective_scan.workspace_bytes")
+    return int(n)
+
+
+def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                  du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None, workspace="auto"):
+    """Backward into caller-allocated gradients.  du, ddelta (and dz) are
+    overwritten; dA, dB, dC, dD, ddelta_bias are fp32 and accumulated into,
+    so pass zeros for plain gradients.
+
+    ``workspace``: "auto" allocates the scratch the library asks for (see
+    ``workspace_bytes``) from torch's caching allocator; a uint8 / any CUDA
+    tensor is used as given; None runs without one (same results).
+    """
+    lib = nat.load()
+    b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                       du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
+    if isinstance(workspace, str):
+        _require(workspace == "auto", f"workspace must be 'auto', None or a tensor, got {workspace!r}")
+        n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))
+        if n < 0:
+            nat.check(nat.SS_ERR_INVALID, "selective_scan.backward")
+        workspace = torch.empty(n, dtype=torch.uint8, device=u.device) if n > 0 else None
+    if workspace is not None:
+        _require(workspace.device == u.device and workspace.is_contiguous(),
+                 "workspace must be a contiguous tensor on the inputs' device")
+        b.workspace = _ptr(workspace)
+        b.workspace_bytes = workspace.numel() * workspace.element_size()
     with torch.cuda.device(u.device):
         nat.check(lib.ss_bwd(ctypes.byref(b), _stream(u.device)), "selective_scan.backward")
+
+
+def backward_kernel_name(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                         du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None):
+    """Base name of the kernel ``backward_into`` launches for these tensors
+    ("" when there is no work).  No device work."""
+    lib = nat.load()
+    b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                       du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
+    name = lib.ss_bwd_kernel_name(ctypes.byref(b))
+    if name is None:
+        nat.check(nat.SS_ERR_INVALID, "selective_scan.backward_kernel_name")
+    return name.decode()
 
 
 def backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus, *, z=None, y=None):

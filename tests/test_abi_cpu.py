@@ -59,7 +59,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 1
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 2
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -304,3 +304,42 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_kernel_name_query(nat, lib):
+    def fname(a):
+        r = lib.ss_fwd_kernel_name(ctypes.byref(a))
+        return None if r is None else r.decode()
+
+    def bname(b):
+        r = lib.ss_bwd_kernel_name(ctypes.byref(b))
+        return None if r is None else r.decode()
+    # dstate 16, variable B / C, seqlen a multiple of 64, 16-channel groups: cooperative fast paths
+    assert fname(valid_fwd(nat, seqlen=128)) == "ss_fwd_fast"
+    assert bname(valid_bwd(nat, seqlen=128)) == "ss_bwd_fast"
+    # a ragged length or another dstate takes the general kernels
+    assert fname(valid_fwd(nat, seqlen=100)) == "ss_fwd_kernel"
+    assert bname(valid_bwd(nat, seqlen=100)) == "ss_bwd_kernel"
+    assert fname(valid_fwd(nat, seqlen=128, dstate=32)) == "ss_fwd_kernel"
+    # no work, and invalid arguments
+    assert fname(valid_fwd(nat, batch=0)) == ""
+    bad = valid_fwd(nat)
+    bad.dstate = 0
+    assert fname(bad) is None and "dstate" in lib.ss_last_error().decode()
+
+
+def test_workspace_query(nat, lib):
+    # 2 channel blocks per group: one slice, no workspace
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, seqlen=128))) == 0
+    # 1536 channels in one group = 96 blocks: 8 slices of dB and dC (batch * dstate * seqlen floats each)
+    b = valid_bwd(nat, batch=2, dim=1536, seqlen=128)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 8 * (2 * 16 * 128) * 4
+    # the general kernel (ragged length) uses none; invalid arguments give -1
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, dim=1536, seqlen=100))) == 0
+    bad = valid_bwd(nat)
+    bad.dout = None
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(bad)) == -1
+    assert "dout is NULL" in lib.ss_last_error().decode()
+    # 5120 channels: 320 blocks, capped at 16 slices
+    b = valid_bwd(nat, batch=1, dim=5120, seqlen=64)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 16 * (16 * 64) * 4

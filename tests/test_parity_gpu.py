@@ -40,6 +40,9 @@ CASES = [
     (1, 32, 16, 128, torch.float16, 2, True, True, True, True, True, True),     # fp16, 2 groups
     (2, 48, 16, 192, torch.float32, 1, True, True, False, True, True, True),    # no z, 3 workgroups
     (1, 16, 16, 64, torch.bfloat16, 1, True, True, True, False, False, True),   # one super-tile, no D / bias
+    # many channel blocks per group: dB / dC summed through workspace slices
+    (2, 512, 16, 256, torch.float32, 1, True, True, True, True, True, True),    # 32 blocks: 3 slices
+    (1, 768, 16, 128, torch.bfloat16, 2, True, True, True, True, True, True),   # 24 blocks per group: 2 slices
     # chunk-boundary invariance: lengths either side of 128 and 2048 steps
     (1, 16, 16, 127, torch.float32, 1, True, True, True, True, True, True),
     (1, 16, 16, 128, torch.float32, 1, True, True, True, True, True, True),
@@ -148,3 +151,27 @@ def test_fast_path_strided_z_and_last_state():
     assert_close(zz.grad.cpu(), rgrads["z"], 1e-3, 1e-3, "dz")
     for k in ("delta", "A", "B", "C", "D", "delta_bias"):
         assert_close(g[k].grad.cpu(), rgrads[k], 1e-3, 1e-3, f"d{k}")
+
+
+def test_backward_with_and_without_workspace():
+    """The dB / dC slices (workspace) and direct accumulation give the same gradients."""
+    from mamba_amd import selective_scan as ss
+    print("\n[parity] workspace vs direct b2-d512-n16-l128 fp32", flush=True)
+    dev = torch.device("cuda:0")
+    x = make_inputs(2, 512, 16, 128, seed=21)
+    t = {k: x[k].to(dev) for k in NAMES}
+    dout = x["dout"].to(dev)
+    out, xck, y = ss.forward(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], True, z=t["z"])
+    res = {}
+    for mode in ("auto", None):
+        g = [torch.empty_like(t["u"]), torch.empty_like(t["delta"])] + \
+            [torch.zeros(t[k].shape, dtype=torch.float32, device=dev) for k in ("A", "B", "C", "D", "delta_bias")]
+        dz = torch.empty_like(t["z"])
+        args = (t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], dout, xck, True, *g)
+        if mode == "auto":
+            assert ss.workspace_bytes(*args, z=t["z"], y=y, dz=dz) == 2 * 3 * (2 * 16 * 128) * 4
+        ss.backward_into(*args, z=t["z"], y=y, dz=dz, workspace=mode)
+        torch.cuda.synchronize()
+        res[mode] = [v.cpu() for v in g] + [dz.cpu()]
+    for a, b_, name in zip(res["auto"], res[None], ("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz")):
+        assert_close(a, b_, 1e-5, 1e-5, name)

@@ -193,7 +193,11 @@ def main():
         fname = ss.forward_kernel_name(u, dl, A, B, C, D, bias, True, out, xck, z=z, y=y)
         bname = ss.backward_kernel_name(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
                                         z=z, y=y, dz=dz)
+        ws = ss.workspace_bytes(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
+                                z=z, y=y, dz=dz)
         fname, bname = f"{fname}<{tname}, z>", f"{bname}<{tname}, z>"
+        if ws > 0:   # the backward is three launches: clear slices, scan, sum slices
+            bname = f"ss_ws_zero + {bname} + ss_ws_reduce"
         kernel_ms = {}
         for name, fn in ((fname, fwd), (bname, bwd)):
             fn()

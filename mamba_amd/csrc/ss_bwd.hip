@@ -373,15 +373,15 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
 constexpr int kSB = 32;                 // steps per backward super-tile
 constexpr int kQB = kSB / kT;           // chunks per super-tile
 constexpr int kStrB = kSB + 16;         // LDS row stride of stream tiles (floats)
-constexpr int kBCB = kSB + 4;           // LDS row stride of B / C tiles (floats)
-constexpr int kTr2Row = kT * 2 * kT;    // float2 transposition: 16 lanes x 16 steps x 2 (512 floats)
 constexpr int kWgN = kSB + 1;           // padded step stride of the dB / dC wave partials
+constexpr int kBCB = kSB + 4;           // LDS row stride of B / C tiles (floats)
+constexpr int kTrHRow = kT * 16;        // half-chunk (s1, s2) transposition: 16 lanes x 8 steps x 2 (256 floats)
 
 template <typename IT>
 struct Piece2 {                         // 2 consecutive elements of one row
-    using raw = typename std::conditional<sizeof(IT) == 4, uint2, uint32_t>::type;
+    using raw = typename std::conditional<sizeof(IT) == 4, u32x2, uint32_t>::type;
     raw v;
-    __device__ __forceinline__ void load(const IT* p) { v = *reinterpret_cast<const raw*>(p); }
+    __device__ __forceinline__ void load(const SS_GLOBAL IT* p) { v = *(const SS_GLOBAL raw*)p; }
     __device__ __forceinline__ float2 f() const {
         if constexpr (sizeof(IT) == 4) {
             return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
@@ -395,14 +395,14 @@ struct Piece2 {                         // 2 consecutive elements of one row
 };
 
 template <typename IT>
-__device__ __forceinline__ void store2(IT* p, float2 v) {
+__device__ __forceinline__ void store2(SS_GLOBAL IT* p, float2 v) {
     if constexpr (sizeof(IT) == 4) {
-        *reinterpret_cast<float2*>(p) = v;
+        *(SS_GLOBAL f32x2*)p = f32x2{v.x, v.y};
     } else if constexpr (__is_same(IT, bf16_t)) {
-        *reinterpret_cast<uint32_t*>(p) = uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16);
+        *(SS_GLOBAL uint32_t*)p = uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16);
     } else {
-        *reinterpret_cast<uint32_t*>(p) = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) |
-                                          (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16);
+        *(SS_GLOBAL uint32_t*)p = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) |
+                                  (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16);
     }
 }
 
@@ -419,12 +419,14 @@ __device__ __forceinline__ float rows4_sum(float v0, float v1, float v2, float v
 }
 
 template <typename IT, bool kZ>
-__global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
+// 3 workgroups per CU (12 waves): at most 168 VGPRs and 54,272 B of LDS
+// (LDS float atomics would save space but are far slower than this layout).
+__global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // streams u, delta, dout, z, y; the first three hold du, ddelta, dz afterwards
     __shared__ __attribute__((aligned(16))) float s_in[5 * kChPerWG * kStrB];
     __shared__ __attribute__((aligned(16))) float s_B[16 * kBCB];
     __shared__ __attribute__((aligned(16))) float s_C[16 * kBCB];
-    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * kRows * kTr2Row];   // [wave][row][lane][step][2]
+    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * kRows * kTrHRow];   // [wave][row][lane][8 steps][2]
     __shared__ __attribute__((aligned(16))) float s_wg[2 * kWaves * 16 * kWgN];     // [dB, dC][wave][n][t]
     const FwdParams& p = q.f;
 
@@ -456,16 +458,20 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     IT* bdu = static_cast<IT*>(q.du) + b * q.du_bs + c0 * q.du_ds;
     IT* bdd = static_cast<IT*>(q.ddelta) + b * q.dd_bs + c0 * q.dd_ds;
     IT* bdz = kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + c0 * q.dz_ds : bdu;
-    const uint32_t ou = uint32_t(prow * p.u_ds + 2 * pc), od = uint32_t(prow * p.dl_ds + 2 * pc);
-    const uint32_t oo = uint32_t(prow * q.do_ds + 2 * pc);
-    const uint32_t oz = kZ ? uint32_t(prow * p.z_ds + 2 * pc) : ou, oy = kZ ? uint32_t(prow * p.y_ds + 2 * pc) : ou;
-    const uint32_t oB = uint32_t(prow * p.B_ns + 2 * pc), oC = uint32_t(prow * p.C_ns + 2 * pc);
-    const uint32_t odu = uint32_t(prow * q.du_ds + 2 * pc), odd = uint32_t(prow * q.dd_ds + 2 * pc);
-    const uint32_t odz = kZ ? uint32_t(prow * q.dz_ds + 2 * pc) : odu;
+    // per-thread byte offsets (below 2^32, checked by bwd_fast_ok)
+    constexpr uint32_t es = sizeof(IT);
+    const uint32_t ou = uint32_t(prow * p.u_ds + 2 * pc) * es, od = uint32_t(prow * p.dl_ds + 2 * pc) * es;
+    const uint32_t oo = uint32_t(prow * q.do_ds + 2 * pc) * es;
+    const uint32_t oz = kZ ? uint32_t(prow * p.z_ds + 2 * pc) * es : ou;
+    const uint32_t oy = kZ ? uint32_t(prow * p.y_ds + 2 * pc) * es : ou;
+    const uint32_t oB = uint32_t(prow * p.B_ns + 2 * pc) * es, oC = uint32_t(prow * p.C_ns + 2 * pc) * es;
+    const uint32_t odu = uint32_t(prow * q.du_ds + 2 * pc) * es, odd = uint32_t(prow * q.dd_ds + 2 * pc) * es;
+    const uint32_t odz = kZ ? uint32_t(prow * q.dz_ds + 2 * pc) * es : odu;
     const int spos = prow * kStrB + 2 * pc;
     const int bpos = prow * kBCB + 2 * pc;
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
-    const float* gx = p.x + (b * p.n_chunks * p.dim + c) * kT + r;
+    const float* gx = p.x + (b * p.n_chunks * p.dim + c0) * kT;
+    const uint32_t ox = uint32_t(row * kT + r) * 4u;
     const int64_t x_chunk_stride = p.dim * kT;
     // dB / dC of this batch row and group, or of its slice of the workspace
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
@@ -478,10 +484,13 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     const float a2 = av * kLog2e;
     const bool softplus = p.softplus != 0;
 
-    // float2 (s1, s2) transposition of one chunk: lane r writes steps 2m, 2m+1
-    // as a float4 at r * 32 + 4 * (m ^ (r & 7)); element (lane r', step s)
-    // is the float2 at r' * 32 + 4 * ((s >> 1) ^ (r' & 7)) + 2 * (s & 1)
-    float* trw = s_tr + (w * kRows + j) * kTr2Row;
+    // (s1, s2) summed over the row's 16 states, 8 steps (half a chunk) at a
+    // time: lane n stores steps 2m, 2m+1 of the half (m = 0..3) as a float4 at
+    // n * 16 + 4 * (m ^ ((n >> 1) & 3)); lane r then adds states
+    // n = 2 i + (r >> 3) (i = 0..7) of step r & 7, and the other 8 states come
+    // from lane r ^ 8 (DPP row_ror:8).  Both access patterns are free of bank
+    // conflicts.
+    float* trw = s_tr + (w * kRows + j) * kTrHRow;
 
     struct Pieces {
         Piece2<IT> u, d, o, z, y, B, C;
@@ -489,16 +498,16 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
     };
     auto fetch = [&](int64_t st, Pieces& P) {     // st clamped by the caller
         const int64_t t0 = st * kSB;
-        P.u.load(bu + t0 + ou);
-        P.d.load(bd + t0 + od);
-        P.o.load(bo + t0 + oo);
-        if constexpr (kZ) { P.z.load(bz + t0 + oz); P.y.load(by + t0 + oy); }
-        P.B.load(bB + t0 + oB);
-        P.C.load(bC + t0 + oC);
+        P.u.load(goff(gbase(bu + t0), ou));
+        P.d.load(goff(gbase(bd + t0), od));
+        P.o.load(goff(gbase(bo + t0), oo));
+        if constexpr (kZ) { P.z.load(goff(gbase(bz + t0), oz)); P.y.load(goff(gbase(by + t0), oy)); }
+        P.B.load(goff(gbase(bB + t0), oB));
+        P.C.load(goff(gbase(bC + t0), oC));
 #pragma unroll
         for (int qq = 0; qq < kQB; ++qq) {
             const int64_t ck = st * kQB + qq;
-            const float v = gx[(ck > 0 ? ck - 1 : 0) * x_chunk_stride];
+            const float v = *goff(gbase(gx + (ck > 0 ? ck - 1 : 0) * x_chunk_stride), ox);
             P.x[qq] = ck > 0 ? v : 0.f;
         }
     };
@@ -525,10 +534,11 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
             const float* pcc = s_wg + ((1 * kWaves + ww) * 16 + nl) * kWgN + k;
             sB0 += pb[0]; sB1 += pb[1]; sC0 += pcc[0]; sC1 += pcc[1];
         }
-        atomicAdd(dBb + nl * L + t0 + k, sB0);
-        atomicAdd(dBb + nl * L + t0 + k + 1, sB1);
-        atomicAdd(dCb + nl * L + t0 + k, sC0);
-        atomicAdd(dCb + nl * L + t0 + k + 1, sC1);
+        const uint32_t o = uint32_t(nl * L + k) * 4u;
+        gatomic_add(goff(gbase(dBb + t0), o), sB0);
+        gatomic_add(goff(gbase(dBb + t0 + 1), o), sB1);
+        gatomic_add(goff(gbase(dCb + t0), o), sC0);
+        gatomic_add(goff(gbase(dCb + t0 + 1), o), sC1);
     };
 
     float gcar = 0.f, acar = 1.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
@@ -583,8 +593,10 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
                 });
             });
 
-            // ---- adjoint, last step first, four steps at a time
+            // ---- adjoint, last step first, four steps at a time; s1r / s2r get
+            // this lane's step r of the sums over states
             float gv = gcar, anext = acar;
+            float s1r = 0.f, s2r = 0.f;
             static_for<4>([&](auto KG) {
                 constexpr int kg = 3 - decltype(KG)::value;
                 const float4 vb = *reinterpret_cast<const float4*>(sBr + 4 * kg);
@@ -608,10 +620,10 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
                     dCp[ki] = dyk * hs[k];
                     anext = as[k];
                 });
-                // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1)
-                *reinterpret_cast<float4*>(trw + r * 32 + 4 * ((2 * kg) ^ (r & 7))) =
+                // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
+                *reinterpret_cast<float4*>(trw + r * 16 + 4 * ((2 * (kg & 1)) ^ ((r >> 1) & 3))) =
                     make_float4(s1p[0], s2p[0], s1p[1], s2p[1]);
-                *reinterpret_cast<float4*>(trw + r * 32 + 4 * ((2 * kg + 1) ^ (r & 7))) =
+                *reinterpret_cast<float4*>(trw + r * 16 + 4 * ((2 * (kg & 1) + 1) ^ ((r >> 1) & 3))) =
                     make_float4(s1p[2], s2p[2], s1p[3], s2p[3]);
                 // dB / dC of steps 4kg..4kg+3 summed over the wave's rows:
                 // row j holds step 4kg + j
@@ -619,24 +631,27 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
                 const float dCs = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
                 s_wg[((0 * kWaves + w) * 16 + r) * kWgN + kT * qi + 4 * kg + j] = dBs;
                 s_wg[((1 * kWaves + w) * 16 + r) * kWgN + kT * qi + 4 * kg + j] = dCs;
+                if constexpr ((kg & 1) == 0) {   // half kg / 2 is complete: sum it
+                    constexpr int h = kg >> 1;
+                    const int e = r & 1, m = (r & 7) >> 1, nh = r >> 3;
+                    float2 v[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int n = 2 * i + nh;
+                        v[i] = *reinterpret_cast<const float2*>(trw + n * 16 + 4 * (m ^ ((n >> 1) & 3)) + 2 * e);
+                    }
+#pragma unroll
+                    for (int wdt = 4; wdt >= 1; wdt >>= 1)
+#pragma unroll
+                        for (int i = 0; i < wdt; ++i) { v[i].x += v[i + wdt].x; v[i].y += v[i + wdt].y; }
+                    const float t1 = v[0].x + row_ror8(v[0].x);
+                    const float t2 = v[0].y + row_ror8(v[0].y);
+                    if (nh == h) { s1r = t1; s2r = t2; }
+                }
             });
             gcar = gv;
             acar = anext;
 
-            // transposed sums over states: this lane's step r
-            float s1r = 0.f, s2r = 0.f;
-            {
-                float2 v[kT];
-#pragma unroll
-                for (int rr = 0; rr < kT; ++rr)
-                    v[rr] = *reinterpret_cast<const float2*>(trw + rr * 32 + 4 * ((r >> 1) ^ (rr & 7)) + 2 * (r & 1));
-#pragma unroll
-                for (int wdt = 8; wdt >= 1; wdt >>= 1)
-#pragma unroll
-                    for (int i = 0; i < wdt; ++i) { v[i].x += v[i + wdt].x; v[i].y += v[i + wdt].y; }
-                s1r = v[0].x;
-                s2r = v[0].y;
-            }
 
             // ---- per-step outputs of step t0 + 16 qi + r into the output tiles
             const float du = Dv * dy + dt * s1r;
@@ -652,9 +667,9 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_fast(const BwdParams q) {
         lds_barrier();
         flush_dbc(t0);
         constexpr int T = kChPerWG * kStrB;
-        store2<IT>(bdu + t0 + odu, *reinterpret_cast<const float2*>(s_in + 0 * T + spos));
-        store2<IT>(bdd + t0 + odd, *reinterpret_cast<const float2*>(s_in + 1 * T + spos));
-        if constexpr (kZ) store2<IT>(bdz + t0 + odz, *reinterpret_cast<const float2*>(s_in + 2 * T + spos));
+        store2<IT>(goff(gbase(bdu + t0), odu), *reinterpret_cast<const float2*>(s_in + 0 * T + spos));
+        store2<IT>(goff(gbase(bdd + t0), odd), *reinterpret_cast<const float2*>(s_in + 1 * T + spos));
+        if constexpr (kZ) store2<IT>(goff(gbase(bdz + t0), odz), *reinterpret_cast<const float2*>(s_in + 2 * T + spos));
     }
 
     // ---- per-channel and per-(channel, state) sums over time and batch
@@ -671,7 +686,9 @@ bool bwd_fast_ok(const BwdParams& q) {
     const FwdParams& p = q.f;
     return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kSB && p.seqlen % kSB == 0 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && q.stream_vec_bwd &&
-           (!p.has_z || p.y != nullptr);
+           (!p.has_z || p.y != nullptr) &&
+           small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
+                          q.do_ds, q.du_ds, q.dd_ds, q.dz_ds});
 }
 
 // ------------------------------------------------------- dB / dC slices --

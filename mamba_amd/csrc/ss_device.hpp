@@ -190,8 +190,15 @@ __device__ __forceinline__ void lds_barrier() {
 template <int K>
 __device__ __forceinline__ float row_bcast(float v) {
     static_assert(K >= 0 && K < 16, "row lane");
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                                 0x150 + K, 0xf, 0xf, false));
+    // every lane of the row is written, so no "old" value is needed (mov_dpp
+    // leaves it undefined, which lets the DPP combiner fold the move and
+    // avoids a v_mov 0 per broadcast)
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + K, 0xf, 0xf, true));
+}
+
+// Value of lane r ^ 8 of this lane's 16-lane row (DPP row_ror:8).
+__device__ __forceinline__ float row_ror8(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, true));
 }
 
 // Sum over the 16 lanes of a row, result in every lane of the row.
@@ -274,6 +281,55 @@ __device__ __forceinline__ int64_t xcd_block_id() {
     const uint32_t n = gridDim.x, i = blockIdx.x;
     if (n % kXcds != 0) return i;
     return int64_t(i % kXcds) * (n / kXcds) + i / kXcds;
+}
+
+// Global (address space 1) pointers.  Loads, stores and atomics through them
+// are global_* instructions even where the compiler cannot infer the address
+// space itself; flat_* forms would also count against lgkmcnt, which the
+// LDS-only barrier waits on.
+#define SS_GLOBAL __attribute__((address_space(1)))
+
+// Builtin vector types for global accesses (the HIP vector classes cannot be
+// assigned from address-space-qualified lvalues).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// A workgroup-uniform pointer, as a global pointer pinned to scalar
+// registers.  Loop strength reduction otherwise turns base + t0 + offset
+// into a 64-bit per-lane induction variable, which costs 64-bit adds per
+// access and loses the scalar-base + 32-bit-offset address form.
+template <typename T>
+__device__ __forceinline__ SS_GLOBAL T* gbase(T* p) {
+    SS_GLOBAL T* g = (SS_GLOBAL T*)p;
+#if defined(__HIP_DEVICE_COMPILE__)   // register constraints exist only in the gfx950 pass
+    __asm__("" : "+s"(g));
+#endif
+    return g;
+}
+
+// p advanced by `bytes`, a 32-bit per-lane offset (callers keep it below
+// 2^32: the launchers check the strides that go into it).
+// The empty asm keeps the 32-bit offset next to its use: hoisted out of a
+// loop, its zero-extension to 64 bits would be materialised there, and the
+// access would again be a 64-bit per-lane address.
+template <typename T>
+__device__ __forceinline__ SS_GLOBAL T* goff(SS_GLOBAL T* p, uint32_t bytes) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__("" : "+v"(bytes));
+#endif
+    return (SS_GLOBAL T*)((SS_GLOBAL char*)p + bytes);
+}
+
+// fp32 atomic add to LDS (ds_add_f32, no return value).
+__device__ __forceinline__ void lds_add(float* p, float v) {
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// fp32 atomic add through a global pointer (no return value).
+__device__ __forceinline__ void gatomic_add(SS_GLOBAL float* p, float v) {
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace ss

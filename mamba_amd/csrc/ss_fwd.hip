@@ -209,9 +209,9 @@ constexpr int kBCs = kS + 4;                 // LDS row stride of B / C tiles (f
 
 template <typename IT>
 struct Piece4 {                              // 4 consecutive elements of one row
-    using raw = typename std::conditional<sizeof(IT) == 4, uint4, uint2>::type;
+    using raw = typename std::conditional<sizeof(IT) == 4, u32x4, u32x2>::type;
     raw v;
-    __device__ __forceinline__ void load(const IT* p) { v = *reinterpret_cast<const raw*>(p); }
+    __device__ __forceinline__ void load(const SS_GLOBAL IT* p) { v = *(const SS_GLOBAL raw*)p; }
     __device__ __forceinline__ float4 f() const {
         if constexpr (sizeof(IT) == 4) {
             return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
@@ -228,19 +228,16 @@ struct Piece4 {                              // 4 consecutive elements of one ro
 };
 
 template <typename IT>
-__device__ __forceinline__ void store4(IT* p, float4 v) {
+__device__ __forceinline__ void store4(SS_GLOBAL IT* p, float4 v) {
     if constexpr (sizeof(IT) == 4) {
-        *reinterpret_cast<float4*>(p) = v;
+        *(SS_GLOBAL f32x4*)p = f32x4{v.x, v.y, v.z, v.w};
     } else if constexpr (__is_same(IT, bf16_t)) {
-        uint2 o;
-        o.x = uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16);
-        o.y = uint32_t(io<bf16_t>::round(v.z)) | (uint32_t(io<bf16_t>::round(v.w)) << 16);
-        *reinterpret_cast<uint2*>(p) = o;
+        *(SS_GLOBAL u32x2*)p = u32x2{uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16),
+                                     uint32_t(io<bf16_t>::round(v.z)) | (uint32_t(io<bf16_t>::round(v.w)) << 16)};
     } else {
-        uint2 o;
-        o.x = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16);
-        o.y = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.z))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.w))) << 16);
-        *reinterpret_cast<uint2*>(p) = o;
+        *(SS_GLOBAL u32x2*)p =
+            u32x2{uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16),
+                  uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.z))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.w))) << 16)};
     }
 }
 
@@ -273,17 +270,26 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 
     // cooperative piece of this thread: row prow, steps 4 pc .. 4 pc + 3
     const int prow = tid >> 4, pc = tid & 15;
-    const IT* gu = static_cast<const IT*>(p.u) + b * p.u_bs + (c0 + prow) * p.u_ds + 4 * pc;
-    const IT* gd = static_cast<const IT*>(p.delta) + b * p.dl_bs + (c0 + prow) * p.dl_ds + 4 * pc;
-    const IT* gz = kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + (c0 + prow) * p.z_ds + 4 * pc : gu;
-    const IT* gB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs + prow * p.B_ns + 4 * pc;
-    const IT* gC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs + prow * p.C_ns + 4 * pc;
-    IT* go = static_cast<IT*>(p.out) + b * p.o_bs + (c0 + prow) * p.o_ds + 4 * pc;
-    IT* gy = kZ ? static_cast<IT*>(p.y) + b * p.y_bs + (c0 + prow) * p.y_ds + 4 * pc : go;
+    // workgroup-uniform row bases plus per-thread byte offsets (below 2^32,
+    // checked by fwd_fast_ok)
+    const IT* gu = static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds;
+    const IT* gd = static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds;
+    const IT* gz = kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : gu;
+    const IT* gB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs;
+    const IT* gC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
+    IT* go = static_cast<IT*>(p.out) + b * p.o_bs + c0 * p.o_ds;
+    IT* gy = kZ ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : go;
+    constexpr uint32_t es = sizeof(IT);
+    const uint32_t ou = uint32_t(prow * p.u_ds + 4 * pc) * es, od = uint32_t(prow * p.dl_ds + 4 * pc) * es;
+    const uint32_t oz = kZ ? uint32_t(prow * p.z_ds + 4 * pc) * es : ou;
+    const uint32_t oB = uint32_t(prow * p.B_ns + 4 * pc) * es, oC = uint32_t(prow * p.C_ns + 4 * pc) * es;
+    const uint32_t oo = uint32_t(prow * p.o_ds + 4 * pc) * es;
+    const uint32_t oy = kZ ? uint32_t(prow * p.y_ds + 4 * pc) * es : oo;
     const int spos = prow * kStrm + 4 * pc;        // this piece in a stream tile
     const int bpos = prow * kBCs + 4 * pc;         // this piece in a B / C tile
     // x: (batch, chunk, dim, dstate); a wave's 4 channels x 16 states are contiguous
-    float* gx = p.x + (b * p.n_chunks * p.dim + c) * kT + r;
+    float* gx = p.x + (b * p.n_chunks * p.dim + c0) * kT;
+    const uint32_t ox = uint32_t(row * kT + r) * 4u;
     const int64_t x_chunk_stride = p.dim * kT;
 
     const float Dv = p.D ? p.D[c] : 0.f;
@@ -293,11 +299,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 
     struct Pieces { Piece4<IT> u, d, z, B, C; };
     auto fetch = [&](int64_t t0, Pieces& P) {   // t0 clamped by the caller
-        P.u.load(gu + t0);
-        P.d.load(gd + t0);
-        if constexpr (kZ) P.z.load(gz + t0);
-        P.B.load(gB + t0);
-        P.C.load(gC + t0);
+        P.u.load(goff(gbase(gu + t0), ou));
+        P.d.load(goff(gbase(gd + t0), od));
+        if constexpr (kZ) P.z.load(goff(gbase(gz + t0), oz));
+        P.B.load(goff(gbase(gB + t0), oB));
+        P.C.load(goff(gbase(gC + t0), oC));
     };
     auto stage = [&](const Pieces& P) {
         *reinterpret_cast<float4*>(s_u + spos) = P.u.f();
@@ -352,7 +358,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                 h = __builtin_fmaf(a[k], h, bb[k]);
                 yp[k] = Ct[k] * h;
             });
-            gx[((t0 + kT * q) / kT) * x_chunk_stride] = h;
+            *goff(gbase(gx + ((t0 + kT * q) / kT) * x_chunk_stride), ox) = h;
             row_transpose_write(wbuf, yp, j, r);
             float y = row_transpose_read(wbuf, j, r) + Dv * uq[q];
             if constexpr (kZ) {
@@ -362,14 +368,15 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             s_u[row * kStrm + kT * q + r] = y;
         }
         lds_barrier();
-        store4<IT>(go + t0, *reinterpret_cast<const float4*>(s_u + spos));
-        if constexpr (kZ) store4<IT>(gy + t0, *reinterpret_cast<const float4*>(s_d + spos));
+        store4<IT>(goff(gbase(go + t0), oo), *reinterpret_cast<const float4*>(s_u + spos));
+        if constexpr (kZ) store4<IT>(goff(gbase(gy + t0), oy), *reinterpret_cast<const float4*>(s_d + spos));
     }
 }
 
 bool fwd_fast_ok(const FwdParams& p) {
     return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kS && p.seqlen % kS == 0 &&
-           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && (!p.has_z || p.y != nullptr);
+           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && (!p.has_z || p.y != nullptr) &&
+           small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns});
 }
 
 template <typename IT>

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "../../include/mamba_ss.h"
 
 namespace ss {
@@ -41,6 +43,16 @@ struct BwdParams {
 
 // dB / dC slices the fast backward uses for p (1: add into dB / dC directly)
 int bwd_ws_slices(const BwdParams& p);
+
+// The fast kernels address a workgroup's rows as a uniform base plus a 32-bit
+// per-thread byte offset of at most 16 rows x stride x 4 bytes; strides and
+// seqlen below 2^26 elements keep every such offset below 2^32.
+constexpr int64_t kMaxOffStride = int64_t(1) << 26;
+inline bool small_strides(std::initializer_list<int64_t> strides) {
+    for (int64_t s : strides)
+        if (s >= kMaxOffStride) return false;
+    return true;
+}
 
 // Return hipSuccess or the launch error.
 hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream);

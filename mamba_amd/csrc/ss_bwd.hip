@@ -399,7 +399,7 @@ __device__ __forceinline__ void store2(SS_GLOBAL IT* p, float2 v) {
     if constexpr (sizeof(IT) == 4) {
         *(SS_GLOBAL f32x2*)p = f32x2{v.x, v.y};
     } else if constexpr (__is_same(IT, bf16_t)) {
-        *(SS_GLOBAL uint32_t*)p = uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16);
+        *(SS_GLOBAL uint32_t*)p = io<bf16_t>::pack2(v.x, v.y);
     } else {
         *(SS_GLOBAL uint32_t*)p = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) |
                                   (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16);

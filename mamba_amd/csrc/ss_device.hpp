@@ -45,11 +45,13 @@ template <> struct io<bf16_t> {
     static __device__ __forceinline__ float load(const bf16_t* p) {
         return __uint_as_float(uint32_t(p->bits) << 16);
     }
-    static __device__ __forceinline__ uint16_t round(float v) {
-        uint32_t u = __float_as_uint(v);
-        if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);  // quiet NaN
-        u += 0x7fffu + ((u >> 16) & 1u);                                           // RNE
-        return uint16_t(u >> 16);
+    // round to nearest even (NaN stays NaN): gfx950's v_cvt_pk_bf16_f32
+    static __device__ __forceinline__ uint16_t round(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+    // two values rounded and packed, lo in bits 0-15, by one v_cvt_pk_bf16_f32
+    static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
     }
     static __device__ __forceinline__ void store(bf16_t* p, float v) { p->bits = round(v); }
 };

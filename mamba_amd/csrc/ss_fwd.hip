@@ -232,8 +232,8 @@ __device__ __forceinline__ void store4(SS_GLOBAL IT* p, float4 v) {
     if constexpr (sizeof(IT) == 4) {
         *(SS_GLOBAL f32x4*)p = f32x4{v.x, v.y, v.z, v.w};
     } else if constexpr (__is_same(IT, bf16_t)) {
-        *(SS_GLOBAL u32x2*)p = u32x2{uint32_t(io<bf16_t>::round(v.x)) | (uint32_t(io<bf16_t>::round(v.y)) << 16),
-                                     uint32_t(io<bf16_t>::round(v.z)) | (uint32_t(io<bf16_t>::round(v.w)) << 16)};
+        *(SS_GLOBAL u32x2*)p = u32x2{io<bf16_t>::pack2(v.x, v.y),
+                                     io<bf16_t>::pack2(v.z, v.w)};
     } else {
         *(SS_GLOBAL u32x2*)p =
             u32x2{uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16),

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 2
+#define SS_ABI_VERSION 3
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -159,6 +159,45 @@ int ss_fwd(const ss_fwd_args* a, void* stream);
    ddelta_bias.  Replaces selective_scan.backward / backward_kernel_launch
    (selective_scan.cpp:246-329, backward_kernel.cu:588-618). */
 int ss_bwd(const ss_bwd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Causal depthwise conv1d (+ SiLU), the step before the scan in the Mamba
+ * block.  Replaces nn.Conv1d(dim, dim, width, groups=dim, padding=width - 1)
+ * cut to the first seqlen outputs, and the SiLU after it
+ * (modules/mamba_simple.py:40-47,100-101):
+ *   out[b, d, t] = act(bias[d] + sum_k weight[d, k] * x[b, d, t - (width - 1) + k])
+ * with x = 0 before t = 0 and act = SiLU or identity.
+ * x, out, dout, dx: (batch, dim, seqlen), seqlen stride 1, element type
+ * itype; weight: fp32 (dim, width) with free strides; bias: fp32 (dim).
+ * ------------------------------------------------------------------------ */
+typedef struct ss_conv1d_args {
+    int64_t batch, dim, seqlen, width;   /* width 1..4 */
+    int32_t itype;                       /* enum ss_dtype */
+    int32_t has_bias, silu;
+    int32_t pad_;
+    int64_t x_batch_stride, x_dim_stride;
+    int64_t out_batch_stride, out_dim_stride;
+    int64_t w_dim_stride, w_width_stride;
+    const void* x;
+    const float* weight;
+    const float* bias;                   /* may be NULL iff !has_bias */
+    void* out;                           /* ignored by ss_conv1d_bwd */
+} ss_conv1d_args;
+
+typedef struct ss_conv1d_bwd_args {
+    ss_conv1d_args f;                    /* as for the forward (f.out ignored) */
+    int64_t dout_batch_stride, dout_dim_stride;
+    int64_t dx_batch_stride, dx_dim_stride;
+    const void* dout;                    /* gradient of out (after the activation) */
+    void* dx;                            /* overwritten, itype */
+    float* dweight;                      /* accumulated into, fp32 (dim, width) contiguous */
+    float* dbias;                        /* accumulated into, fp32 (dim); may be NULL iff !has_bias */
+} ss_conv1d_bwd_args;
+
+/* Forward: writes out.  Backward: writes dx, accumulates dweight / dbias;
+   recomputes the pre-activation from x, weight and bias. */
+int ss_conv1d_fwd(const ss_conv1d_args* a, void* stream);
+int ss_conv1d_bwd(const ss_conv1d_bwd_args* a, void* stream);
 
 #ifdef __cplusplus
 }

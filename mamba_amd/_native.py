@@ -13,13 +13,13 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
     "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_bwd_workspace_bytes",
     "ss_fwd_kernel_name", "ss_bwd_kernel_name",
-    "ss_fwd", "ss_bwd",
+    "ss_fwd", "ss_bwd", "ss_conv1d_fwd", "ss_conv1d_bwd",
 )
 
 _i64, _i32, _p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
@@ -57,6 +57,26 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
+class Conv1dArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("dim", _i64), ("seqlen", _i64), ("width", _i64),
+        ("itype", _i32), ("has_bias", _i32), ("silu", _i32), ("pad_", _i32),
+        ("x_batch_stride", _i64), ("x_dim_stride", _i64),
+        ("out_batch_stride", _i64), ("out_dim_stride", _i64),
+        ("w_dim_stride", _i64), ("w_width_stride", _i64),
+        ("x", _p), ("weight", _p), ("bias", _p), ("out", _p),
+    ]
+
+
+class Conv1dBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("f", Conv1dArgs),
+        ("dout_batch_stride", _i64), ("dout_dim_stride", _i64),
+        ("dx_batch_stride", _i64), ("dx_dim_stride", _i64),
+        ("dout", _p), ("dx", _p), ("dweight", _p), ("dbias", _p),
+    ]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -88,6 +108,10 @@ def load():
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(T)]
             fn.restype = ctypes.c_char_p
+        lib.ss_conv1d_fwd.argtypes = [ctypes.POINTER(Conv1dArgs), _p]
+        lib.ss_conv1d_fwd.restype = ctypes.c_int
+        lib.ss_conv1d_bwd.argtypes = [ctypes.POINTER(Conv1dBwdArgs), _p]
+        lib.ss_conv1d_bwd.restype = ctypes.c_int
         lib.ss_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
         lib.ss_bwd_workspace_bytes.restype = _i64
         lib.ss_fwd.argtypes = [ctypes.POINTER(FwdArgs), _p]

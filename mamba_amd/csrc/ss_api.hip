@@ -214,6 +214,32 @@ int64_t ws_bytes_for(const ss::BwdParams& p, int* slices) {
     return int64_t(2) * *slices * stride * int64_t(sizeof(float));
 }
 
+int check_conv(const ss_conv1d_args* a, bool* empty) {
+    if (!a) return fail(SS_ERR_INVALID, "null argument block");
+    if (a->batch < 0 || a->dim < 0 || a->seqlen < 0)
+        return fail(SS_ERR_INVALID, "negative size (batch=%lld dim=%lld seqlen=%lld)",
+                    (long long)a->batch, (long long)a->dim, (long long)a->seqlen);
+    if (a->width < 1 || a->width > 4) return fail(SS_ERR_UNSUPPORTED, "width=%lld outside [1, 4]", (long long)a->width);
+    if (a->itype != SS_F32 && a->itype != SS_BF16 && a->itype != SS_F16)
+        return fail(SS_ERR_INVALID, "unknown itype %d", a->itype);
+    if (a->batch > 0 && a->dim > INT32_MAX / a->batch)
+        return fail(SS_ERR_UNSUPPORTED, "batch * dim = %lld rows is too many", (long long)(a->batch * a->dim));
+    if ((a->seqlen + 1023) / 1024 > 65535)
+        return fail(SS_ERR_UNSUPPORTED, "seqlen=%lld is too long", (long long)a->seqlen);
+    *empty = a->batch == 0 || a->dim == 0 || a->seqlen == 0;
+    if (*empty) return SS_OK;
+    const size_t es = elem_size(a->itype);
+    if (!a->x) return fail(SS_ERR_INVALID, "x is NULL");
+    if (!a->weight) return fail(SS_ERR_INVALID, "weight is NULL");
+    if (a->has_bias && !a->bias) return fail(SS_ERR_INVALID, "bias is NULL");
+    if (!aligned(a->x, es)) return fail(SS_ERR_INVALID, "x is misaligned");
+    if (!aligned(a->weight, 4) || (a->bias && !aligned(a->bias, 4))) return fail(SS_ERR_INVALID, "weight / bias is misaligned");
+    const int64_t st[] = {a->x_batch_stride, a->x_dim_stride, a->w_dim_stride, a->w_width_stride};
+    for (int64_t v : st)
+        if (v < 0) return fail(SS_ERR_INVALID, "negative stride");
+    return SS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -296,6 +322,39 @@ int ss_bwd(const ss_bwd_args* a, void* stream) {
     }
     hipError_t e = ss::launch_bwd(p, a->f.itype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int ss_conv1d_fwd(const ss_conv1d_args* a, void* stream) {
+    bool empty = false;
+    int rc = check_conv(a, &empty);
+    if (rc != SS_OK) return rc;
+    if (empty) return ok();
+    if (!a->out) return fail(SS_ERR_INVALID, "out is NULL");
+    if (!aligned(a->out, elem_size(a->itype))) return fail(SS_ERR_INVALID, "out is misaligned");
+    if (a->out_batch_stride < 0 || a->out_dim_stride < 0) return fail(SS_ERR_INVALID, "negative stride");
+    hipError_t e = ss::conv1d_launch(a, nullptr, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "conv1d forward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int ss_conv1d_bwd(const ss_conv1d_bwd_args* g, void* stream) {
+    if (!g) return fail(SS_ERR_INVALID, "null argument block");
+    bool empty = false;
+    int rc = check_conv(&g->f, &empty);
+    if (rc != SS_OK) return rc;
+    if (empty) return ok();
+    const size_t es = elem_size(g->f.itype);
+    if (!g->dout || !g->dx) return fail(SS_ERR_INVALID, "%s is NULL", g->dout ? "dx" : "dout");
+    if (!g->dweight) return fail(SS_ERR_INVALID, "dweight is NULL");
+    if (g->f.has_bias && !g->dbias) return fail(SS_ERR_INVALID, "dbias is NULL");
+    if (!aligned(g->dout, es) || !aligned(g->dx, es)) return fail(SS_ERR_INVALID, "dout / dx is misaligned");
+    if (!aligned(g->dweight, 4) || (g->dbias && !aligned(g->dbias, 4)))
+        return fail(SS_ERR_INVALID, "dweight / dbias is misaligned");
+    if (g->dout_batch_stride < 0 || g->dout_dim_stride < 0 || g->dx_batch_stride < 0 || g->dx_dim_stride < 0)
+        return fail(SS_ERR_INVALID, "negative stride");
+    hipError_t e = ss::conv1d_launch(&g->f, g, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "conv1d backward launch failed: %s", hipGetErrorString(e));
     return ok();
 }
 

@@ -57,6 +57,8 @@ inline bool small_strides(std::initializer_list<int64_t> strides) {
 // Return hipSuccess or the launch error.
 hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int itype, hipStream_t stream);
+// causal depthwise conv1d (+ SiLU); g == nullptr: forward, else backward
+hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, hipStream_t stream);
 // base name of the kernel template launch_fwd / launch_bwd picks for p
 const char* fwd_kernel_name(const FwdParams& p);
 const char* bwd_kernel_name(const BwdParams& p);

@@ -1,0 +1,117 @@
+"""MambaSimple with the reference's constructor, parameters and forward.
+
+The module mirrors modules/mamba_simple.py:8-149: the same constructor
+arguments, parameter names and shapes (input_proj, short_conv,
+ssm_param_proj, delta_proj, log_A, D, output_proj) and the same
+initialisation, so the reference's state_dict loads unchanged.  Two
+forward paths compute the same function:
+
+* ``use_fast_path=True`` (default): in-projection as one GEMM straight into
+  the channel-major xz layout, then ``mamba_inner_fn`` (HIP conv1d + SiLU,
+  projections, HIP selective scan with the z gate fused, out-projection);
+* ``use_fast_path=False``: the reference's own sequence of PyTorch ops
+  around ``SelectiveScanFn`` (modules/mamba_simple.py:95-149), with the scan
+  on the HIP library.
+"""
+import math
+
+import torch
+import torch.nn as nn
+
+from ..ops.selective_scan_interface import SelectiveScanFn, mamba_inner_fn
+
+
+class MambaSimple(nn.Module):
+    def __init__(
+        self,
+        model_dim: int,
+        state_dim: int = 16,
+        conv_kernel: int = 4,
+        expansion_factor: int = 2,
+        delta_rank="auto",
+        delta_min: float = 0.001,
+        delta_max: float = 0.1,
+        delta_init: str = "random",
+        delta_scale: float = 1.0,
+        delta_init_floor: float = 1e-4,
+        conv_bias: bool = False,
+        bias: bool = False,
+        device=None,
+        dtype=None,
+        use_fast_path: bool = True,
+    ):
+        super().__init__()
+        fk = {"device": device, "dtype": dtype}
+        self.model_dim = model_dim
+        self.state_dim = state_dim
+        self.conv_kernel = conv_kernel
+        self.expansion_factor = expansion_factor
+        self.inner_dim = int(expansion_factor * model_dim)
+        self.delta_rank = math.ceil(model_dim / 16) if delta_rank == "auto" else delta_rank
+        self.use_fast_path = use_fast_path
+
+        self.input_proj = nn.Linear(self.model_dim, self.inner_dim * 2, bias=bias, **fk)
+        self.short_conv = nn.Conv1d(self.inner_dim, self.inner_dim, kernel_size=conv_kernel,
+                                    padding=conv_kernel - 1, groups=self.inner_dim, bias=conv_bias, **fk)
+        self.act = nn.SiLU()
+        self.ssm_param_proj = nn.Linear(self.inner_dim, self.delta_rank + self.state_dim * 2, bias=False, **fk)
+        self.delta_proj = nn.Linear(self.delta_rank, self.inner_dim, bias=True, **fk)
+
+        # initialisation of modules/mamba_simple.py:61-85
+        delta_std = self.delta_rank ** -0.5 * delta_scale
+        if delta_init == "constant":
+            nn.init.constant_(self.delta_proj.weight, delta_std)
+        elif delta_init == "random":
+            nn.init.uniform_(self.delta_proj.weight, -delta_std, delta_std)
+        else:
+            raise NotImplementedError
+        delta = torch.exp(
+            torch.rand(self.inner_dim, device=device, dtype=torch.float32)
+            * (math.log(delta_max) - math.log(delta_min)) + math.log(delta_min)
+        ).clamp(min=delta_init_floor)
+        inv_delta = delta + torch.log(-torch.expm1(-delta))
+        with torch.no_grad():
+            self.delta_proj.bias.copy_(inv_delta)
+        A = torch.arange(1, state_dim + 1, device=device, dtype=torch.float32)
+        A = A.unsqueeze(0).expand(self.inner_dim, state_dim).contiguous()
+        self.log_A = nn.Parameter(torch.log(A))
+        self.D = nn.Parameter(torch.ones(self.inner_dim, device=device))
+        self.output_proj = nn.Linear(self.inner_dim, model_dim, bias=bias, **fk)
+
+    def forward(self, hidden_states):
+        """(batch, seqlen, model_dim) -> (batch, seqlen, model_dim)."""
+        if self.use_fast_path and hidden_states.is_cuda:
+            return self._forward_fast(hidden_states)
+        return self._forward_reference(hidden_states)
+
+    def _forward_fast(self, hidden_states):
+        batch, seqlen, _ = hidden_states.shape
+        # xz = W_in @ h^T: (2 * inner_dim, batch * seqlen), viewed as (batch, 2 * inner_dim, seqlen)
+        xz = self.input_proj.weight @ hidden_states.reshape(batch * seqlen, self.model_dim).t()
+        if self.input_proj.bias is not None:
+            xz = xz + self.input_proj.bias[:, None]
+        xz = xz.view(2 * self.inner_dim, batch, seqlen).permute(1, 0, 2)
+        A = -torch.exp(self.log_A.float())
+        return mamba_inner_fn(xz, self.short_conv.weight, self.short_conv.bias, self.ssm_param_proj.weight,
+                              self.delta_proj.weight, self.output_proj.weight, self.output_proj.bias, A,
+                              D=self.D.float(), delta_bias=self.delta_proj.bias.float(), delta_softplus=True)
+
+    def _forward_reference(self, hidden_states):
+        # the reference's op sequence (modules/mamba_simple.py:95-149)
+        batch_size, seq_len, _ = hidden_states.shape
+        state_inputs, gate_logits = torch.chunk(
+            self.input_proj(hidden_states).permute(0, 2, 1).contiguous(), chunks=2, dim=1)
+        state_inputs = self.act(self.short_conv(state_inputs)[..., :seq_len])
+        ssm_params = self.ssm_param_proj(
+            state_inputs.permute(0, 2, 1).contiguous().view(batch_size * seq_len, self.inner_dim))
+        delta, B, C = torch.split(ssm_params, [self.delta_rank, self.state_dim, self.state_dim], dim=-1)
+        delta = self.delta_proj.weight @ delta.t()
+        delta = delta.view(self.inner_dim, batch_size, seq_len).permute(1, 0, 2).contiguous()
+        B = B.view(batch_size, seq_len, self.state_dim).permute(0, 2, 1).contiguous().unsqueeze(1)
+        C = C.view(batch_size, seq_len, self.state_dim).permute(0, 2, 1).contiguous().unsqueeze(1)
+        A = -torch.exp(self.log_A.float())
+        state_outputs = SelectiveScanFn.apply(state_inputs, delta, A, B, C, self.D.float(),
+                                              self.delta_proj.bias.float(), True)
+        hidden_states = state_outputs.permute(0, 2, 1).contiguous()
+        hidden_states = hidden_states * self.act(gate_logits.permute(0, 2, 1).contiguous())
+        return self.output_proj(hidden_states)

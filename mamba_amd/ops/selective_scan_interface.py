@@ -137,3 +137,152 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None,
     when ``return_last_state``.
     """
     return SelectiveScanZFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state)
+
+
+# ------------------------------------------------------------ Mamba block --
+def _cm_view(buf, batch, L):
+    """(dim, batch * L) channel-major buffer as a (batch, dim, L) view (unit seqlen stride)."""
+    return buf.view(buf.shape[0], batch, L).permute(1, 0, 2)
+
+
+class MambaInnerFn(torch.autograd.Function):
+    """The Mamba block between in- and out-projection, with the scan fused.
+
+    Same computation as the reference's MambaSimple.forward after its
+    input_proj (modules/mamba_simple.py:98-149), in the mamba_ssm
+    ``mamba_inner_fn`` argument order: causal conv1d + SiLU on the x half of
+    xz, x_proj into (dt, B, C), delta = delta_proj_weight @ dt, the selective
+    scan with the delta bias, softplus and the z gate fused, and the
+    out-projection.
+
+    Every (batch, dim, seqlen) intermediate lives channel-major, as a
+    (dim, batch * seqlen) buffer viewed as (batch, dim, seqlen) with unit
+    seqlen stride: the HIP conv and scan kernels take those strides
+    directly, and every projection (x_proj, delta_proj, out_proj and their
+    gradients) is then one plain GEMM with no layout copies.  B and C are
+    strided views of x_proj's output.  Intermediates are kept for the
+    backward (no recomputation: HBM capacity is not the constraint here).
+    """
+
+    @staticmethod
+    def forward(ctx, xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                out_proj_weight, out_proj_bias, A, B=None, C=None, D=None, delta_bias=None,
+                B_proj_bias=None, C_proj_bias=None, delta_softplus=True):
+        from .causal_conv1d import causal_conv1d_fwd
+        if B is not None or C is not None:
+            raise ValueError("mamba_inner_fn: B and C must come from x_proj (pass B=None, C=None)")
+        if xz.shape[-1] > 1 and xz.stride(-1) != 1:
+            xz = xz.contiguous()
+        batch, two_d, L = xz.shape
+        dim = two_d // 2
+        R = delta_proj_weight.shape[1]
+        N = A.shape[-1]
+        dt, dev = xz.dtype, xz.device
+        BL = batch * L
+        x, z = xz[:, :dim], xz[:, dim:]
+
+        conv_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+        conv_out = _cm_view(conv_buf, batch, L)
+        causal_conv1d_fwd(x, conv1d_weight, conv1d_bias, silu=True, out=conv_out)
+        x_dblT = x_proj_weight.to(dt) @ conv_buf                          # (R + 2N, b l)
+        if B_proj_bias is not None:
+            x_dblT[R:R + N] += B_proj_bias.to(dt)[:, None]
+        if C_proj_bias is not None:
+            x_dblT[R + N:] += C_proj_bias.to(dt)[:, None]
+        delta_buf = delta_proj_weight.to(dt) @ x_dblT[:R]                # (dim, b l)
+        delta = _cm_view(delta_buf, batch, L)
+        Bv = _cm_view(x_dblT[R:R + N], batch, L).unsqueeze(1)           # (batch, 1, N, L)
+        Cv = _cm_view(x_dblT[R + N:R + 2 * N], batch, L).unsqueeze(1)
+        A32 = A.float().contiguous()
+        D32 = D.float().contiguous() if D is not None else None
+        db32 = delta_bias.float().contiguous() if delta_bias is not None else None
+
+        out_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+        y_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+        xck = torch.empty((batch, selective_scan.n_chunks(L), dim, N), dtype=torch.float32, device=dev)
+        selective_scan.forward_into(conv_out, delta, A32, Bv, Cv, D32, db32, delta_softplus,
+                                    _cm_view(out_buf, batch, L), xck, z=z, y=_cm_view(y_buf, batch, L))
+        out_w = out_proj_weight.to(dt)
+        res = torch.nn.functional.linear(out_buf.t(), out_w,
+                                         out_proj_bias.to(dt) if out_proj_bias is not None else None)
+        ctx.save_for_backward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+                              conv_buf, x_dblT, delta_buf, A32, D32, db32, xck, y_buf, out_buf,
+                              A, D, delta_bias, out_proj_bias, B_proj_bias, C_proj_bias)
+        ctx.delta_softplus = delta_softplus
+        ctx.dims = (batch, dim, L, R, N)
+        return res.view(batch, L, -1)
+
+    @staticmethod
+    def backward(ctx, dres):
+        from .causal_conv1d import causal_conv1d_bwd
+        (xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+         conv_buf, x_dblT, delta_buf, A32, D32, db32, xck, y_buf, out_buf,
+         A, D, delta_bias, out_proj_bias, B_proj_bias, C_proj_bias) = ctx.saved_tensors
+        batch, dim, L, R, N = ctx.dims
+        dt, dev = xz.dtype, xz.device
+        BL = batch * L
+        dres2 = dres.reshape(BL, -1).to(dt)
+        if not dres2.is_contiguous():
+            dres2 = dres2.contiguous()
+        out_w = out_proj_weight.to(dt)
+
+        # out-projection
+        dout_buf = out_w.t() @ dres2.t()                                 # (dim, b l)
+        dout_proj_weight = dres2.t() @ out_buf.t()                       # (out, dim)
+        dout_proj_bias = dres2.sum(0) if out_proj_bias is not None else None
+
+        # scan (writes du / ddelta channel-major, dz into the z half of dxz)
+        dxz = torch.empty_like(xz)
+        dconv_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+        ddelta_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+        Bv = _cm_view(x_dblT[R:R + N], batch, L).unsqueeze(1)
+        Cv = _cm_view(x_dblT[R + N:R + 2 * N], batch, L).unsqueeze(1)
+        dA = torch.zeros(A32.shape, dtype=torch.float32, device=dev)
+        dB = torch.zeros((batch, 1, N, L), dtype=torch.float32, device=dev)
+        dC = torch.zeros((batch, 1, N, L), dtype=torch.float32, device=dev)
+        dD = torch.zeros(D32.shape, dtype=torch.float32, device=dev) if D32 is not None else None
+        ddb = torch.zeros(db32.shape, dtype=torch.float32, device=dev) if db32 is not None else None
+        selective_scan.backward_into(_cm_view(conv_buf, batch, L), _cm_view(delta_buf, batch, L), A32, Bv, Cv,
+                                     D32, db32, _cm_view(dout_buf, batch, L), xck, ctx.delta_softplus,
+                                     _cm_view(dconv_buf, batch, L), _cm_view(ddelta_buf, batch, L),
+                                     dA, dB, dC, dD, ddb, z=xz[:, dim:], y=_cm_view(y_buf, batch, L),
+                                     dz=dxz[:, dim:])
+
+        # x_proj / delta_proj
+        dx_dblT = torch.empty(R + 2 * N, BL, dtype=dt, device=dev)
+        dx_dblT[R:R + N].view(N, batch, L).copy_(dB[:, 0].permute(1, 0, 2))
+        dx_dblT[R + N:].view(N, batch, L).copy_(dC[:, 0].permute(1, 0, 2))
+        ddelta_proj_weight = ddelta_buf @ x_dblT[:R].t()                 # (dim, R)
+        torch.matmul(delta_proj_weight.to(dt).t(), ddelta_buf, out=dx_dblT[:R])
+        dx_proj_weight = dx_dblT @ conv_buf.t()                          # (R + 2N, dim)
+        dconv_buf.addmm_(x_proj_weight.to(dt).t(), dx_dblT)
+        dB_proj_bias = dx_dblT[R:R + N].sum(1) if B_proj_bias is not None else None
+        dC_proj_bias = dx_dblT[R + N:].sum(1) if C_proj_bias is not None else None
+
+        # conv1d + SiLU (dx into the x half of dxz)
+        _, dconv_w, dconv_b = causal_conv1d_bwd(xz[:, :dim], conv1d_weight, conv1d_bias,
+                                                _cm_view(dconv_buf, batch, L), silu=True, dx=dxz[:, :dim])
+
+        def like(g, ref):
+            return None if g is None or ref is None else g.reshape(ref.shape).to(ref.dtype)
+        return (dxz, like(dconv_w, conv1d_weight), like(dconv_b, conv1d_bias), like(dx_proj_weight, x_proj_weight),
+                like(ddelta_proj_weight, delta_proj_weight), like(dout_proj_weight, out_proj_weight),
+                like(dout_proj_bias, out_proj_bias), like(dA, A), None, None, like(dD, D),
+                like(ddb, delta_bias), like(dB_proj_bias, B_proj_bias), like(dC_proj_bias, C_proj_bias), None)
+
+
+def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                   out_proj_weight, out_proj_bias, A, B=None, C=None, D=None, delta_bias=None,
+                   B_proj_bias=None, C_proj_bias=None, delta_softplus=True):
+    """Mamba block (conv, projections, scan with z gate) on the HIP kernels.
+
+    xz: (batch, 2 * dim, seqlen) with unit seqlen stride (the channel-major
+    output of the in-projection, viewed as (batch, 2 * dim, seqlen), is used
+    without a copy); conv1d_weight: (dim, 1, width) or (dim, width);
+    x_proj_weight: (dt_rank + 2 * dstate, dim); delta_proj_weight:
+    (dim, dt_rank); out_proj_weight: (out_features, dim); A: (dim, dstate).
+    Returns (batch, seqlen, out_features).
+    """
+    return MambaInnerFn.apply(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                              out_proj_weight, out_proj_bias, A, B, C, D, delta_bias, B_proj_bias,
+                              C_proj_bias, delta_softplus)

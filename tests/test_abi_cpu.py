@@ -59,7 +59,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 2
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 3
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -79,8 +79,10 @@ int main(void) {
 
 
 def test_struct_layout_matches_c_compiler(nat, lib, tmp_path):
-    fields = [f"F(ss_fwd_args, {n})" for n, _ in nat.FwdArgs._fields_]
-    fields += [f"F(ss_bwd_args, {n})" for n, _ in nat.BwdArgs._fields_]
+    structs = ((nat.FwdArgs, "ss_fwd_args"), (nat.BwdArgs, "ss_bwd_args"),
+               (nat.Conv1dArgs, "ss_conv1d_args"), (nat.Conv1dBwdArgs, "ss_conv1d_bwd_args"))
+    fields = [f"F({name}, {n})" for T, name in structs for n, _ in T._fields_]
+    fields += [f'printf("sizeof {name} %zu\\n", sizeof({name}));' for _, name in structs]
     src = tmp_path / "probe.c"
     src.write_text(C_PROBE.replace("FIELDS", "\n    ".join(fields)))
     exe = tmp_path / "probe"
@@ -90,7 +92,8 @@ def test_struct_layout_matches_c_compiler(nat, lib, tmp_path):
     got = {tuple(l.split()[:2]): int(l.split()[2]) for l in lines}
     assert got[("sizeof", "ss_fwd_args")] == ctypes.sizeof(nat.FwdArgs)
     assert got[("sizeof", "ss_bwd_args")] == ctypes.sizeof(nat.BwdArgs)
-    for T, name in ((nat.FwdArgs, "ss_fwd_args"), (nat.BwdArgs, "ss_bwd_args")):
+    for T, name in structs:
+        assert got[("sizeof", name)] == ctypes.sizeof(T), name
         for n, _ in T._fields_:
             assert got[(name, n)] == getattr(T, n).offset, f"{name}.{n}"
     fs, bs = ctypes.c_int64(), ctypes.c_int64()

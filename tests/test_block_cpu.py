@@ -1,0 +1,129 @@
+"""CPU checks of the Mamba-block oracle and the module mirrors (no GPU).
+
+* causal_conv1d_ref against torch's conv1d configured as the reference
+  configures it (nn.Conv1d(dim, dim, width, groups=dim, padding=width - 1),
+  output cut to seqlen: modules/mamba_simple.py:40-47,100);
+* mamba_simple_ref (the oracle of the whole block, from a parameter dict)
+  against the reference's own op sequence (modules/mamba_simple.py:95-149)
+  run on real nn.Linear / nn.Conv1d modules with the scan oracle in place of
+  SelectiveScanFn;
+* causal_lm_ref against the same op sequence stacked as models/causal_lm.py
+  stacks it;
+* the module mirrors carry the reference's state_dict keys and shapes.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from mamba_amd.models import CausalLM, CausalLMConfig
+from mamba_amd.modules import MambaSimple, RMSNorm
+from oracle.mamba_block_ref import causal_conv1d_ref, causal_lm_ref, mamba_simple_ref, rms_norm_ref
+from oracle.selective_scan_ref import selective_scan_ref
+
+F64 = torch.float64
+
+
+@pytest.mark.parametrize("width", [1, 2, 3, 4])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_conv_oracle_matches_torch_conv1d(width, bias, act):
+    g = torch.Generator().manual_seed(width)
+    dim, L = 6, 23
+    x = torch.randn(3, dim, L, generator=g, dtype=F64)
+    conv = torch.nn.Conv1d(dim, dim, width, padding=width - 1, groups=dim, bias=bias).double()
+    want = conv(x)[..., :L]
+    if act:
+        want = F.silu(want)
+    got = causal_conv1d_ref(x, conv.weight, conv.bias, activation=act)
+    assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def _reference_forward(m, hidden):
+    """modules/mamba_simple.py:95-149 on module m, scan oracle for SelectiveScanFn."""
+    batch_size, seq_len, _ = hidden.shape
+    state_inputs, gate_logits = torch.chunk(m.input_proj(hidden).permute(0, 2, 1).contiguous(), chunks=2, dim=1)
+    state_inputs = m.act(m.short_conv(state_inputs)[..., :seq_len])
+    ssm_params = m.ssm_param_proj(state_inputs.permute(0, 2, 1).contiguous().view(batch_size * seq_len, m.inner_dim))
+    delta, B, C = torch.split(ssm_params, [m.delta_rank, m.state_dim, m.state_dim], dim=-1)
+    delta = m.delta_proj.weight @ delta.t()
+    delta = delta.view(m.inner_dim, batch_size, seq_len).permute(1, 0, 2).contiguous()
+    B = B.view(batch_size, seq_len, m.state_dim).permute(0, 2, 1).contiguous().unsqueeze(1)
+    C = C.view(batch_size, seq_len, m.state_dim).permute(0, 2, 1).contiguous().unsqueeze(1)
+    A = -torch.exp(m.log_A.double())
+    y = selective_scan_ref(state_inputs, delta, A, B, C, m.D.double(), delta_bias=m.delta_proj.bias.double(),
+                           delta_softplus=True, compute_dtype=F64)
+    h = y.permute(0, 2, 1).contiguous() * m.act(gate_logits.permute(0, 2, 1).contiguous())
+    return m.output_proj(h)
+
+
+@pytest.mark.parametrize("bias,conv_bias", [(False, False), (True, True)])
+def test_block_oracle_matches_reference_op_sequence(bias, conv_bias):
+    torch.manual_seed(0)
+    m = MambaSimple(model_dim=16, state_dim=4, conv_kernel=4, expansion_factor=2, bias=bias,
+                    conv_bias=conv_bias).double()
+    hidden = torch.randn(2, 11, 16, dtype=F64)
+    want = _reference_forward(m, hidden)
+    got = mamba_simple_ref({k: v for k, v in m.state_dict().items()}, hidden, state_dim=4)
+    assert torch.allclose(got, want, rtol=1e-10, atol=1e-12)
+
+
+def test_causal_lm_oracle_matches_reference_structure():
+    torch.manual_seed(1)
+    cfg = CausalLMConfig(vocab_size=37, model_dim=16, state_dim=4, num_layers=2)
+    model = CausalLM(cfg).double().eval()
+    ids = torch.randint(0, cfg.vocab_size, (2, 9))
+    with torch.no_grad():
+        h = model.embedding(ids)
+        for blk in model.layers:
+            h = h + _reference_forward(blk.mamba, rms_norm_ref(h, blk.norm.weight))
+        want = model.lm_head(rms_norm_ref(h, model.norm.weight))
+        got = causal_lm_ref(model.state_dict(), ids, num_layers=2, state_dim=4)
+    assert torch.allclose(got, want, rtol=1e-10, atol=1e-12)
+
+
+def test_rms_norm_module_matches_oracle():
+    torch.manual_seed(2)
+    n = RMSNorm(24)
+    with torch.no_grad():
+        n.weight.uniform_(-0.5, 0.5)
+    x = torch.randn(3, 5, 24)
+    assert torch.allclose(n(x), rms_norm_ref(x, n.weight), rtol=1e-6, atol=1e-6)
+    # closed form: a constant row c normalises to sign(c) * (1 + w) when eps is negligible
+    x = torch.full((1, 1, 24), -3.0)
+    assert torch.allclose(n(x)[0, 0], -(1 + n.weight.detach()), rtol=1e-5, atol=1e-5)
+
+
+def test_state_dict_keys_are_the_references():
+    # parameter names and shapes of models/causal_lm.py:21-51 and modules/mamba_simple.py:35-85
+    cfg = CausalLMConfig(vocab_size=50, model_dim=24, state_dim=16, conv_kernel=4, num_layers=2)
+    sd = CausalLM(cfg).state_dict()
+    inner, rank = 48, 2          # expansion 2; delta rank ceil(24 / 16)
+    want = {"embedding.weight": (50, 24), "norm.weight": (24,), "lm_head.weight": (50, 24)}
+    for i in range(2):
+        p = f"layers.{i}."
+        want.update({
+            p + "norm.weight": (24,),
+            p + "mamba.input_proj.weight": (2 * inner, 24),
+            p + "mamba.short_conv.weight": (inner, 1, 4),
+            p + "mamba.ssm_param_proj.weight": (rank + 32, inner),
+            p + "mamba.delta_proj.weight": (inner, rank),
+            p + "mamba.delta_proj.bias": (inner,),
+            p + "mamba.log_A": (inner, 16),
+            p + "mamba.D": (inner,),
+            p + "mamba.output_proj.weight": (24, inner),
+        })
+    assert {k: tuple(v.shape) for k, v in sd.items()} == want
+    m = CausalLM(cfg)
+    assert m.lm_head.weight is m.embedding.weight
+
+
+def test_initialisation_matches_reference_rules():
+    torch.manual_seed(3)
+    m = MambaSimple(model_dim=32, state_dim=16)
+    A = torch.exp(m.log_A.detach())
+    assert torch.allclose(A, torch.arange(1, 17, dtype=torch.float32).expand(64, 16))
+    assert torch.all(m.D.detach() == 1)
+    dt = F.softplus(m.delta_proj.bias.detach())          # inverse softplus of dt in [1e-3, 1e-1]
+    assert float(dt.min()) >= 1e-3 * 0.999 and float(dt.max()) <= 1e-1 * 1.001
+    bound = m.delta_rank ** -0.5
+    assert float(m.delta_proj.weight.detach().abs().max()) <= bound

@@ -187,7 +187,7 @@ def main():
 
         def bwd():
             ss.backward_into(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
-                             z=z, y=y, dz=dz)
+                             z=z, y=y, dz=dz, zero_grads=True)
 
         tname = {torch.float32: "float", torch.bfloat16: "bf16", torch.float16: "half"}[dtype]
         fname = ss.forward_kernel_name(u, dl, A, B, C, D, bias, True, out, xck, z=z, y=y)
@@ -196,8 +196,8 @@ def main():
         ws = ss.workspace_bytes(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
                                 z=z, y=y, dz=dz)
         fname, bname = f"{fname}<{tname}, z>", f"{bname}<{tname}, z>"
-        if ws > 0:   # the backward is three launches: clear slices, scan, sum slices
-            bname = f"ss_ws_zero + {bname} + ss_ws_reduce"
+        if ws > 0:   # the backward is three launches: clear slices and accumulators, scan, sum slices
+            bname = f"ss_zero_segs + {bname} + ss_ws_reduce"
         kernel_ms = {}
         for name, fn in ((fname, fwd), (bname, bwd)):
             fn()

@@ -12,8 +12,8 @@
  *  - plain C: POD argument structs, raw device pointers, 64-bit sizes and
  *    element strides; no torch types and no C++ exceptions cross the ABI;
  *  - the library never allocates: the caller passes every output, the
- *    checkpoint buffer x and zero-initialised gradient accumulators
- *    (dA, dB, dC, dD, ddelta_bias are accumulated into);
+ *    checkpoint buffer x and the gradient accumulators (dA, dB, dC, dD,
+ *    ddelta_bias are accumulated into, or cleared first with zero_grads);
  *  - errors are returned as status codes, with a message in
  *    ss_last_error() (the reference has no argument checks at all);
  *  - an optional fused z gate (out = y * silu(z)) and bf16/fp16 I/O, which
@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 3
+#define SS_ABI_VERSION 4
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -98,7 +98,7 @@ typedef struct ss_bwd_args {
     void* du;                /* overwritten, itype */
     void* ddelta;            /* overwritten, itype */
     void* dz;                /* overwritten, itype; may be NULL iff !has_z */
-    float* dA;               /* accumulated into, (dim, dstate) contiguous */
+    float* dA;               /* accumulated into (see zero_grads), (dim, dstate) contiguous */
     float* dB;               /* accumulated into, fp32, shape of B, contiguous */
     float* dC;               /* accumulated into, fp32, shape of C, contiguous */
     float* dD;               /* accumulated into; may be NULL iff !has_D */
@@ -112,6 +112,13 @@ typedef struct ss_bwd_args {
        share a workspace. */
     void* workspace;
     int64_t workspace_bytes;
+    /* nonzero: dA, dB, dC, dD and ddelta_bias are cleared by the call before
+       it accumulates (their contents on entry are ignored), as the
+       reference's backward zero-initialises them (selective_scan.cpp:274-287);
+       the clearing shares a launch with the workspace's.  0: accumulate into
+       what the caller passes. */
+    int32_t zero_grads;
+    int32_t pad_;
 } ss_bwd_args;
 
 /* ABI version (SS_ABI_VERSION of the built library). */
@@ -156,7 +163,7 @@ const char* ss_bwd_kernel_name(const ss_bwd_args* a);
 int ss_fwd(const ss_fwd_args* a, void* stream);
 
 /* Backward scan: writes du, ddelta, dz; accumulates dA, dB, dC, dD,
-   ddelta_bias.  Replaces selective_scan.backward / backward_kernel_launch
+   ddelta_bias (after clearing them when zero_grads is set).  Replaces selective_scan.backward / backward_kernel_launch
    (selective_scan.cpp:246-329, backward_kernel.cu:588-618). */
 int ss_bwd(const ss_bwd_args* a, void* stream);
 

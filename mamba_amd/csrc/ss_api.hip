@@ -199,6 +199,13 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     p.ws = nullptr;
     p.ws_slices = 1;
     p.ws_stride = 0;
+    p.zero_grads = a->zero_grads != 0;
+    const ss_fwd_args& f = a->f;
+    const int64_t G = (f.is_var_B || f.is_var_C) ? f.n_groups : 1;
+    p.dA_n = f.dim * f.dstate;
+    p.dB_n = f.is_var_B ? f.batch * G * f.dstate * f.seqlen : f.dim * f.dstate;
+    p.dC_n = f.is_var_C ? f.batch * G * f.dstate * f.seqlen : f.dim * f.dstate;
+    p.dD_n = f.dim;
     return p;
 }
 
@@ -307,7 +314,23 @@ int ss_bwd(const ss_bwd_args* a, void* stream) {
     bool empty = false;
     int rc = check_bwd(a, &empty);
     if (rc != SS_OK) return rc;
-    if (empty) return ok();
+    if (empty) {
+        // no scan work, but zero_grads still owes zeroed accumulators
+        if (!a->zero_grads) return ok();
+        ss::BwdParams p = make_bwd_params(a);
+        struct G { const float* ptr; int64_t n; const char* name; };
+        const G gs[] = {{a->dA, p.dA_n, "dA"}, {a->dB, p.dB_n, "dB"}, {a->dC, p.dC_n, "dC"},
+                        {a->f.has_D ? a->dD : nullptr, a->f.has_D ? p.dD_n : 0, "dD"},
+                        {a->f.has_delta_bias ? a->ddelta_bias : nullptr, a->f.has_delta_bias ? p.dD_n : 0,
+                         "ddelta_bias"}};
+        for (const G& g : gs) {
+            if (g.n > 0 && !g.ptr) return fail(SS_ERR_INVALID, "%s is NULL", g.name);
+            if (g.ptr && !aligned(g.ptr, 4)) return fail(SS_ERR_INVALID, "%s is misaligned", g.name);
+        }
+        hipError_t e = ss::launch_bwd_zero_only(p, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
+        return ok();
+    }
     ss::BwdParams p = make_bwd_params(a);
     int slices = 1;
     const int64_t need = ws_bytes_for(p, &slices);

@@ -541,7 +541,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         gatomic_add(goff(gbase(dCb + t0 + 1), o), sC1);
     };
 
-    float gcar = 0.f, acar = 1.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
+    float gacar = 0.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
     const int64_t nst = L / kSB;
     Pieces P;
     fetch(nst - 1, P);
@@ -567,10 +567,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         for (int qi = kQB - 1; qi >= 0; --qi) {
             const float uu = in_v[0][qi], pre = in_v[1][qi] + bias, dout = in_v[2][qi];
             const float zz = in_v[3][qi], yv = in_v[4][qi];
-            const float dt = softplus ? softplus20(pre) : pre;
-            const float dtu = dt * uu;
+            float dt = softplus ? softplus20(pre) : pre;
+            float dtu = dt * uu;
             const float sgz = kZ ? sigmoidf_(zz) : 1.f;
-            const float dy = kZ ? dout * zz * sgz : dout;
+            float dy = kZ ? dout * zz * sgz : dout;
+            dpp_sources_ready(dt, dtu, dy);
             const float h0 = h0s[qi];
             const float* sBr = s_B + r * kBCB + kT * qi;
             const float* sCr = s_C + r * kBCB + kT * qi;
@@ -579,6 +580,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             float as[kT], hs[kT];
             static_for<kT>([&](auto K) {
                 constexpr int k = decltype(K)::value;
+                // the compiler's own fused broadcast: it knows the consumer is a
+                // transcendental and needs no wait state after a plain VALU
                 as[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
             });
             float hcur = h0;
@@ -588,14 +591,16 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                 const float bq[4] = {vb.x, vb.y, vb.z, vb.w};
                 static_for<4>([&](auto KI) {
                     constexpr int k = 4 * i + decltype(KI)::value;
-                    hcur = __builtin_fmaf(as[k], hcur, row_bcast<k>(dtu) * bq[k & 3]);
+                    hcur = __builtin_fmaf(as[k], hcur, bmul<k>(dtu, bq[k & 3]));
                     hs[k] = hcur;
                 });
             });
 
             // ---- adjoint, last step first, four steps at a time; s1r / s2r get
-            // this lane's step r of the sums over states
-            float gv = gcar, anext = acar;
+            // this lane's step r of the sums over states.  ga carries
+            // g_{t+1} a_{t+1}: it is both the decayed adjoint entering step t
+            // and, times h_{t-1}, the dA / ddelta term of step t + 1.
+            float ga = gacar;
             float s1r = 0.f, s2r = 0.f;
             static_for<4>([&](auto KG) {
                 constexpr int kg = 3 - decltype(KG)::value;
@@ -607,18 +612,18 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                 static_for<4>([&](auto KI) {
                     constexpr int ki = 3 - decltype(KI)::value;
                     constexpr int k = 4 * kg + ki;
-                    const float dyk = row_bcast<k>(dy);
-                    gv = __builtin_fmaf(anext, gv, dyk * cq[ki]);
+                    float gv = ga;
+                    bfmac<k>(gv, dy, cq[ki]);            // g_t = a_{t+1} g_{t+1} + dy_t C_t
+                    ga = gv * as[k];
                     float hprev;
                     if constexpr (k == 0) hprev = h0;
                     else hprev = hs[k - 1];
-                    const float gah = gv * (as[k] * hprev);
-                    dA_acc = __builtin_fmaf(row_bcast<k>(dt), gah, dA_acc);
+                    const float gah = ga * hprev;        // g_t a_t h_{t-1}
+                    bfmac<k>(dA_acc, dt, gah);
                     s2p[ki] = av * gah;
                     s1p[ki] = gv * bq[ki];
-                    dBp[ki] = gv * row_bcast<k>(dtu);
-                    dCp[ki] = dyk * hs[k];
-                    anext = as[k];
+                    dBp[ki] = bmul<k>(dtu, gv);
+                    dCp[ki] = bmul<k>(dy, hs[k]);
                 });
                 // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
                 *reinterpret_cast<float4*>(trw + r * 16 + 4 * ((2 * (kg & 1)) ^ ((r >> 1) & 3))) =
@@ -649,8 +654,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                     if (nh == h) { s1r = t1; s2r = t2; }
                 }
             });
-            gcar = gv;
-            acar = anext;
+            gacar = ga;
 
 
             // ---- per-step outputs of step t0 + 16 qi + r into the output tiles
@@ -692,20 +696,42 @@ bool bwd_fast_ok(const BwdParams& q) {
 }
 
 // ------------------------------------------------------- dB / dC slices --
-// Clears the workspace (a fill kernel rather than a memset, so the sequence
-// can be captured in a graph).
-__global__ __launch_bounds__(256) void ss_ws_zero(float4* __restrict__ ws, int64_t n4) {
+// Clears up to kZeroSegs float arrays in one launch: the workspace slices
+// and, when the caller asks for it, the gradient accumulators.  A fill
+// kernel rather than memsets, so the whole backward can be captured in a
+// graph.
+struct ZeroSegs {
+    float* p[kZeroSegs];
+    int64_t n[kZeroSegs];
+    int count;
+};
+
+__global__ __launch_bounds__(256) void ss_zero_segs(const ZeroSegs z) {
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride)
-        ws[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (int s = 0; s < z.count; ++s) {
+        float* p = z.p[s];
+        const int64_t n = z.n[s];
+        int64_t head = 0;
+        if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+            const int64_t n4 = n >> 2;
+            float4* p4 = reinterpret_cast<float4*>(p);
+            for (int64_t i = tid; i < n4; i += stride) p4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            head = 4 * n4;
+        }
+        for (int64_t i = head + tid; i < n; i += stride) p[i] = 0.f;
+    }
 }
 
-// dB += sum of the dB slices, dC += sum of the dC slices (n4 float4 each).
+// dB (+)= sum of the dB slices, dC (+)= sum of the dC slices (n4 float4
+// each); `overwrite` ignores what dB / dC held.
 __global__ __launch_bounds__(256) void ss_ws_reduce(const float4* __restrict__ ws, int slices, int64_t n4,
-                                                    float4* __restrict__ dB, float4* __restrict__ dC) {
+                                                    float4* __restrict__ dB, float4* __restrict__ dC,
+                                                    int overwrite) {
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        float4 sb = dB[i], sc = dC[i];
+        float4 sb = overwrite ? make_float4(0.f, 0.f, 0.f, 0.f) : dB[i];
+        float4 sc = overwrite ? make_float4(0.f, 0.f, 0.f, 0.f) : dC[i];
         for (int k = 0; k < slices; ++k) {
             const float4 vb = ws[(2 * k) * n4 + i], vc = ws[(2 * k + 1) * n4 + i];
             sb.x += vb.x; sb.y += vb.y; sb.z += vb.z; sb.w += vb.w;
@@ -715,6 +741,37 @@ __global__ __launch_bounds__(256) void ss_ws_reduce(const float4* __restrict__ w
         dC[i] = sc;
     }
 }
+
+// Launches the clearing pass for p: workspace slices, and with zero_grads
+// the accumulators (dB / dC only when no slice sum overwrites them).
+static hipError_t launch_zero(const BwdParams& p, bool sliced, hipStream_t stream) {
+    ZeroSegs z{};
+    int64_t most = 0;
+    auto add = [&](float* ptr, int64_t n) {
+        if (!ptr || n <= 0) return;
+        z.p[z.count] = ptr;
+        z.n[z.count] = n;
+        ++z.count;
+        most = n > most ? n : most;
+    };
+    if (sliced) add(p.ws, 2 * p.ws_slices * p.ws_stride);
+    if (p.zero_grads) {
+        add(p.dA, p.dA_n);
+        add(p.dD, p.dD_n);
+        add(p.ddelta_bias, p.dD_n);
+        if (!sliced) {
+            add(p.dB, p.dB_n);
+            add(p.dC, p.dC_n);
+        }
+    }
+    if (z.count == 0) return hipSuccess;
+    const int64_t blocks = (most / 4 + 255) / 256;
+    const unsigned grid = unsigned(blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks));
+    hipLaunchKernelGGL(ss_zero_segs, dim3(grid), dim3(256), 0, stream, z);
+    return hipGetLastError();
+}
+
+hipError_t launch_bwd_zero_only(const BwdParams& p, hipStream_t stream) { return launch_zero(p, false, stream); }
 
 int bwd_ws_slices(const BwdParams& p) {
     if (!bwd_fast_ok(p)) return 1;
@@ -732,19 +789,20 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     const dim3 block(kThreads);
     const int spl = int((p.f.dstate + 15) / 16);
     const bool vbc = p.f.var_B && p.f.var_C;
-    if (bwd_fast_ok(p)) {
-        const int64_t n4 = p.ws ? p.ws_stride / 4 : 0;
+    const bool fast = bwd_fast_ok(p);
+    const bool sliced = fast && p.ws != nullptr;
+    hipError_t e = launch_zero(p, sliced, stream);
+    if (e != hipSuccess) return e;
+    if (fast) {
+        const int64_t n4 = sliced ? p.ws_stride / 4 : 0;
         const unsigned rgrid = unsigned(n4 > 0 ? (n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048 : 1);
-        if (p.ws) {
-            hipLaunchKernelGGL(ss_ws_zero, dim3(rgrid), dim3(256), 0, stream,
-                               reinterpret_cast<float4*>(p.ws), 2 * p.ws_slices * n4);
-        }
         if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_bwd_fast<IT, false>), grid, block, 0, stream, p);
-        if (p.ws) {
+        if (sliced) {
             hipLaunchKernelGGL(ss_ws_reduce, dim3(rgrid), dim3(256), 0, stream,
                                reinterpret_cast<const float4*>(p.ws), int(p.ws_slices), n4,
-                               reinterpret_cast<float4*>(p.dB), reinterpret_cast<float4*>(p.dC));
+                               reinterpret_cast<float4*>(p.dB), reinterpret_cast<float4*>(p.dC),
+                               int(p.zero_grads));
         }
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, true>), grid, block, 0, stream, p);

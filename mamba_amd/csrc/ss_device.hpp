@@ -198,6 +198,39 @@ __device__ __forceinline__ float row_bcast(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + K, 0xf, 0xf, true));
 }
 
+// Row broadcasts fused into the consuming instruction, written as inline asm:
+// the compiler folds a row_newbcast move only into a single VOP2 use and
+// never into v_fmac_f32, so a broadcast value used twice, or as the
+// multiplicand of an accumulation, would otherwise cost a v_mov_b32_dpp per
+// lane and step.
+//   bmul<K>(s, y)        = s[lane K of the row] * y        (v_mul_f32_dpp)
+//   bfmac<K>(acc, s, y) : acc += s[lane K of the row] * y  (v_fmac_f32_dpp)
+// Hazards: gfx950 needs two wait states between a VALU write of a VGPR and a
+// DPP read of it, and one between a transcendental result and a VALU that
+// reads it.  The compiler does not look inside inline asm for either, so
+// every broadcast source goes through dpp_sources_ready() after it is
+// computed (the asm's outputs are the only definitions the DPP reads see),
+// and no transcendental result is passed straight into these helpers.  The
+// gfx950 assembly of the library is checked for both rules by the test suite.
+template <int K>
+__device__ __forceinline__ float bmul(float s, float y) {
+    static_assert(K >= 0 && K < 16, "row lane");
+    float r;
+    __asm__("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+            : "=v"(r) : "v"(s), "v"(y), "n"(K));
+    return r;
+}
+template <int K>
+__device__ __forceinline__ void bfmac(float& acc, float s, float y) {
+    static_assert(K >= 0 && K < 16, "row lane");
+    __asm__("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+            : "+v"(acc) : "v"(s), "v"(y), "n"(K));
+}
+// Two wait states after the last write of the broadcast sources a, b, c.
+__device__ __forceinline__ void dpp_sources_ready(float& a, float& b, float& c) {
+    __asm__ volatile("s_nop 1" : "+v"(a), "+v"(b), "+v"(c));
+}
+
 // Value of lane r ^ 8 of this lane's 16-lane row (DPP row_ror:8).
 __device__ __forceinline__ float row_ror8(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, true));

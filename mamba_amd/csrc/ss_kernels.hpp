@@ -39,10 +39,19 @@ struct BwdParams {
     float* ws;
     int32_t ws_slices;
     int64_t ws_stride;
+    // clear dA, dB, dC, dD, ddelta_bias before accumulating (element counts
+    // of each; dB / dC are overwritten by the slice sum when ws is used)
+    int32_t zero_grads;
+    int64_t dA_n, dB_n, dC_n, dD_n;
 };
 
 // dB / dC slices the fast backward uses for p (1: add into dB / dC directly)
 int bwd_ws_slices(const BwdParams& p);
+// arrays one clearing launch handles (workspace + five accumulators)
+constexpr int kZeroSegs = 6;
+// clears the accumulators of p (zero_grads) and nothing else: a call with
+// no scan work (batch or seqlen 0) still returns zeroed gradients
+hipError_t launch_bwd_zero_only(const BwdParams& p, hipStream_t stream);
 
 // The fast kernels address a workgroup's rows as a uniform base plus a 32-bit
 // per-thread byte offset of at most 16 rows x stride x 4 bytes; strides and

@@ -237,16 +237,16 @@ class MambaInnerFn(torch.autograd.Function):
         ddelta_buf = torch.empty(dim, BL, dtype=dt, device=dev)
         Bv = _cm_view(x_dblT[R:R + N], batch, L).unsqueeze(1)
         Cv = _cm_view(x_dblT[R + N:R + 2 * N], batch, L).unsqueeze(1)
-        dA = torch.zeros(A32.shape, dtype=torch.float32, device=dev)
-        dB = torch.zeros((batch, 1, N, L), dtype=torch.float32, device=dev)
-        dC = torch.zeros((batch, 1, N, L), dtype=torch.float32, device=dev)
-        dD = torch.zeros(D32.shape, dtype=torch.float32, device=dev) if D32 is not None else None
-        ddb = torch.zeros(db32.shape, dtype=torch.float32, device=dev) if db32 is not None else None
+        dA = torch.empty(A32.shape, dtype=torch.float32, device=dev)
+        dB = torch.empty((batch, 1, N, L), dtype=torch.float32, device=dev)
+        dC = torch.empty((batch, 1, N, L), dtype=torch.float32, device=dev)
+        dD = torch.empty(D32.shape, dtype=torch.float32, device=dev) if D32 is not None else None
+        ddb = torch.empty(db32.shape, dtype=torch.float32, device=dev) if db32 is not None else None
         selective_scan.backward_into(_cm_view(conv_buf, batch, L), _cm_view(delta_buf, batch, L), A32, Bv, Cv,
                                      D32, db32, _cm_view(dout_buf, batch, L), xck, ctx.delta_softplus,
                                      _cm_view(dconv_buf, batch, L), _cm_view(ddelta_buf, batch, L),
                                      dA, dB, dC, dD, ddb, z=xz[:, dim:], y=_cm_view(y_buf, batch, L),
-                                     dz=dxz[:, dim:])
+                                     dz=dxz[:, dim:], zero_grads=True)
 
         # x_proj / delta_proj
         dx_dblT = torch.empty(R + 2 * N, BL, dtype=dt, device=dev)

@@ -214,10 +214,12 @@ def workspace_bytes(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplu
 
 
 def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
-                  du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None, workspace="auto"):
+                  du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None, workspace="auto",
+                  zero_grads=False):
     """Backward into caller-allocated gradients.  du, ddelta (and dz) are
     overwritten; dA, dB, dC, dD, ddelta_bias are fp32 and accumulated into,
-    so pass zeros for plain gradients.
+    or, with ``zero_grads``, cleared by the library first (their contents on
+    entry are ignored, so ``torch.empty`` buffers will do).
 
     ``workspace``: "auto" allocates the scratch the library asks for (see
     ``workspace_bytes``) from torch's caching allocator; a uint8 / any CUDA
@@ -237,6 +239,7 @@ def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                  "workspace must be a contiguous tensor on the inputs' device")
         b.workspace = _ptr(workspace)
         b.workspace_bytes = workspace.numel() * workspace.element_size()
+    b.zero_grads = int(bool(zero_grads))
     with torch.cuda.device(u.device):
         nat.check(lib.ss_bwd(ctypes.byref(b), _stream(u.device)), "selective_scan.backward")
 
@@ -262,15 +265,17 @@ def backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus, *, z
     """
     du = torch.empty_like(u, memory_format=torch.contiguous_format)
     ddelta = torch.empty_like(delta, memory_format=torch.contiguous_format)
-    dA = torch.zeros(A.shape, dtype=torch.float32, device=A.device)
-    dB = torch.zeros(B.shape, dtype=torch.float32, device=B.device)
-    dC = torch.zeros(C.shape, dtype=torch.float32, device=C.device)
-    dD = torch.zeros(D.shape, dtype=torch.float32, device=D.device) if D is not None else None
-    ddelta_bias = (torch.zeros(delta_bias.shape, dtype=torch.float32, device=delta_bias.device)
+    # the accumulators are cleared by the library in the launch that clears
+    # its workspace (zero_grads), not by separate torch fills
+    dA = torch.empty(A.shape, dtype=torch.float32, device=A.device)
+    dB = torch.empty(B.shape, dtype=torch.float32, device=B.device)
+    dC = torch.empty(C.shape, dtype=torch.float32, device=C.device)
+    dD = torch.empty(D.shape, dtype=torch.float32, device=D.device) if D is not None else None
+    ddelta_bias = (torch.empty(delta_bias.shape, dtype=torch.float32, device=delta_bias.device)
                    if delta_bias is not None else None)
     dz = torch.empty_like(z, memory_format=torch.contiguous_format) if z is not None else None
     backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
-                  du, ddelta, dA, dB, dC, dD, ddelta_bias, z=z, y=y, dz=dz)
+                  du, ddelta, dA, dB, dC, dD, ddelta_bias, z=z, y=y, dz=dz, zero_grads=True)
     res = [du, ddelta, dA, dB, dC, dD, ddelta_bias]
     if z is not None:
         res.append(dz)

@@ -175,3 +175,56 @@ def test_backward_with_and_without_workspace():
         res[mode] = [v.cpu() for v in g] + [dz.cpu()]
     for a, b_, name in zip(res["auto"], res[None], ("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz")):
         assert_close(a, b_, 1e-5, 1e-5, name)
+
+
+@pytest.mark.parametrize("mode", ["auto", None])
+def test_zero_grads_clears_and_plain_call_accumulates(mode):
+    """zero_grads ignores what the accumulators hold (NaN here); without it the
+    call adds into them (the reference's backward zero-initialises them,
+    selective_scan.cpp:274-287; this boundary lets the caller choose)."""
+    from mamba_amd import selective_scan as ss
+    print(f"\n[parity] zero_grads workspace={mode} b2-d512-n16-l128 fp32", flush=True)
+    dev = torch.device("cuda:0")
+    x = make_inputs(2, 512, 16, 128, seed=23)
+    t = {k: x[k].to(dev) for k in NAMES}
+    dout = x["dout"].to(dev)
+    out, xck, y = ss.forward(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], True, z=t["z"])
+    acc_names = ("A", "B", "C", "D", "delta_bias")
+
+    def run(fill, zero_grads):
+        g = [torch.empty_like(t["u"]), torch.empty_like(t["delta"])] + \
+            [torch.full(t[k].shape, fill, dtype=torch.float32, device=dev) for k in acc_names]
+        dz = torch.empty_like(t["z"])
+        ss.backward_into(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], dout, xck, True,
+                         *g, z=t["z"], y=y, dz=dz, workspace=mode, zero_grads=zero_grads)
+        torch.cuda.synchronize()
+        return [v.cpu() for v in g]
+
+    ref = run(0.0, False)
+    cleared = run(float("nan"), True)
+    added = run(1.0, False)
+    names = ("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias")
+    for a, b_, name in zip(cleared, ref, names):
+        assert torch.isfinite(a).all(), name
+        assert_close(a, b_, 1e-5, 1e-5, name)
+    for i, name in enumerate(names):
+        want = ref[i] + 1.0 if i >= 2 else ref[i]
+        assert_close(added[i], want, 1e-5, 1e-5, name)
+
+
+def test_zero_grads_with_empty_batch():
+    """batch 0: no scan work, but zero_grads still returns zeroed dA / dD / ddelta_bias."""
+    from mamba_amd import selective_scan as ss
+    print("\n[parity] zero_grads with batch 0", flush=True)
+    dev = torch.device("cuda:0")
+    x = make_inputs(1, 32, 16, 64, seed=24)
+    t = {k: x[k].to(dev) for k in NAMES}
+    e = {k: t[k][:0] for k in ("u", "delta", "z", "B", "C")}
+    xck = torch.empty((0, ss.n_chunks(64), 32, 16), dtype=torch.float32, device=dev)
+    y = torch.empty_like(e["u"])
+    res = ss.backward(e["u"], e["delta"], t["A"], e["B"], e["C"], t["D"], t["delta_bias"], torch.empty_like(e["u"]),
+                      xck, True, z=e["z"], y=y)
+    torch.cuda.synchronize()
+    for i, shape in ((2, (32, 16)), (5, (32,)), (6, (32,))):
+        assert tuple(res[i].shape) == shape
+        assert (res[i].cpu() == 0).all()

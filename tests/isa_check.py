@@ -1,0 +1,141 @@
+"""Static checks over the gfx950 disassembly of libmamba_ss.so.
+
+The scan kernels issue some DPP row broadcasts as inline asm (bmul / bfmac
+in ss_device.hpp), where the compiler's hazard recognizer does not look.
+These checks re-derive, from the disassembled code object, the rules such
+asm must keep:
+
+* DPP source wait states: a VALU write of a VGPR followed by a DPP
+  instruction that reads it as src0 needs at least 2 wait states between
+  them (each issued instruction counts as one, s_nop N as N + 1);
+* transcendental forwarding: the result of v_exp / v_log / v_rcp / v_rsq /
+  v_sqrt / v_sin / v_cos read by a non-transcendental VALU needs at least
+  1 wait state;
+* no packed fp32 VALU ops (v_pk_fma_f32, v_pk_mul_f32, v_pk_add_f32): the
+  library is built with them disabled.
+
+The scan is linear over each function's instruction stream, the order the
+compiler laid out; a branch instruction counts as one wait state like any
+other.  Only the library's own build is disassembled.
+"""
+import os
+import re
+import shutil
+import subprocess
+
+LLVM_BIN = "/opt/rocm/llvm/bin"
+TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
+TRANS = re.compile(r"^v_(exp|log|rcp|rsq|sqrt|sin|cos)_")
+PACKED_F32 = re.compile(r"^v_pk_(fma|mul|add)_f32")
+
+
+def tools_available():
+    return all(os.path.exists(os.path.join(LLVM_BIN, t))
+               for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump"))
+
+
+MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+
+def disassemble(lib_path, workdir):
+    """gfx950 disassembly (text) of the device code embedded in lib_path:
+    the .hip_fatbin section holds one offload bundle per source file."""
+    fat = os.path.join(workdir, "fatbin.bin")
+    subprocess.run([os.path.join(LLVM_BIN, "llvm-objcopy"), f"--dump-section=.hip_fatbin={fat}", lib_path,
+                    os.path.join(workdir, "stripped.so")], check=True, capture_output=True)
+    data = open(fat, "rb").read()
+    starts, i = [], data.find(MAGIC)
+    while i >= 0:
+        starts.append(i)
+        i = data.find(MAGIC, i + len(MAGIC))
+    texts = []
+    for k, st in enumerate(starts):
+        end = starts[k + 1] if k + 1 < len(starts) else len(data)
+        part = os.path.join(workdir, f"bundle{k}.bin")
+        co = os.path.join(workdir, f"co{k}.o")
+        with open(part, "wb") as f:
+            f.write(data[st:end])
+        subprocess.run([os.path.join(LLVM_BIN, "clang-offload-bundler"), "--unbundle", "--type=o",
+                        f"--input={part}", f"--targets={TARGET}", f"--output={co}"], check=True,
+                       capture_output=True)
+        res = subprocess.run([os.path.join(LLVM_BIN, "llvm-objdump"), "-d", "--mcpu=gfx950", co],
+                             check=True, capture_output=True, text=True)
+        texts.append(res.stdout)
+    shutil.rmtree(workdir, ignore_errors=True)
+    return "\n".join(texts)
+
+
+def _vregs(tok):
+    tok = tok.strip()
+    m = re.match(r"^v\[(\d+):(\d+)\]$", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"^v(\d+)$", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def functions(disasm):
+    """{name: [instruction text, ...]} from llvm-objdump output."""
+    out, cur = {}, None
+    for line in disasm.splitlines():
+        m = re.match(r"^[0-9a-f]+ <(\S+)>:", line)
+        if m:
+            cur = out.setdefault(m.group(1), [])
+            continue
+        if cur is None:
+            continue
+        text = line.split("//")[0].strip()
+        if text and not text.endswith(":"):
+            cur.append(text)
+    return out
+
+
+def _split(text):
+    parts = text.split(None, 1)
+    op = parts[0]
+    rest = parts[1] if len(parts) > 1 else ""
+    # operands end where the modifiers (row_*, quad_perm, *_mask, bound_ctrl, offset...) begin
+    ops = []
+    for tok in rest.split(","):
+        tok = tok.strip()
+        head = tok.split()[0] if tok else ""
+        ops.append(head)
+    return op, ops
+
+
+def check_function(name, insns):
+    """List of (kind, message) problems found in one function."""
+    problems = []
+    hist = []           # (op, vgprs written, wait states it provides)
+    for text in insns:
+        op, ops = _split(text)
+        if op == "s_nop":
+            hist.append((op, set(), int(ops[0], 0) + 1))
+            continue
+        if PACKED_F32.match(op):
+            problems.append(("packed-fp32", f"{name}: {text}"))
+        srcs = [_vregs(o) for o in ops[1:]]
+        is_dpp = op.startswith("v_") and ("row_" in text or "quad_perm" in text or "_dpp" in op)
+        if is_dpp and srcs:
+            ws = 0
+            for hop, hdst, hw in reversed(hist):
+                if ws >= 2:
+                    break
+                if hdst & srcs[0] and hop.startswith("v_"):
+                    problems.append(("dpp", f"{name}: '{text}' reads v{sorted(hdst & srcs[0])} "
+                                            f"written by {hop} {ws} wait state(s) before"))
+                    break
+                ws += hw
+        if op.startswith("v_") and not TRANS.match(op):
+            used = set().union(*srcs) if srcs else set()
+            if op.startswith(("v_fmac", "v_mac")) and ops:
+                used |= _vregs(ops[0])
+            if hist:
+                hop, hdst, _ = hist[-1]
+                if TRANS.match(hop) and hdst & used:
+                    problems.append(("trans", f"{name}: '{text}' reads v{sorted(hdst & used)} "
+                                              f"straight after {hop}"))
+        writes_vgpr = op.startswith("v_") and not op.startswith(("v_cmp", "v_readlane", "v_readfirstlane"))
+        hist.append((op, _vregs(ops[0]) if (writes_vgpr and ops) else set(), 1))
+        del hist[:-8]
+    return problems

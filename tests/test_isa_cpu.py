@@ -1,0 +1,60 @@
+"""The built library's gfx950 code keeps the DPP / transcendental wait
+states its inline asm relies on and has no packed fp32 VALU ops (CPU only:
+disassembles the library, runs nothing)."""
+import os
+import tempfile
+
+import pytest
+
+from tests import isa_check
+
+LIB = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "mamba_amd", "_lib",
+                   "libmamba_ss.so")
+
+pytestmark = pytest.mark.skipif(not (os.path.exists(LIB) and isa_check.tools_available()),
+                                reason="library not built or ROCm LLVM tools missing")
+
+
+@pytest.fixture(scope="module")
+def funcs():
+    return isa_check.functions(isa_check.disassemble(LIB, tempfile.mkdtemp()))
+
+
+def test_every_scan_kernel_is_present(funcs):
+    names = " ".join(funcs)
+    for k in ("ss_fwd_fast", "ss_bwd_fast", "ss_fwd_kernel", "ss_bwd_kernel", "ss_zero_segs", "ss_ws_reduce"):
+        assert k in names, k
+
+
+def test_inline_asm_dpp_is_used(funcs):
+    """The fused v_fmac_f32_dpp only comes from the inline asm: its presence
+    shows the check below looks at the code it is meant for."""
+    bwd = [f for f in funcs if "ss_bwd_fast" in f]
+    assert bwd and all(any(i.startswith("v_fmac_f32_dpp") for i in funcs[f]) for f in bwd)
+
+
+def test_no_hazards_and_no_packed_fp32(funcs):
+    problems = []
+    for name, insns in funcs.items():
+        problems += isa_check.check_function(name, insns)
+    assert not problems, "\n".join(f"{k}: {m}" for k, m in problems[:20])
+
+
+def test_checker_catches_planted_hazards():
+    """The checker itself flags a DPP read 1 wait state after the write, a
+    transcendental result read at once, and a packed fp32 op."""
+    bad = ["v_mul_f32_e32 v1, 0x40400000, v1",
+           "s_waitcnt vmcnt(2)",
+           "v_mul_f32_dpp v2, v1, v2 row_newbcast:3 row_mask:0xf bank_mask:0xf",
+           "v_exp_f32_e32 v5, v2",
+           "v_add_f32_e32 v6, v5, v6",
+           "v_pk_fma_f32 v[8:9], v[8:9], v[10:11], v[12:13]"]
+    kinds = sorted(k for k, _ in isa_check.check_function("planted", bad))
+    assert kinds == ["dpp", "packed-fp32", "trans"]
+    good = ["v_mul_f32_e32 v1, 0x40400000, v1",
+            "s_nop 1",
+            "v_mul_f32_dpp v2, v1, v2 row_newbcast:3 row_mask:0xf bank_mask:0xf",
+            "v_exp_f32_e32 v5, v2",
+            "s_nop 0",
+            "v_add_f32_e32 v6, v5, v6"]
+    assert isa_check.check_function("clean", good) == []

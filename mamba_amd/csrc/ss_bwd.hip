@@ -358,53 +358,25 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
 }
 
 // ------------------------------------------------------------ fast path --
-// dstate 16, variable B and C, seqlen a multiple of 32, dim and channels per
+// dstate 16, variable B and C, seqlen a multiple of 16, dim and channels per
 // group multiples of 16, z gate fixed at compile time: no branch around a
-// memory access in the loop (see the forward fast path).  Global traffic is
-// workgroup-cooperative per 32-step super-tile (two checkpoint chunks):
-// every thread moves one 2-element piece of each of u, delta, dout, z, y, B
-// and C, prefetched one super-tile ahead and staged in LDS; du, ddelta and
-// dz go back the same way.  The sums over states (sum_n g B, sum_n A g a h)
-// share one float2 transposition per chunk.  dB / dC are first summed over
-// the wave's 4 channel rows with v_permlane32_swap / v_permlane16_swap, then
-// over the 4 waves in LDS once per super-tile (inside barriers the
-// super-tile needs anyway), and added to global memory once per workgroup,
-// state and step.
-constexpr int kSB = 32;                 // steps per backward super-tile
-constexpr int kQB = kSB / kT;           // chunks per super-tile
-constexpr int kStrB = kSB + 16;         // LDS row stride of stream tiles (floats)
-constexpr int kWgN = kSB + 1;           // padded step stride of the dB / dC wave partials
-constexpr int kBCB = kSB + 4;           // LDS row stride of B / C tiles (floats)
+// memory access in the loop (on gfx950 the compiler waits for every
+// outstanding load at a branch, which would serialise the prefetch).
+//
+// One 16-step chunk per iteration, last chunk first, one barrier per chunk:
+//  - per-step inputs (u, delta, dout, z, y) and the checkpoint come straight
+//    from HBM into the lane that owns the step (a row's 16 lanes read one
+//    64-byte segment), two chunks ahead; du, ddelta, dz go back the same way;
+//  - the B / C tile of the chunk (shared by the workgroup's 16 channels) is
+//    staged through LDS, double-buffered, one chunk ahead;
+//  - sums over states (sum_n g B, sum_n A g a h) use a per-row LDS
+//    transposition with one region per half chunk, so the reads of one half
+//    overlap the arithmetic of the next; A_n is applied inside that sum;
+//  - dB / dC: summed over the wave's 4 rows with v_permlane32_swap /
+//    v_permlane16_swap, over the 4 waves through LDS (double-buffered), and
+//    added to global memory once per workgroup, state and step, one chunk
+//    later (after the next barrier).
 constexpr int kTrHRow = kT * 16;        // half-chunk (s1, s2) transposition: 16 lanes x 8 steps x 2 (256 floats)
-
-template <typename IT>
-struct Piece2 {                         // 2 consecutive elements of one row
-    using raw = typename std::conditional<sizeof(IT) == 4, u32x2, uint32_t>::type;
-    raw v;
-    __device__ __forceinline__ void load(const SS_GLOBAL IT* p) { v = *(const SS_GLOBAL raw*)p; }
-    __device__ __forceinline__ float2 f() const {
-        if constexpr (sizeof(IT) == 4) {
-            return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
-        } else if constexpr (__is_same(IT, bf16_t)) {
-            return make_float2(__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u));
-        } else {
-            return make_float2(float(__builtin_bit_cast(_Float16, uint16_t(v & 0xffffu))),
-                               float(__builtin_bit_cast(_Float16, uint16_t(v >> 16))));
-        }
-    }
-};
-
-template <typename IT>
-__device__ __forceinline__ void store2(SS_GLOBAL IT* p, float2 v) {
-    if constexpr (sizeof(IT) == 4) {
-        *(SS_GLOBAL f32x2*)p = f32x2{v.x, v.y};
-    } else if constexpr (__is_same(IT, bf16_t)) {
-        *(SS_GLOBAL uint32_t*)p = io<bf16_t>::pack2(v.x, v.y);
-    } else {
-        *(SS_GLOBAL uint32_t*)p = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) |
-                                  (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16);
-    }
-}
 
 // Sum of v0..v3 (steps 4kg + 0..3 of one state) over the wave's 4 rows; row
 // j of the result holds the sum for step 4kg + j.
@@ -418,16 +390,22 @@ __device__ __forceinline__ float rows4_sum(float v0, float v1, float v2, float v
     return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
+// B / C tile slot of (state n, step t): 4-step groups XOR-swizzled by state
+// so that 8 lanes reading 4-step groups of states 0..7 (or 8..15) with
+// ds_read_b128 hit 8 distinct groups of 4 banks, and a staging row of 16
+// steps fills one bank half.
+__device__ __forceinline__ int bc_slot(int n, int t) { return n * kT + 4 * ((t >> 2) ^ ((n >> 1) & 3)) + (t & 3); }
+// dB / dC wave-partial slot of (step t, state n): state XOR-swizzled by step,
+// conflict-free both for rows writing (4 steps x 16 states) and for the
+// flush reading (16 steps x 2 states).
+__device__ __forceinline__ int wg_slot(int t, int n) { return t * 16 + (n ^ t); }
+
 template <typename IT, bool kZ>
-// 3 workgroups per CU (12 waves): at most 168 VGPRs and 54,272 B of LDS
-// (LDS float atomics would save space but are far slower than this layout).
+// 3 workgroups per CU (12 waves): at most 168 VGPRs and 54,613 B of LDS.
 __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
-    // streams u, delta, dout, z, y; the first three hold du, ddelta, dz afterwards
-    __shared__ __attribute__((aligned(16))) float s_in[5 * kChPerWG * kStrB];
-    __shared__ __attribute__((aligned(16))) float s_B[16 * kBCB];
-    __shared__ __attribute__((aligned(16))) float s_C[16 * kBCB];
-    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * kRows * kTrHRow];   // [wave][row][lane][8 steps][2]
-    __shared__ __attribute__((aligned(16))) float s_wg[2 * kWaves * 16 * kWgN];     // [dB, dC][wave][n][t]
+    __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kT];              // [buf][B, C][n][t]
+    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * kRows * 2 * kTrHRow]; // [wave][row][half][lane][8 steps][2]
+    __shared__ __attribute__((aligned(16))) float s_wg[2 * 2 * kWaves * kT * 16];     // [buf][dB, dC][wave][t][n]
     const FwdParams& p = q.f;
 
     const int tid = threadIdx.x;
@@ -444,44 +422,41 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const int64_t g = c0 / p.dpg;
     const int64_t L = p.seqlen;
     const int64_t G = p.dim / p.dpg;
+    const int nck = int(L / kT);     // even; below 2^22 (seqlen < 2^26)
 
-    // cooperative piece of this thread: row prow, steps 2 pc, 2 pc + 1.
-    // Workgroup-uniform bases plus 32-bit per-thread offsets.
-    const int prow = tid >> 4, pc = tid & 15;
-    const IT* bu = static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds;
-    const IT* bd = static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds;
-    const IT* bo = static_cast<const IT*>(q.dout) + b * q.do_bs + c0 * q.do_ds;
-    const IT* bz = kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : bu;
-    const IT* by = kZ ? static_cast<const IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : bu;
-    const IT* bB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs;
-    const IT* bC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
-    IT* bdu = static_cast<IT*>(q.du) + b * q.du_bs + c0 * q.du_ds;
-    IT* bdd = static_cast<IT*>(q.ddelta) + b * q.dd_bs + c0 * q.dd_ds;
-    IT* bdz = kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + c0 * q.dz_ds : bdu;
-    // per-thread byte offsets (below 2^32, checked by bwd_fast_ok)
-    constexpr uint32_t es = sizeof(IT);
-    const uint32_t ou = uint32_t(prow * p.u_ds + 2 * pc) * es, od = uint32_t(prow * p.dl_ds + 2 * pc) * es;
-    const uint32_t oo = uint32_t(prow * q.do_ds + 2 * pc) * es;
-    const uint32_t oz = kZ ? uint32_t(prow * p.z_ds + 2 * pc) * es : ou;
-    const uint32_t oy = kZ ? uint32_t(prow * p.y_ds + 2 * pc) * es : ou;
-    const uint32_t oB = uint32_t(prow * p.B_ns + 2 * pc) * es, oC = uint32_t(prow * p.C_ns + 2 * pc) * es;
-    const uint32_t odu = uint32_t(prow * q.du_ds + 2 * pc) * es, odd = uint32_t(prow * q.dd_ds + 2 * pc) * es;
-    const uint32_t odz = kZ ? uint32_t(prow * q.dz_ds + 2 * pc) * es : odu;
-    const int spos = prow * kStrB + 2 * pc;
-    const int bpos = prow * kBCB + 2 * pc;
+    // Buffer resources at the workgroup's rows; lane (row, r) owns step r of
+    // channel c0 + row and, for the B / C staging, step r of state row.  The
+    // chunk advance is the uniform offset.  Offsets stay below 2^32 (checked
+    // by bwd_fast_ok).
+    const rsrc_t Ru = make_rsrc(static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds);
+    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
+    const rsrc_t Ro = make_rsrc(static_cast<const IT*>(q.dout) + b * q.do_bs + c0 * q.do_ds);
+    const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
+    const rsrc_t Ry = make_rsrc(kZ ? static_cast<const IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : nullptr);
+    const rsrc_t RB = make_rsrc(static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs);
+    const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
+    const rsrc_t Rdu = make_rsrc(static_cast<IT*>(q.du) + b * q.du_bs + c0 * q.du_ds);
+    const rsrc_t Rdd = make_rsrc(static_cast<IT*>(q.ddelta) + b * q.dd_bs + c0 * q.dd_ds);
+    const rsrc_t Rdz = make_rsrc(kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + c0 * q.dz_ds : nullptr);
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
-    const float* gx = p.x + (b * p.n_chunks * p.dim + c0) * kT;
-    const uint32_t ox = uint32_t(row * kT + r) * 4u;
-    const int64_t x_chunk_stride = p.dim * kT;
+    const rsrc_t Rx = make_rsrc(p.x + (b * nck * p.dim + c0) * kT);
     // dB / dC of this batch row and group, or of its slice of the workspace
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
-    float* dBb = (q.ws ? q.ws + 2 * slice * q.ws_stride : q.dB) + (b * G + g) * int64_t(kT) * L;
-    float* dCb = (q.ws ? q.ws + (2 * slice + 1) * q.ws_stride : q.dC) + (b * G + g) * int64_t(kT) * L;
+    const rsrc_t RdB = make_rsrc((q.ws ? q.ws + 2 * slice * q.ws_stride : q.dB) + (b * G + g) * int64_t(kT) * L);
+    const rsrc_t RdC = make_rsrc((q.ws ? q.ws + (2 * slice + 1) * q.ws_stride : q.dC) + (b * G + g) * int64_t(kT) * L);
+    constexpr uint32_t es = sizeof(IT);
+    const uint32_t ou = uint32_t(row * p.u_ds + r) * es, od = uint32_t(row * p.dl_ds + r) * es;
+    const uint32_t oo = uint32_t(row * q.do_ds + r) * es;
+    const uint32_t oz = uint32_t(row * p.z_ds + r) * es, oy = uint32_t(row * p.y_ds + r) * es;
+    const uint32_t oB = uint32_t(row * p.B_ns + r) * es, oC = uint32_t(row * p.C_ns + r) * es;
+    const uint32_t odu = uint32_t(row * q.du_ds + r) * es, odd = uint32_t(row * q.dd_ds + r) * es;
+    const uint32_t odz = uint32_t(row * q.dz_ds + r) * es;
+    const uint32_t ox = uint32_t(row * kT + r) * 4u;
+    const uint32_t x_chunk_bytes = uint32_t(p.dim * kT * 4);
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
-    const float av = p.A[c * p.A_ds + r * p.A_ns];
-    const float a2 = av * kLog2e;
+    const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
 
     // (s1, s2) summed over the row's 16 states, 8 steps (half a chunk) at a
@@ -489,192 +464,198 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // n * 16 + 4 * (m ^ ((n >> 1) & 3)); lane r then adds states
     // n = 2 i + (r >> 3) (i = 0..7) of step r & 7, and the other 8 states come
     // from lane r ^ 8 (DPP row_ror:8).  Both access patterns are free of bank
-    // conflicts.
-    float* trw = s_tr + (w * kRows + j) * kTrHRow;
-
-    struct Pieces {
-        Piece2<IT> u, d, o, z, y, B, C;
-        float x[kQB];
-    };
-    auto fetch = [&](int64_t st, Pieces& P) {     // st clamped by the caller
-        const int64_t t0 = st * kSB;
-        P.u.load(goff(gbase(bu + t0), ou));
-        P.d.load(goff(gbase(bd + t0), od));
-        P.o.load(goff(gbase(bo + t0), oo));
-        if constexpr (kZ) { P.z.load(goff(gbase(bz + t0), oz)); P.y.load(goff(gbase(by + t0), oy)); }
-        P.B.load(goff(gbase(bB + t0), oB));
-        P.C.load(goff(gbase(bC + t0), oC));
+    // conflicts.  s2 is summed with the weights A_n of those states.
+    float* trw = s_tr + (w * kRows + j) * 2 * kTrHRow;
+    const int te = r & 1, tm = (r & 7) >> 1, tnh = r >> 3;
+    float Aw[8];
 #pragma unroll
-        for (int qq = 0; qq < kQB; ++qq) {
-            const int64_t ck = st * kQB + qq;
-            const float v = *goff(gbase(gx + (ck > 0 ? ck - 1 : 0) * x_chunk_stride), ox);
-            P.x[qq] = ck > 0 ? v : 0.f;
-        }
-    };
-    auto stage = [&](const Pieces& P) {
-        constexpr int T = kChPerWG * kStrB;
-        *reinterpret_cast<float2*>(s_in + 0 * T + spos) = P.u.f();
-        *reinterpret_cast<float2*>(s_in + 1 * T + spos) = P.d.f();
-        *reinterpret_cast<float2*>(s_in + 2 * T + spos) = P.o.f();
+    for (int i = 0; i < 8; ++i) Aw[i] = p.A[c * p.A_ds + (2 * i + tnh) * p.A_ns];
+
+    struct Chunk { float u, d, o, z, y, B, C, x; };
+    auto fetch = [&](int ck, Chunk& P) {     // 0 <= ck < nck
+        const uint32_t so = uint32_t(ck * kT) * es;
+        P.u = bload<IT>(Ru, ou, so);
+        P.d = bload<IT>(Rd, od, so);
+        P.o = bload<IT>(Ro, oo, so);
         if constexpr (kZ) {
-            *reinterpret_cast<float2*>(s_in + 3 * T + spos) = P.z.f();
-            *reinterpret_cast<float2*>(s_in + 4 * T + spos) = P.y.f();
+            P.z = bload<IT>(Rz, oz, so);
+            P.y = bload<IT>(Ry, oy, so);
+        } else {
+            P.z = 0.f;
+            P.y = 0.f;
         }
-        *reinterpret_cast<float2*>(s_B + bpos) = P.B.f();
-        *reinterpret_cast<float2*>(s_C + bpos) = P.C.f();
+        P.B = bload<IT>(RB, oB, so);
+        P.C = bload<IT>(RC, oC, so);
+        const float v = bload<float>(Rx, ox, uint32_t(ck > 0 ? ck - 1 : 0) * x_chunk_bytes);
+        P.x = ck > 0 ? v : 0.f;
     };
-    // dB / dC of the super-tile at t0: sum the 4 wave partials; thread tid adds
-    // steps 2 (tid & 15), +1 of state tid >> 4
-    auto flush_dbc = [&](int64_t t0) {
-        const int nl = tid >> 4, k = 2 * (tid & 15);
-        float sB0 = 0.f, sB1 = 0.f, sC0 = 0.f, sC1 = 0.f;
+    // this lane's element of the B / C tile (state row, step r) into buffer buf
+    auto stage = [&](const Chunk& P, int buf) {
+        s_bc[(buf * 2 + 0) * 16 * kT + bc_slot(row, r)] = P.B;
+        s_bc[(buf * 2 + 1) * 16 * kT + bc_slot(row, r)] = P.C;
+    };
+    // dB / dC of chunk ck from wave-partial buffer buf: thread (n, t) sums the
+    // 4 waves and adds once into global memory (16 consecutive steps per state)
+    const int fn = tid >> 4, ft = tid & 15;
+    const uint32_t ofl = uint32_t(fn * L + ft) * 4u;
+    auto flush = [&](int ck, int buf) {
+        float sB = 0.f, sC = 0.f;
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) {
-            const float* pb = s_wg + ((0 * kWaves + ww) * 16 + nl) * kWgN + k;
-            const float* pcc = s_wg + ((1 * kWaves + ww) * 16 + nl) * kWgN + k;
-            sB0 += pb[0]; sB1 += pb[1]; sC0 += pcc[0]; sC1 += pcc[1];
+            sB += s_wg[((buf * 2 + 0) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
+            sC += s_wg[((buf * 2 + 1) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
         }
-        const uint32_t o = uint32_t(nl * L + k) * 4u;
-        gatomic_add(goff(gbase(dBb + t0), o), sB0);
-        gatomic_add(goff(gbase(dBb + t0 + 1), o), sB1);
-        gatomic_add(goff(gbase(dCb + t0), o), sC0);
-        gatomic_add(goff(gbase(dCb + t0 + 1), o), sC1);
+        const uint32_t so = uint32_t(ck * kT) * 4u;
+        batomic_add(RdB, ofl, so, sB);
+        batomic_add(RdC, ofl, so, sC);
     };
 
     float gacar = 0.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
-    const int64_t nst = L / kSB;
-    Pieces P;
-    fetch(nst - 1, P);
-    for (int64_t st = nst - 1; st >= 0; --st) {
-        const int64_t t0 = st * kSB;
-        lds_barrier();                 // previous super-tile's outputs and dB / dC partials are consumed
-        stage(P);
-        float h0s[kQB];
-#pragma unroll
-        for (int qq = 0; qq < kQB; ++qq) h0s[qq] = P.x[qq];
-        lds_barrier();
-        fetch(st > 0 ? st - 1 : 0, P);              // prefetch the previous super-tile
 
-        float in_v[5][kQB];
-#pragma unroll
-        for (int a = 0; a < 5; ++a)
-#pragma unroll
-            for (int qq = 0; qq < kQB; ++qq)
-                in_v[a][qq] = (a < 3 || kZ) ? s_in[a * kChPerWG * kStrB + row * kStrB + kT * qq + r] : 0.f;
-        lds_barrier();                 // s_in is reused for the outputs below
+    // One chunk: `cur` holds its inputs (fetched two chunks ago) and is
+    // refilled with chunk ck - 2; `nxt` holds chunk ck - 1, staged at the end.
+    // BUF = ck & 1 is a compile-time constant of each unrolled half, so every
+    // LDS address is an immediate offset.
+    auto chunk = [&](int ck, Chunk& cur_in, const Chunk& nxt, auto BUF) {
+        constexpr int buf = decltype(BUF)::value;
+        lds_barrier();   // B / C tile of ck staged; dB / dC partials of ck + 1 complete
+        const Chunk cur = cur_in;
+        fetch(ck > 1 ? ck - 2 : 0, cur_in);
 
+        // B / C of this lane's state for the 16 steps of the chunk
+        float Bq[kT], Cq[kT];
+        const float* sB = s_bc + (buf * 2 + 0) * 16 * kT;
+        const float* sC = s_bc + (buf * 2 + 1) * 16 * kT;
 #pragma unroll
-        for (int qi = kQB - 1; qi >= 0; --qi) {
-            const float uu = in_v[0][qi], pre = in_v[1][qi] + bias, dout = in_v[2][qi];
-            const float zz = in_v[3][qi], yv = in_v[4][qi];
-            float dt = softplus ? softplus20(pre) : pre;
-            float dtu = dt * uu;
-            const float sgz = kZ ? sigmoidf_(zz) : 1.f;
-            float dy = kZ ? dout * zz * sgz : dout;
-            dpp_sources_ready(dt, dtu, dy);
-            const float h0 = h0s[qi];
-            const float* sBr = s_B + r * kBCB + kT * qi;
-            const float* sCr = s_C + r * kBCB + kT * qi;
-
-            // ---- recompute a_t and h_t of the chunk from the checkpoint
-            float as[kT], hs[kT];
-            static_for<kT>([&](auto K) {
-                constexpr int k = decltype(K)::value;
-                // the compiler's own fused broadcast: it knows the consumer is a
-                // transcendental and needs no wait state after a plain VALU
-                as[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
-            });
-            float hcur = h0;
-            static_for<4>([&](auto I) {
-                constexpr int i = decltype(I)::value;
-                const float4 vb = *reinterpret_cast<const float4*>(sBr + 4 * i);
-                const float bq[4] = {vb.x, vb.y, vb.z, vb.w};
-                static_for<4>([&](auto KI) {
-                    constexpr int k = 4 * i + decltype(KI)::value;
-                    hcur = __builtin_fmaf(as[k], hcur, bmul<k>(dtu, bq[k & 3]));
-                    hs[k] = hcur;
-                });
-            });
-
-            // ---- adjoint, last step first, four steps at a time; s1r / s2r get
-            // this lane's step r of the sums over states.  ga carries
-            // g_{t+1} a_{t+1}: it is both the decayed adjoint entering step t
-            // and, times h_{t-1}, the dA / ddelta term of step t + 1.
-            float ga = gacar;
-            float s1r = 0.f, s2r = 0.f;
-            static_for<4>([&](auto KG) {
-                constexpr int kg = 3 - decltype(KG)::value;
-                const float4 vb = *reinterpret_cast<const float4*>(sBr + 4 * kg);
-                const float4 vc = *reinterpret_cast<const float4*>(sCr + 4 * kg);
-                const float bq[4] = {vb.x, vb.y, vb.z, vb.w};
-                const float cq[4] = {vc.x, vc.y, vc.z, vc.w};
-                float s1p[4], s2p[4], dBp[4], dCp[4];
-                static_for<4>([&](auto KI) {
-                    constexpr int ki = 3 - decltype(KI)::value;
-                    constexpr int k = 4 * kg + ki;
-                    float gv = ga;
-                    bfmac<k>(gv, dy, cq[ki]);            // g_t = a_{t+1} g_{t+1} + dy_t C_t
-                    ga = gv * as[k];
-                    float hprev;
-                    if constexpr (k == 0) hprev = h0;
-                    else hprev = hs[k - 1];
-                    const float gah = ga * hprev;        // g_t a_t h_{t-1}
-                    bfmac<k>(dA_acc, dt, gah);
-                    s2p[ki] = av * gah;
-                    s1p[ki] = gv * bq[ki];
-                    dBp[ki] = bmul<k>(dtu, gv);
-                    dCp[ki] = bmul<k>(dy, hs[k]);
-                });
-                // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
-                *reinterpret_cast<float4*>(trw + r * 16 + 4 * ((2 * (kg & 1)) ^ ((r >> 1) & 3))) =
-                    make_float4(s1p[0], s2p[0], s1p[1], s2p[1]);
-                *reinterpret_cast<float4*>(trw + r * 16 + 4 * ((2 * (kg & 1) + 1) ^ ((r >> 1) & 3))) =
-                    make_float4(s1p[2], s2p[2], s1p[3], s2p[3]);
-                // dB / dC of steps 4kg..4kg+3 summed over the wave's rows:
-                // row j holds step 4kg + j
-                const float dBs = rows4_sum(dBp[0], dBp[1], dBp[2], dBp[3]);
-                const float dCs = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
-                s_wg[((0 * kWaves + w) * 16 + r) * kWgN + kT * qi + 4 * kg + j] = dBs;
-                s_wg[((1 * kWaves + w) * 16 + r) * kWgN + kT * qi + 4 * kg + j] = dCs;
-                if constexpr ((kg & 1) == 0) {   // half kg / 2 is complete: sum it
-                    constexpr int h = kg >> 1;
-                    const int e = r & 1, m = (r & 7) >> 1, nh = r >> 3;
-                    float2 v[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int n = 2 * i + nh;
-                        v[i] = *reinterpret_cast<const float2*>(trw + n * 16 + 4 * (m ^ ((n >> 1) & 3)) + 2 * e);
-                    }
-#pragma unroll
-                    for (int wdt = 4; wdt >= 1; wdt >>= 1)
-#pragma unroll
-                        for (int i = 0; i < wdt; ++i) { v[i].x += v[i + wdt].x; v[i].y += v[i + wdt].y; }
-                    const float t1 = v[0].x + row_ror8(v[0].x);
-                    const float t2 = v[0].y + row_ror8(v[0].y);
-                    if (nh == h) { s1r = t1; s2r = t2; }
-                }
-            });
-            gacar = ga;
-
-
-            // ---- per-step outputs of step t0 + 16 qi + r into the output tiles
-            const float du = Dv * dy + dt * s1r;
-            const float ddt = uu * s1r + s2r;
-            const float dd = softplus ? ddt * sigmoidf_(pre) : ddt;
-            const int opos = row * kStrB + kT * qi + r;
-            s_in[0 * kChPerWG * kStrB + opos] = du;
-            s_in[1 * kChPerWG * kStrB + opos] = dd;
-            if constexpr (kZ) s_in[2 * kChPerWG * kStrB + opos] = dout * yv * sgz * (1.f + zz * (1.f - sgz));
-            dD_acc += dy * uu;
-            db_acc += dd;
+        for (int i = 0; i < 4; ++i) {
+            const float4 vb = *reinterpret_cast<const float4*>(sB + bc_slot(r, 4 * i));
+            const float4 vc = *reinterpret_cast<const float4*>(sC + bc_slot(r, 4 * i));
+            Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
+            Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
         }
-        lds_barrier();
-        flush_dbc(t0);
-        constexpr int T = kChPerWG * kStrB;
-        store2<IT>(goff(gbase(bdu + t0), odu), *reinterpret_cast<const float2*>(s_in + 0 * T + spos));
-        store2<IT>(goff(gbase(bdd + t0), odd), *reinterpret_cast<const float2*>(s_in + 1 * T + spos));
-        if constexpr (kZ) store2<IT>(goff(gbase(bdz + t0), odz), *reinterpret_cast<const float2*>(s_in + 2 * T + spos));
+        flush(ck + 1 < nck ? ck + 1 : nck - 1, buf ^ 1);
+
+        const float uu = cur.u, pre = cur.d + bias, dout = cur.o, zz = cur.z, yv = cur.y, h0 = cur.x;
+        float dt = softplus ? softplus20(pre) : pre;
+        float dtu = dt * uu;
+        const float sgz = kZ ? sigmoidf_(zz) : 1.f;
+        float dy = kZ ? dout * zz * sgz : dout;
+        dpp_sources_ready(dt, dtu, dy);
+
+        // ---- recompute a_t and h_t of the chunk from the checkpoint
+        float as[kT], hs[kT];
+        static_for<kT>([&](auto K) {
+            constexpr int k = decltype(K)::value;
+            // the compiler's own fused broadcast: it knows the consumer is a
+            // transcendental and needs no wait state after a plain VALU
+            as[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
+        });
+        float hcur = h0;
+        static_for<kT>([&](auto K) {
+            constexpr int k = decltype(K)::value;
+            hcur = __builtin_fmaf(as[k], hcur, bmul<k>(dtu, Bq[k]));
+            hs[k] = hcur;
+        });
+
+        // ---- adjoint, last step first, four steps at a time.  ga carries
+        // g_{t+1} a_{t+1}: it is both the decayed adjoint entering step t
+        // and, times h_{t-1}, the dA / ddelta term of step t + 1.
+        float ga = gacar;
+        float2 tv1[8], tv0[8];
+        float* wgB = s_wg + ((buf * 2 + 0) * kWaves + w) * kT * 16;
+        float* wgC = s_wg + ((buf * 2 + 1) * kWaves + w) * kT * 16;
+        static_for<4>([&](auto KG) {
+            constexpr int kg = 3 - decltype(KG)::value;
+            constexpr int hh = kg >> 1;
+            float s1p[4], s2p[4], dBp[4], dCp[4];
+            static_for<4>([&](auto KI) {
+                constexpr int ki = 3 - decltype(KI)::value;
+                constexpr int k = 4 * kg + ki;
+                float gv = ga;
+                bfmac<k>(gv, dy, Cq[k]);             // g_t = a_{t+1} g_{t+1} + dy_t C_t
+                ga = gv * as[k];
+                float hprev;
+                if constexpr (k == 0) hprev = h0;
+                else hprev = hs[k - 1];
+                const float gah = ga * hprev;        // g_t a_t h_{t-1}
+                bfmac<k>(dA_acc, dt, gah);
+                s2p[ki] = gah;                       // times A_n in the sum over states
+                s1p[ki] = gv * Bq[k];
+                dBp[ki] = bmul<k>(dtu, gv);
+                dCp[ki] = bmul<k>(dy, hs[k]);
+            });
+            // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
+            float* trh = trw + hh * kTrHRow;
+            *reinterpret_cast<float4*>(trh + r * 16 + 4 * ((2 * (kg & 1)) ^ ((r >> 1) & 3))) =
+                make_float4(s1p[0], s2p[0], s1p[1], s2p[1]);
+            *reinterpret_cast<float4*>(trh + r * 16 + 4 * ((2 * (kg & 1) + 1) ^ ((r >> 1) & 3))) =
+                make_float4(s1p[2], s2p[2], s1p[3], s2p[3]);
+            // dB / dC of steps 4kg..4kg+3 summed over the wave's rows: row j
+            // holds step 4kg + j
+            wgB[wg_slot(4 * kg + j, r)] = rows4_sum(dBp[0], dBp[1], dBp[2], dBp[3]);
+            wgC[wg_slot(4 * kg + j, r)] = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
+            if constexpr ((kg & 1) == 0) {           // half hh is written: read it back
+                float2 (&tv)[8] = hh ? tv1 : tv0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int n = 2 * i + tnh;
+                    tv[i] = *reinterpret_cast<const float2*>(trh + n * 16 + 4 * (tm ^ ((n >> 1) & 3)) + 2 * te);
+                }
+            }
+        });
+        gacar = ga;
+
+        // sums over states: lane r ends with step r of the chunk
+        auto half_sum = [&](const float2 (&tv)[8], float& t1, float& t2) {
+            const float a0 = tv[0].x + tv[4].x, a1 = tv[1].x + tv[5].x;
+            const float a2_ = tv[2].x + tv[6].x, a3 = tv[3].x + tv[7].x;
+            const float s1 = (a0 + a2_) + (a1 + a3);
+            float e0 = Aw[0] * tv[0].y, e1 = Aw[1] * tv[1].y;
+            e0 = __builtin_fmaf(Aw[2], tv[2].y, e0);
+            e1 = __builtin_fmaf(Aw[3], tv[3].y, e1);
+            e0 = __builtin_fmaf(Aw[4], tv[4].y, e0);
+            e1 = __builtin_fmaf(Aw[5], tv[5].y, e1);
+            e0 = __builtin_fmaf(Aw[6], tv[6].y, e0);
+            e1 = __builtin_fmaf(Aw[7], tv[7].y, e1);
+            const float s2 = e0 + e1;
+            t1 = s1 + row_ror8(s1);
+            t2 = s2 + row_ror8(s2);
+        };
+        float t1a, t2a, t1b, t2b;
+        half_sum(tv1, t1a, t2a);
+        half_sum(tv0, t1b, t2b);
+        const float s1r = tnh ? t1a : t1b;
+        const float s2r = tnh ? t2a : t2b;
+
+        // ---- per-step outputs of step 16 ck + r
+        const float du = Dv * dy + dt * s1r;
+        const float ddt = uu * s1r + s2r;
+        const float dd = softplus ? ddt * sigmoidf_(pre) : ddt;
+        const uint32_t so = uint32_t(ck * kT) * es;
+        bstore<IT>(Rdu, odu, so, du);
+        bstore<IT>(Rdd, odd, so, dd);
+        if constexpr (kZ) bstore<IT>(Rdz, odz, so, dout * yv * sgz * (1.f + zz * (1.f - sgz)));
+        dD_acc += dy * uu;
+        db_acc += dd;
+
+        // B / C tile of the next chunk (ck - 1) into the other buffer
+        stage(nxt, buf ^ 1);
+    };
+
+    // chunks nck - 1, nck - 2 first; two buffers of inputs alternate roles
+    Chunk PA, PB;
+    fetch(nck - 1, PA);
+    fetch(nck - 2, PB);
+    // the first flush (of the nonexistent chunk nck) adds these zeros to chunk nck - 1
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s_wg[i * kThreads + tid] = 0.f;     // buffer nck & 1 = 0
+    stage(PA, 1);
+    for (int ck = nck - 1; ck > 0; ck -= 2) {   // nck is even: ck odd, then even
+        chunk(ck, PA, PB, std::integral_constant<int, 1>{});
+        chunk(ck - 1, PB, PA, std::integral_constant<int, 0>{});
     }
+    lds_barrier();
+    flush(0, 0);
 
     // ---- per-channel and per-(channel, state) sums over time and batch
     dD_acc = row_allsum(dD_acc);
@@ -688,11 +669,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
 
 bool bwd_fast_ok(const BwdParams& q) {
     const FwdParams& p = q.f;
-    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kSB && p.seqlen % kSB == 0 &&
-           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && q.stream_vec_bwd &&
-           (!p.has_z || p.y != nullptr) &&
+    // every byte offset the kernel forms stays below 2^32: rows and seqlen
+    // below 2^26 elements, and the checkpoint offset (chunk x dim x 64 B)
+    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 2 * kT && p.seqlen % (2 * kT) == 0 &&
+           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && (!p.has_z || p.y != nullptr) &&
            small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
-                          q.do_ds, q.du_ds, q.dd_ds, q.dz_ds});
+                          q.do_ds, q.du_ds, q.dd_ds, q.dz_ds}) &&
+           p.seqlen * p.dim < (int64_t(1) << 30);
 }
 
 // ------------------------------------------------------- dB / dC slices --

@@ -357,6 +357,43 @@ __device__ __forceinline__ SS_GLOBAL T* goff(SS_GLOBAL T* p, uint32_t bytes) {
     return (SS_GLOBAL T*)((SS_GLOBAL char*)p + bytes);
 }
 
+// Buffer resources: a workgroup-uniform base held in SGPRs, addressed by a
+// 32-bit per-lane byte offset (VGPR) plus a uniform byte offset (SGPR), so
+// neither the row base nor the chunk advance costs VALU address arithmetic.
+// The range is left unbounded (num_records = 2^32 - 1): the launchers check
+// that every offset a kernel forms stays below 2^32.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;   // gfx9-family raw buffer, 32-bit data format
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, kRsrcWord3);
+}
+// Element (voff + soff bytes) of an IT array as float.
+template <typename T>
+__device__ __forceinline__ float bload(rsrc_t r, uint32_t voff, uint32_t soff) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), 0));
+    } else {
+        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b16(r, int(voff), int(soff), 0);
+        if constexpr (__is_same(T, bf16_t)) return __uint_as_float(v << 16);
+        else return float(__builtin_bit_cast(_Float16, uint16_t(v)));
+    }
+}
+template <typename T>
+__device__ __forceinline__ void bstore(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+    if constexpr (sizeof(T) == 4) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, int(voff), int(soff), 0);
+    } else {
+        uint16_t h;
+        if constexpr (__is_same(T, bf16_t)) h = io<bf16_t>::round(v);
+        else h = __builtin_bit_cast(uint16_t, _Float16(v));
+        __builtin_amdgcn_raw_buffer_store_b16(h, r, int(voff), int(soff), 0);
+    }
+}
+// fp32 atomic add through a buffer resource (no return value).
+__device__ __forceinline__ void batomic_add(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, int(voff), int(soff), 0);
+}
+
 // fp32 atomic add to LDS (ds_add_f32, no return value).
 __device__ __forceinline__ void lds_add(float* p, float v) {
     __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

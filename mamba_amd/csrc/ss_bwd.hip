@@ -377,6 +377,7 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
 //    added to global memory once per workgroup, state and step, one chunk
 //    later (after the next barrier).
 constexpr int kTrHRow = kT * 16;        // half-chunk (s1, s2) transposition: 16 lanes x 8 steps x 2 (256 floats)
+constexpr int kTrRowB = kTrHRow + 32;   // per-row region, padded so rows j, j + 1 use different 64-bank halves
 
 // Sum of v0..v3 (steps 4kg + 0..3 of one state) over the wave's 4 rows; row
 // j of the result holds the sum for step 4kg + j.
@@ -390,11 +391,6 @@ __device__ __forceinline__ float rows4_sum(float v0, float v1, float v2, float v
     return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
 
-// B / C tile slot of (state n, step t): 4-step groups XOR-swizzled by state
-// so that 8 lanes reading 4-step groups of states 0..7 (or 8..15) with
-// ds_read_b128 hit 8 distinct groups of 4 banks, and a staging row of 16
-// steps fills one bank half.
-__device__ __forceinline__ int bc_slot(int n, int t) { return n * kT + 4 * ((t >> 2) ^ ((n >> 1) & 3)) + (t & 3); }
 // dB / dC wave-partial slot of (step t, state n): state XOR-swizzled by step,
 // conflict-free both for rows writing (4 steps x 16 states) and for the
 // flush reading (16 steps x 2 states).
@@ -404,7 +400,7 @@ template <typename IT, bool kZ>
 // 3 workgroups per CU (12 waves): at most 168 VGPRs and 54,613 B of LDS.
 __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kT];              // [buf][B, C][n][t]
-    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * kRows * 2 * kTrHRow]; // [wave][row][half][lane][8 steps][2]
+    __shared__ __attribute__((aligned(16))) float s_tr[kWaves * kRows * kTrRowB];     // [wave][row][lane][8 steps][2]
     __shared__ __attribute__((aligned(16))) float s_wg[2 * 2 * kWaves * kT * 16];     // [buf][dB, dC][wave][t][n]
     const FwdParams& p = q.f;
 
@@ -461,11 +457,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
 
     // (s1, s2) summed over the row's 16 states, 8 steps (half a chunk) at a
     // time: lane n stores steps 2m, 2m+1 of the half (m = 0..3) as a float4 at
-    // n * 16 + 4 * (m ^ ((n >> 1) & 3)); lane r then adds states
-    // n = 2 i + (r >> 3) (i = 0..7) of step r & 7, and the other 8 states come
-    // from lane r ^ 8 (DPP row_ror:8).  Both access patterns are free of bank
-    // conflicts.  s2 is summed with the weights A_n of those states.
-    float* trw = s_tr + (w * kRows + j) * 2 * kTrHRow;
+    // n * 16 + 4 * (m ^ (n >> 2)); lane r then adds states n = 2 i + (r >> 3)
+    // (i = 0..7) of step r & 7, and the other 8 states come from lane r ^ 8
+    // (DPP row_ror:8).  The float4 writes and float2 reads of a wave both take
+    // the minimum number of LDS cycles.  One region per row serves both halves:
+    // a wave's LDS operations execute in order, so the second half's writes
+    // cannot overtake the first half's reads.  s2 is summed with the weights
+    // A_n of those states.
+    float* trw = s_tr + (w * kRows + j) * kTrRowB;
     const int te = r & 1, tm = (r & 7) >> 1, tnh = r >> 3;
     float Aw[8];
 #pragma unroll
@@ -585,10 +584,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                 dCp[ki] = bmul<k>(dy, hs[k]);
             });
             // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
-            float* trh = trw + hh * kTrHRow;
-            *reinterpret_cast<float4*>(trh + r * 16 + 4 * ((2 * (kg & 1)) ^ ((r >> 1) & 3))) =
+            float* trh = trw;
+            *reinterpret_cast<float4*>(trh + r * 16 + 4 * ((2 * (kg & 1)) ^ (r >> 2))) =
                 make_float4(s1p[0], s2p[0], s1p[1], s2p[1]);
-            *reinterpret_cast<float4*>(trh + r * 16 + 4 * ((2 * (kg & 1) + 1) ^ ((r >> 1) & 3))) =
+            *reinterpret_cast<float4*>(trh + r * 16 + 4 * ((2 * (kg & 1) + 1) ^ (r >> 2))) =
                 make_float4(s1p[2], s2p[2], s1p[3], s2p[3]);
             // dB / dC of steps 4kg..4kg+3 summed over the wave's rows: row j
             // holds step 4kg + j
@@ -599,7 +598,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int n = 2 * i + tnh;
-                    tv[i] = *reinterpret_cast<const float2*>(trh + n * 16 + 4 * (tm ^ ((n >> 1) & 3)) + 2 * te);
+                    tv[i] = *reinterpret_cast<const float2*>(trh + n * 16 + 4 * (tm ^ (n >> 2)) + 2 * te);
                 }
             }
         });

@@ -189,69 +189,46 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
     finish_pending(slot ^ 1);
 }
 
-// Fast path: dstate 16, variable B and C, seqlen a multiple of 64, dim a
-// multiple of 16, z gate fixed at compile time.  Every step, state and
-// channel is real, so the loop body has no branch around a memory access
-// (loads and stores share one in-order counter, vmcnt; after a branch that
-// contains memory accesses the compiler waits for all of them, which would
-// also wait for the prefetch of the next super-tile).
+// Fast path: dstate 16, variable B and C, seqlen a multiple of 64, dim and
+// channels per group multiples of 16, z gate fixed at compile time.  Every
+// step, state and channel is real, so the loop has no branch around a memory
+// access (on gfx950 the compiler waits for every outstanding load at such a
+// branch, which would serialise the prefetch).
 //
-// Global traffic is workgroup-cooperative: per 64-step super-tile, each of
-// the 256 threads moves one 16-byte piece of each of u, delta, z, B and C
-// (16 rows x 256 contiguous bytes per array for fp32), prefetched one
-// super-tile ahead in registers and staged in LDS; outputs go back the same
-// way.  Lanes then read their per-step values and B / C rows from LDS.  A
-// wave's checkpoint store is 4 channels x 16 states = 256 contiguous bytes.
-constexpr int kS = 64;                       // steps per super-tile
-constexpr int kSq = kS / kT;                 // 16-step sub-tiles per super-tile
-constexpr int kStrm = kS + 16;               // LDS row stride of stream tiles (floats)
-constexpr int kBCs = kS + 4;                 // LDS row stride of B / C tiles (floats)
+// Global traffic moves in 64-step super-chunks with one barrier each: lane r
+// of a row owns steps 4r..4r+3 of its channel and reads / writes them as one
+// 16-byte (fp32) access, so every row segment is 256 contiguous bytes (HBM
+// streams of 64-byte segments reach only about 70 % of the bandwidth of
+// 256-byte ones on this part).  Within a super-chunk, four 16-step chunks:
+//  - step k of chunk q is owned by lane 4q + k/4, component k % 4, and
+//    reaches the other lanes of the row by a DPP row broadcast of that lane;
+//  - the B / C tile of the super-chunk is staged through LDS (double
+//    buffered, loaded one super-chunk ahead);
+//  - y_t = sum_n C h is an in-row transposition through LDS: each lane
+//    writes its 16 products C_t h_t, and lane r sums the 16 states of step r
+//    one chunk later (after the next chunk's decay factors, so the LDS round
+//    trip is off the critical path); the 64 sums of a super-chunk are
+//    regrouped through LDS into the owners' float4 for the stores, one
+//    super-chunk late;
+//  - the checkpoint of the state is one store per lane and chunk (a wave's
+//    4 channels x 16 states are 256 contiguous bytes).
+constexpr int kSC = 64;                      // steps per super-chunk
+constexpr int kQ = kSC / kT;                 // chunks per super-chunk
+constexpr int kYRow = kT * kT + 16;          // per-row product tile, padded so rows j, j + 1 use different bank halves
+constexpr int kYoRow = kSC + 16;             // per-row regroup area, padded likewise
 
-template <typename IT>
-struct Piece4 {                              // 4 consecutive elements of one row
-    using raw = typename std::conditional<sizeof(IT) == 4, u32x4, u32x2>::type;
-    raw v;
-    __device__ __forceinline__ void load(const SS_GLOBAL IT* p) { v = *(const SS_GLOBAL raw*)p; }
-    __device__ __forceinline__ float4 f() const {
-        if constexpr (sizeof(IT) == 4) {
-            return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
-        } else if constexpr (__is_same(IT, bf16_t)) {
-            return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
-                               __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u));
-        } else {
-            return make_float4(float(__builtin_bit_cast(_Float16, uint16_t(v.x & 0xffffu))),
-                               float(__builtin_bit_cast(_Float16, uint16_t(v.x >> 16))),
-                               float(__builtin_bit_cast(_Float16, uint16_t(v.y & 0xffffu))),
-                               float(__builtin_bit_cast(_Float16, uint16_t(v.y >> 16))));
-        }
-    }
-};
-
-template <typename IT>
-__device__ __forceinline__ void store4(SS_GLOBAL IT* p, float4 v) {
-    if constexpr (sizeof(IT) == 4) {
-        *(SS_GLOBAL f32x4*)p = f32x4{v.x, v.y, v.z, v.w};
-    } else if constexpr (__is_same(IT, bf16_t)) {
-        *(SS_GLOBAL u32x2*)p = u32x2{io<bf16_t>::pack2(v.x, v.y),
-                                     io<bf16_t>::pack2(v.z, v.w)};
-    } else {
-        *(SS_GLOBAL u32x2*)p =
-            u32x2{uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16),
-                  uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.z))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.w))) << 16)};
-    }
-}
+// LDS bank model of gfx950 (measured): 4-byte accesses see 32 banks of 4
+// bytes, 8- and 16-byte accesses see 64.
+// B / C super-chunk tile slot of (state n, 4-step group gi): the 16 lanes of
+// states 0..15 reading group gi with ds_read_b128 cover all 64 banks once,
+// and a staging row writing its 16 groups does too.
+__device__ __forceinline__ int bc64_slot(int n, int gi) { return n * kSC + 4 * (gi ^ n); }
 
 template <typename IT, bool kZ>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
-    __shared__ __attribute__((aligned(16))) float tr_buf[kWaves * kTrWave];
-    // stream tiles [16 channels][64 steps] of u, delta, z; u and delta hold
-    // the outputs (out, y) once every lane has read its inputs
-    __shared__ __attribute__((aligned(16))) float s_u[kChPerWG * kStrm];
-    __shared__ __attribute__((aligned(16))) float s_d[kChPerWG * kStrm];
-    __shared__ __attribute__((aligned(16))) float s_z[kZ ? kChPerWG * kStrm : 4];
-    // B / C tiles [16 states][64 steps]
-    __shared__ __attribute__((aligned(16))) float s_B[16 * kBCs];
-    __shared__ __attribute__((aligned(16))) float s_C[16 * kBCs];
+    __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B, C][n][64 steps]
+    __shared__ __attribute__((aligned(16))) float s_yp[kWaves * kRows * kYRow];    // [wave][row][n][16 steps]
+    __shared__ __attribute__((aligned(16))) float s_yo[kWaves * kRows * kYoRow];   // [wave][row][64 steps]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -265,118 +242,165 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
-    const int64_t L = p.seqlen;
-    float* wbuf = tr_buf + w * kTrWave;
+    const int nsc = int(p.seqlen / kSC);           // below 2^20
 
-    // cooperative piece of this thread: row prow, steps 4 pc .. 4 pc + 3
-    const int prow = tid >> 4, pc = tid & 15;
-    // workgroup-uniform row bases plus per-thread byte offsets (below 2^32,
-    // checked by fwd_fast_ok)
-    const IT* gu = static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds;
-    const IT* gd = static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds;
-    const IT* gz = kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : gu;
-    const IT* gB = static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs;
-    const IT* gC = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
-    IT* go = static_cast<IT*>(p.out) + b * p.o_bs + c0 * p.o_ds;
-    IT* gy = kZ ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : go;
+    // buffer resources at the workgroup's rows; lane (row, r) owns steps
+    // 4r..4r+3 of channel c0 + row and, for the B / C staging, of state row
+    const rsrc_t Ru = make_rsrc(static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds);
+    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
+    const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
+    const rsrc_t RB = make_rsrc(static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs);
+    const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
+    const rsrc_t Ro = make_rsrc(static_cast<IT*>(p.out) + b * p.o_bs + c0 * p.o_ds);
+    const rsrc_t Ry = make_rsrc(kZ ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : nullptr);
+    // x: (batch, chunk, dim, dstate)
+    const rsrc_t Rx = make_rsrc(p.x + (b * p.n_chunks * p.dim + c0) * kT);
     constexpr uint32_t es = sizeof(IT);
-    const uint32_t ou = uint32_t(prow * p.u_ds + 4 * pc) * es, od = uint32_t(prow * p.dl_ds + 4 * pc) * es;
-    const uint32_t oz = kZ ? uint32_t(prow * p.z_ds + 4 * pc) * es : ou;
-    const uint32_t oB = uint32_t(prow * p.B_ns + 4 * pc) * es, oC = uint32_t(prow * p.C_ns + 4 * pc) * es;
-    const uint32_t oo = uint32_t(prow * p.o_ds + 4 * pc) * es;
-    const uint32_t oy = kZ ? uint32_t(prow * p.y_ds + 4 * pc) * es : oo;
-    const int spos = prow * kStrm + 4 * pc;        // this piece in a stream tile
-    const int bpos = prow * kBCs + 4 * pc;         // this piece in a B / C tile
-    // x: (batch, chunk, dim, dstate); a wave's 4 channels x 16 states are contiguous
-    float* gx = p.x + (b * p.n_chunks * p.dim + c0) * kT;
+    const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
+    const uint32_t oz = uint32_t(row * p.z_ds + 4 * r) * es;
+    const uint32_t oB = uint32_t(row * p.B_ns + 4 * r) * es, oC = uint32_t(row * p.C_ns + 4 * r) * es;
+    const uint32_t oo = uint32_t(row * p.o_ds + 4 * r) * es, oy = uint32_t(row * p.y_ds + 4 * r) * es;
     const uint32_t ox = uint32_t(row * kT + r) * 4u;
-    const int64_t x_chunk_stride = p.dim * kT;
+    const uint32_t x_chunk_bytes = uint32_t(p.dim * kT * 4);
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
     const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
 
-    struct Pieces { Piece4<IT> u, d, z, B, C; };
-    auto fetch = [&](int64_t t0, Pieces& P) {   // t0 clamped by the caller
-        P.u.load(goff(gbase(gu + t0), ou));
-        P.d.load(goff(gbase(gd + t0), od));
-        if constexpr (kZ) P.z.load(goff(gbase(gz + t0), oz));
-        P.B.load(goff(gbase(gB + t0), oB));
-        P.C.load(goff(gbase(gC + t0), oC));
+    struct Super { float4 u, d, z, B, C; };
+    auto fetch = [&](int sc, Super& S) {       // 0 <= sc < nsc
+        const uint32_t so = uint32_t(sc * kSC) * es;
+        S.u = bload4<IT>(Ru, ou, so);
+        S.d = bload4<IT>(Rd, od, so);
+        S.z = kZ ? bload4<IT>(Rz, oz, so) : make_float4(0.f, 0.f, 0.f, 0.f);
+        S.B = bload4<IT>(RB, oB, so);
+        S.C = bload4<IT>(RC, oC, so);
     };
-    auto stage = [&](const Pieces& P) {
-        *reinterpret_cast<float4*>(s_u + spos) = P.u.f();
-        *reinterpret_cast<float4*>(s_d + spos) = P.d.f();
-        if constexpr (kZ) *reinterpret_cast<float4*>(s_z + spos) = P.z.f();
-        *reinterpret_cast<float4*>(s_B + bpos) = P.B.f();
-        *reinterpret_cast<float4*>(s_C + bpos) = P.C.f();
+    auto stage = [&](const Super& S, int buf) {
+        *reinterpret_cast<float4*>(s_bc + (buf * 2 + 0) * 16 * kSC + bc64_slot(row, r)) = S.B;
+        *reinterpret_cast<float4*>(s_bc + (buf * 2 + 1) * 16 * kSC + bc64_slot(row, r)) = S.C;
     };
+    // this row's product tile: lane n writes its steps 4m..4m+3 as a float4
+    // at n * 16 + 4 * (m ^ ((n >> 1) & 3)); lane r reads step r of state n at
+    // n * 16 + 4 * ((r >> 2) ^ ((n >> 1) & 3)) + (r & 3)
+    float* yrow = s_yp + (w * kRows + j) * kYRow;
+    float* yo = s_yo + (w * kRows + j) * kYoRow;
+    int yoff[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) yoff[m] = 4 * ((r >> 2) ^ m) + (r & 3);
 
     float h = 0.f;
-    Pieces P;
-    fetch(0, P);
-    for (int64_t t0 = 0; t0 < L; t0 += kS) {
-        lds_barrier();                 // previous super-tile's outputs have been stored
-        stage(P);
-        lds_barrier();
-        fetch(t0 + kS < L ? t0 + kS : t0, P);      // prefetch (re-reads the last super-tile at the end)
+    float4 pu = make_float4(0.f, 0.f, 0.f, 0.f), pz = pu;   // u, z of the previous super-chunk
 
-        // per-step inputs of steps t0 + 16 q + r of this lane's channel
-        float uq[kSq], dq[kSq], zq[kSq];
-#pragma unroll
-        for (int q = 0; q < kSq; ++q) {
-            uq[q] = s_u[row * kStrm + kT * q + r];
-            dq[q] = s_d[row * kStrm + kT * q + r];
-            zq[q] = kZ ? s_z[row * kStrm + kT * q + r] : 0.f;
+    // out / y of super-chunk sc (its 64 sums are in yo)
+    auto finish_super = [&](int sc) {
+        float4 y = *reinterpret_cast<const float4*>(yo + 4 * r);
+        y.x = __builtin_fmaf(Dv, pu.x, y.x);
+        y.y = __builtin_fmaf(Dv, pu.y, y.y);
+        y.z = __builtin_fmaf(Dv, pu.z, y.z);
+        y.w = __builtin_fmaf(Dv, pu.w, y.w);
+        const uint32_t so = uint32_t(sc * kSC) * es;
+        if constexpr (kZ) {
+            bstore4<IT>(Ry, oy, so, y);
+            y.x *= pz.x * sigmoidf_(pz.x);
+            y.y *= pz.y * sigmoidf_(pz.y);
+            y.z *= pz.z * sigmoidf_(pz.z);
+            y.w *= pz.w * sigmoidf_(pz.w);
         }
-        lds_barrier();                 // s_u / s_d are reused for the outputs below
-
+        bstore4<IT>(Ro, oo, so, y);
+    };
+    // sum over states of the chunk whose products are in the tile: step r
+    auto read_tile = [&](float (&ys)[kT]) {
 #pragma unroll
-        for (int q = 0; q < kSq; ++q) {
-            float Bt[kT], Ct[kT];
+        for (int n = 0; n < kT; ++n) ys[n] = yrow[n * 16 + yoff[(n >> 1) & 3]];
+    };
+    auto sum16 = [&](const float (&ys)[kT]) {
+        const float s0 = (ys[0] + ys[1]) + (ys[2] + ys[3]);
+        const float s1 = (ys[4] + ys[5]) + (ys[6] + ys[7]);
+        const float s2 = (ys[8] + ys[9]) + (ys[10] + ys[11]);
+        const float s3 = (ys[12] + ys[13]) + (ys[14] + ys[15]);
+        return (s0 + s1) + (s2 + s3);
+    };
+
+    Super S;
+    fetch(0, S);
+    stage(S, 0);
+    for (int sc = 0; sc < nsc; ++sc) {
+        const int buf = sc & 1;
+        lds_barrier();   // B / C tile of sc staged
+        const float4 cu = S.u, cd = S.d, cz = S.z;
+        fetch(sc + 1 < nsc ? sc + 1 : nsc - 1, S);
+
+        float4 dt, dtu;
+        {
+            const float p0 = cd.x + bias, p1 = cd.y + bias, p2 = cd.z + bias, p3 = cd.w + bias;
+            dt = softplus ? make_float4(softplus20(p0), softplus20(p1), softplus20(p2), softplus20(p3))
+                          : make_float4(p0, p1, p2, p3);
+            dtu = make_float4(dt.x * cu.x, dt.y * cu.y, dt.z * cu.z, dt.w * cu.w);
+        }
+        dpp_sources_ready4(dt, dtu);
+        const float* sB = s_bc + (buf * 2 + 0) * 16 * kSC;
+        const float* sC = s_bc + (buf * 2 + 1) * 16 * kSC;
+
+        static_for<kQ>([&](auto Q) {
+            constexpr int q = decltype(Q)::value;
+            float Bq[kT], Cq[kT];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float4 vb = *reinterpret_cast<const float4*>(s_B + r * kBCs + kT * q + 4 * i);
-                const float4 vc = *reinterpret_cast<const float4*>(s_C + r * kBCs + kT * q + 4 * i);
-                Bt[4 * i] = vb.x; Bt[4 * i + 1] = vb.y; Bt[4 * i + 2] = vb.z; Bt[4 * i + 3] = vb.w;
-                Ct[4 * i] = vc.x; Ct[4 * i + 1] = vc.y; Ct[4 * i + 2] = vc.z; Ct[4 * i + 3] = vc.w;
+                const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
+                const float4 vc = *reinterpret_cast<const float4*>(sC + bc64_slot(r, 4 * q + i));
+                Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
+                Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
             }
-            const float pre = dq[q] + bias;
-            const float dt = softplus ? softplus20(pre) : pre;
-            const float dtu = dt * uq[q];
-            // decay factors and inputs of all 16 steps first: they do not
-            // depend on h, so the exp latency stays off the h chain
-            float a[kT], bb[kT], yp[kT];
+            // products of the previous chunk, written by this row last chunk
+            float ys[kT];
+            read_tile(ys);
+            // decay factors of all 16 steps first: they do not depend on h, so
+            // the exp latency stays off the h chain
+            float a[kT];
             static_for<kT>([&](auto K) {
                 constexpr int k = decltype(K)::value;
-                a[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
-                bb[k] = row_bcast<k>(dtu) * Bt[k];
+                a[k] = __builtin_amdgcn_exp2f(row_bcast<4 * q + k / 4>(f4get(dt, k % 4)) * a2);
             });
+            // the previous chunk's sums (chunk 4 sc + q - 1) into the regroup area
+            yo[((q + kQ - 1) % kQ) * kT + r] = sum16(ys);
+            if constexpr (q == 0) {
+                finish_super(sc > 0 ? sc - 1 : 0);
+                pu = cu;     // this super-chunk's u, z wait for its outputs
+                pz = cz;
+            }
+            float yp[kT];
             static_for<kT>([&](auto K) {
                 constexpr int k = decltype(K)::value;
-                h = __builtin_fmaf(a[k], h, bb[k]);
-                yp[k] = Ct[k] * h;
+                h = __builtin_fmaf(a[k], h, bmul<4 * q + k / 4>(f4get(dtu, k % 4), Bq[k]));
+                yp[k] = Cq[k] * h;
             });
-            *goff(gbase(gx + ((t0 + kT * q) / kT) * x_chunk_stride), ox) = h;
-            row_transpose_write(wbuf, yp, j, r);
-            float y = row_transpose_read(wbuf, j, r) + Dv * uq[q];
-            if constexpr (kZ) {
-                s_d[row * kStrm + kT * q + r] = y;
-                y *= zq[q] * sigmoidf_(zq[q]);
-            }
-            s_u[row * kStrm + kT * q + r] = y;
-        }
-        lds_barrier();
-        store4<IT>(goff(gbase(go + t0), oo), *reinterpret_cast<const float4*>(s_u + spos));
-        if constexpr (kZ) store4<IT>(goff(gbase(gy + t0), oy), *reinterpret_cast<const float4*>(s_d + spos));
+            bstore<float>(Rx, ox, uint32_t(kQ * sc + q) * x_chunk_bytes, h);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                *reinterpret_cast<float4*>(yrow + r * 16 + 4 * (m ^ ((r >> 1) & 3))) =
+                    make_float4(yp[4 * m], yp[4 * m + 1], yp[4 * m + 2], yp[4 * m + 3]);
+        });
+        // B / C tile of the next super-chunk into the other buffer
+        stage(S, buf ^ 1);
+    }
+    // the last chunk's sums, then the last super-chunk's outputs
+    {
+        float ys[kT];
+        read_tile(ys);
+        yo[(kQ - 1) * kT + r] = sum16(ys);
+        finish_super(nsc - 1);
     }
 }
 
 bool fwd_fast_ok(const FwdParams& p) {
-    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kS && p.seqlen % kS == 0 &&
+    // every byte offset the kernel forms stays below 2^32: rows and seqlen
+    // below 2^26 elements, and the checkpoint offset (chunk x dim x 64 B)
+    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kSC && p.seqlen % kSC == 0 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && (!p.has_z || p.y != nullptr) &&
-           small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns});
+           small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns}) &&
+           p.seqlen * p.dim < (int64_t(1) << 30);
 }
 
 template <typename IT>

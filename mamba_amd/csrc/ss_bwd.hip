@@ -497,16 +497,26 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // 4 waves and adds once into global memory (16 consecutive steps per state)
     const int fn = tid >> 4, ft = tid & 15;
     const uint32_t ofl = uint32_t(fn * L + ft) * 4u;
-    auto flush = [&](int ck, int buf) {
-        float sB = 0.f, sC = 0.f;
+    // split in the LDS reads and the sums + global adds, so that other work
+    // can sit between them
+    auto flush_read = [&](int buf, float (&v)[2 * kWaves]) {
 #pragma unroll
         for (int ww = 0; ww < kWaves; ++ww) {
-            sB += s_wg[((buf * 2 + 0) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
-            sC += s_wg[((buf * 2 + 1) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
+            v[ww] = s_wg[((buf * 2 + 0) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
+            v[kWaves + ww] = s_wg[((buf * 2 + 1) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
         }
+    };
+    auto flush_commit = [&](int ck, const float (&v)[2 * kWaves]) {
+        const float sB = (v[0] + v[1]) + (v[2] + v[3]);
+        const float sC = (v[4] + v[5]) + (v[6] + v[7]);
         const uint32_t so = uint32_t(ck * kT) * 4u;
         batomic_add(RdB, ofl, so, sB);
         batomic_add(RdC, ofl, so, sC);
+    };
+    auto flush = [&](int ck, int buf) {
+        float v[2 * kWaves];
+        flush_read(buf, v);
+        flush_commit(ck, v);
     };
 
     float gacar = 0.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
@@ -532,7 +542,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
             Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
         }
-        flush(ck + 1 < nck ? ck + 1 : nck - 1, buf ^ 1);
+        float fv[2 * kWaves];
+        flush_read(buf ^ 1, fv);
 
         const float uu = cur.u, pre = cur.d + bias, dout = cur.o, zz = cur.z, yv = cur.y, h0 = cur.x;
         float dt = softplus ? softplus20(pre) : pre;
@@ -549,6 +560,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             // transcendental and needs no wait state after a plain VALU
             as[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
         });
+        // the LDS reads issued above have had the decay factors to land
+        __builtin_amdgcn_sched_barrier(0);
+        flush_commit(ck + 1 < nck ? ck + 1 : nck - 1, fv);
         float hcur = h0;
         static_for<kT>([&](auto K) {
             constexpr int k = decltype(K)::value;
@@ -603,6 +617,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             }
         });
         gacar = ga;
+        // keep the sums below after the whole adjoint, so the reads of the
+        // first half have that time to land
+        __builtin_amdgcn_sched_barrier(0);
 
         // sums over states: lane r ends with step r of the chunk
         auto half_sum = [&](const float2 (&tv)[8], float& t1, float& t2) {

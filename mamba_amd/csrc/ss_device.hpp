@@ -420,20 +420,25 @@ __device__ __forceinline__ float4 bload4(rsrc_t r, uint32_t voff, uint32_t soff)
         }
     }
 }
+// Stores of more than 8 bytes read their data VGPRs after issue, and a VALU
+// write to those VGPRs too soon after the store corrupts the stored data.
+// The compiler inserts the wait states for that only when the store's
+// uniform offset is not a register, so this store takes no uniform offset:
+// callers fold their advance into the resource base.
 template <typename T>
-__device__ __forceinline__ void bstore4(rsrc_t r, uint32_t voff, uint32_t soff, float4 v) {
+__device__ __forceinline__ void bstore4(rsrc_t r, uint32_t voff, float4 v) {
     if constexpr (sizeof(T) == 4) {
         const u32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
-        __builtin_amdgcn_raw_buffer_store_b128(w, r, int(voff), int(soff), 0);
+        __builtin_amdgcn_raw_buffer_store_b128(w, r, int(voff), 0, 0);
     } else if constexpr (__is_same(T, bf16_t)) {
         const u32x2 w = {io<bf16_t>::pack2(v.x, v.y), io<bf16_t>::pack2(v.z, v.w)};
-        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), int(soff), 0);
+        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), 0, 0);
     } else {
         const u32x2 w = {uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) |
                              (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16),
                          uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.z))) |
                              (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.w))) << 16)};
-        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), int(soff), 0);
+        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), 0, 0);
     }
 }
 __device__ __forceinline__ float f4get(const float4& v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }

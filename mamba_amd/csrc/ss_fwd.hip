@@ -251,8 +251,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
     const rsrc_t RB = make_rsrc(static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs);
     const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
-    const rsrc_t Ro = make_rsrc(static_cast<IT*>(p.out) + b * p.o_bs + c0 * p.o_ds);
-    const rsrc_t Ry = make_rsrc(kZ ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : nullptr);
+    // out / y are written with 16-byte stores, which take their advance in the
+    // resource base and no uniform offset (see bstore4)
+    IT* const go = static_cast<IT*>(p.out) + b * p.o_bs + c0 * p.o_ds;
+    IT* const gy = kZ ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : go;
     // x: (batch, chunk, dim, dstate)
     const rsrc_t Rx = make_rsrc(p.x + (b * p.n_chunks * p.dim + c0) * kT);
     constexpr uint32_t es = sizeof(IT);
@@ -300,15 +302,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.y = __builtin_fmaf(Dv, pu.y, y.y);
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
-        const uint32_t so = uint32_t(sc * kSC) * es;
         if constexpr (kZ) {
-            bstore4<IT>(Ry, oy, so, y);
+            bstore4<IT>(make_rsrc(gy + int64_t(sc) * kSC), oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);
             y.w *= pz.w * sigmoidf_(pz.w);
         }
-        bstore4<IT>(Ro, oo, so, y);
+        bstore4<IT>(make_rsrc(go + int64_t(sc) * kSC), oo, y);
     };
     // sum over states of the chunk whose products are in the tile: step r
     auto read_tile = [&](float (&ys)[kT]) {
@@ -363,6 +364,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                 constexpr int k = decltype(K)::value;
                 a[k] = __builtin_amdgcn_exp2f(row_bcast<4 * q + k / 4>(f4get(dt, k % 4)) * a2);
             });
+            // the LDS reads issued above have had the decay factors to land
+            __builtin_amdgcn_sched_barrier(0);
             // the previous chunk's sums (chunk 4 sc + q - 1) into the regroup area
             yo[((q + kQ - 1) % kQ) * kT + r] = sum16(ys);
             if constexpr (q == 0) {

@@ -11,6 +11,11 @@ asm must keep:
 * transcendental forwarding: the result of v_exp / v_log / v_rcp / v_rsq /
   v_sqrt / v_sin / v_cos read by a non-transcendental VALU needs at least
   1 wait state;
+* wide store data: a store of more than 8 bytes (dwordx3 / dwordx4) reads
+  its data VGPRs after issue, so a VALU write to one of them needs at least
+  2 wait states after the store.  The compiler skips this for buffer stores
+  whose uniform offset is a register, so the kernels avoid that form; the
+  check covers every wide store;
 * no packed fp32 VALU ops (v_pk_fma_f32, v_pk_mul_f32, v_pk_add_f32): the
   library is built with them disabled.
 
@@ -26,6 +31,7 @@ import subprocess
 LLVM_BIN = "/opt/rocm/llvm/bin"
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 TRANS = re.compile(r"^v_(exp|log|rcp|rsq|sqrt|sin|cos)_")
+WIDE_STORE = re.compile(r"^(buffer|global|flat|scratch)_store_dwordx[34]$")
 PACKED_F32 = re.compile(r"^v_pk_(fma|mul|add)_f32")
 
 
@@ -107,10 +113,12 @@ def check_function(name, insns):
     """List of (kind, message) problems found in one function."""
     problems = []
     hist = []           # (op, vgprs written, wait states it provides)
+    stores = []         # (wide store op or None, its data vgprs, wait states it provides)
     for text in insns:
         op, ops = _split(text)
         if op == "s_nop":
             hist.append((op, set(), int(ops[0], 0) + 1))
+            stores.append((None, set(), int(ops[0], 0) + 1))
             continue
         if PACKED_F32.match(op):
             problems.append(("packed-fp32", f"{name}: {text}"))
@@ -136,6 +144,23 @@ def check_function(name, insns):
                     problems.append(("trans", f"{name}: '{text}' reads v{sorted(hdst & used)} "
                                               f"straight after {hop}"))
         writes_vgpr = op.startswith("v_") and not op.startswith(("v_cmp", "v_readlane", "v_readfirstlane"))
-        hist.append((op, _vregs(ops[0]) if (writes_vgpr and ops) else set(), 1))
+        dst = _vregs(ops[0]) if (writes_vgpr and ops) else set()
+        if dst:
+            ws = 0
+            for hop, hdata, hw in reversed(stores):
+                if ws >= 2:
+                    break
+                if hop is not None and hdata & dst:
+                    problems.append(("store-data", f"{name}: '{text}' overwrites v{sorted(hdata & dst)} "
+                                                   f"{ws} wait state(s) after {hop}"))
+                    break
+                ws += hw
+        if WIDE_STORE.match(op) and ops:
+            data = _vregs(ops[0] if op.startswith("buffer_") else ops[1])
+            stores.append((op, data, 1))
+        else:
+            stores.append((None, set(), int(ops[0], 0) + 1 if op == "s_nop" else 1))
+        del stores[:-8]
+        hist.append((op, dst, 1))
         del hist[:-8]
     return problems

@@ -1,6 +1,6 @@
-"""The built library's gfx950 code keeps the DPP / transcendental wait
-states its inline asm relies on and has no packed fp32 VALU ops (CPU only:
-disassembles the library, runs nothing)."""
+"""The built library's gfx950 code keeps the DPP / transcendental / wide-store
+wait states its inline asm and buffer stores rely on and has no packed fp32
+VALU ops (CPU only: disassembles the library, runs nothing)."""
 import os
 import tempfile
 
@@ -51,6 +51,14 @@ def test_checker_catches_planted_hazards():
            "v_pk_fma_f32 v[8:9], v[8:9], v[10:11], v[12:13]"]
     kinds = sorted(k for k, _ in isa_check.check_function("planted", bad))
     assert kinds == ["dpp", "packed-fp32", "trans"]
+    store = ["buffer_store_dwordx4 v[58:61], v66, s[20:23], s2 offen",
+             "v_mul_f32_e32 v58, v122, v58"]
+    assert [k for k, _ in isa_check.check_function("store", store)] == ["store-data"]
+    store_ok = ["buffer_store_dwordx4 v[58:61], v66, s[20:23], 0 offen",
+                "v_mul_f32_e32 v123, 0xbfb8aa3b, v119",
+                "v_exp_f32_e32 v123, v123",
+                "v_mul_f32_e32 v58, v122, v58"]
+    assert isa_check.check_function("store_ok", store_ok) == []
     good = ["v_mul_f32_e32 v1, 0x40400000, v1",
             "s_nop 1",
             "v_mul_f32_dpp v2, v1, v2 row_newbcast:3 row_mask:0xf bank_mask:0xf",

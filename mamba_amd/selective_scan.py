@@ -141,6 +141,24 @@ def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *
         nat.check(lib.ss_fwd(ctypes.byref(a), _stream(u.device)), "selective_scan.forward")
 
 
+def prepare_forward(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
+    """Validates the arguments of ``forward_into`` once and returns a callable
+    that launches the same forward again, on the stream that is current now,
+    with no host-side work beyond the C call (the tensors must stay alive
+    and keep their storage).  For repeated launches over fixed buffers."""
+    lib = nat.load()
+    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y)
+    dev = u.device
+    stream = torch.cuda.current_stream(dev)
+    handle = ctypes.c_void_p(stream.cuda_stream)
+    ref = ctypes.byref(a)
+
+    def launch():
+        nat.check(lib.ss_fwd(ref, handle), "selective_scan.forward")
+    launch.args = a
+    return launch
+
+
 def forward_kernel_name(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
     """Base name of the kernel ``forward_into`` launches for these tensors
     ("" when there is no work).  No device work."""
@@ -242,6 +260,38 @@ def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
     b.zero_grads = int(bool(zero_grads))
     with torch.cuda.device(u.device):
         nat.check(lib.ss_bwd(ctypes.byref(b), _stream(u.device)), "selective_scan.backward")
+
+
+def prepare_backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                     du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None, workspace="auto",
+                     zero_grads=False):
+    """``backward_into`` validated once, as a callable that relaunches it on
+    the stream that is current now (see ``prepare_forward``); the workspace,
+    if any, is allocated here and kept by the callable."""
+    lib = nat.load()
+    b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
+                       du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
+    if isinstance(workspace, str):
+        _require(workspace == "auto", f"workspace must be 'auto', None or a tensor, got {workspace!r}")
+        n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))
+        if n < 0:
+            nat.check(nat.SS_ERR_INVALID, "selective_scan.backward")
+        workspace = torch.empty(n, dtype=torch.uint8, device=u.device) if n > 0 else None
+    if workspace is not None:
+        _require(workspace.device == u.device and workspace.is_contiguous(),
+                 "workspace must be a contiguous tensor on the inputs' device")
+        b.workspace = _ptr(workspace)
+        b.workspace_bytes = workspace.numel() * workspace.element_size()
+    b.zero_grads = int(bool(zero_grads))
+    stream = torch.cuda.current_stream(u.device)
+    handle = ctypes.c_void_p(stream.cuda_stream)
+    ref = ctypes.byref(b)
+
+    def launch():
+        nat.check(lib.ss_bwd(ref, handle), "selective_scan.backward")
+    launch.args = b
+    launch.workspace = workspace
+    return launch
 
 
 def backward_kernel_name(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,

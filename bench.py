@@ -12,6 +12,22 @@ describes the dominant kernel, timed with HIP events on the stream it runs
 on; ``cpu_baseline`` times the CPU oracle (pure-PyTorch selective_scan_ref)
 on a bounded slice of the same workload on this host's cores.
 
+Other workloads (``--workload``; one JSON line each, reported against the
+reference's own op order run on the same GPU, not against the CPU):
+  mamba_block_b8_l2048_d1024_bf16   MambaSimple block (d_model 1024, d_inner
+      2048, dt_rank 64, dstate 16, conv 4) forward + backward, bf16 weights
+      and activations, fp32 A / D, hidden states ~ N(0, 1) of (8, 2048, 1024);
+  causal_lm_24x768_b16_l2048_bf16   CausalLM (24 layers, d_model 768, vocab
+      50280) forward in eval mode on token ids of (16, 2048);
+  causal_lm_24x768_b1_l32768_bf16   the same model on one sequence of 32768.
+``value`` is tokens per second; ``ref_op_order`` gives the same step with
+the reference's op sequence (RMSNorm and MambaSimple as PyTorch ops around
+SelectiveScanFn, the residual added after each block).
+  add_rmsnorm_r32768_d768_bf16   the fused residual add + RMSNorm between
+      two blocks of that model (32768 rows of 768, bf16) forward + backward;
+      ``value`` is algorithmic GB/s, with a roofline line and a CPU baseline
+      as for the scan.
+
 ``--calibrate-copy MIB`` instead times a plain device-to-device copy of MIB
 MiB (torch's copy kernel); under ``rocprofv3 --pmc FETCH_SIZE`` /
 ``WRITE_SIZE`` it gives the factor between those counters and bytes actually
@@ -38,6 +54,206 @@ WORKLOADS = {
     "ss_fwd_bwd_b4_d5120_n16_l8192_bf16": (4, 5120, 16, 8192, "bfloat16", 1002),
 }
 DEFAULT = "ss_fwd_bwd_b8_d1536_n16_l2048_f32"
+MODEL_WORKLOADS = {
+    # name: (kind, batch, seqlen, d_model, layers, vocab)
+    "mamba_block_b8_l2048_d1024_bf16": ("block", 8, 2048, 1024, 1, 0),
+    "causal_lm_24x768_b16_l2048_bf16": ("lm", 16, 2048, 768, 24, 50280),
+    "causal_lm_24x768_b1_l32768_bf16": ("lm", 1, 32768, 768, 24, 50280),
+}
+
+NORM_WORKLOADS = {
+    # name: (rows, dim, dtype): the residual add + RMSNorm between two blocks of
+    # the 24 x 768 CausalLM at batch 16, seqlen 2048 (32768 token rows)
+    "add_rmsnorm_r32768_d768_bf16": (32768, 768, "bfloat16"),
+}
+
+
+def norm_bytes(rows, dim, s):
+    """Algorithmic HBM bytes of the fused add + RMSNorm.
+
+    forward: read x, residual; write out, s (4 * rows * dim * s); write rstd
+    (rows * 4); read weight.  backward: read s, dout, dresidual_out; write dx
+    (4 * rows * dim * s); read rstd; read weight, write dweight.  The
+    per-workgroup dweight rows are scratch and are not counted."""
+    fwd = 4 * rows * dim * s + rows * 4 + dim * s
+    bwd = 4 * rows * dim * s + rows * 4 + 2 * dim * s
+    return fwd, bwd
+
+
+def bench_norm(args):
+    """Fused residual add + RMSNorm forward + backward; one JSON line."""
+    import torch
+    from mamba_amd import _native as nat
+    from mamba_amd.ops.rms_norm import prepare_rms_norm_bwd, prepare_rms_norm_fwd
+
+    rows, dim, dtype_name = NORM_WORKLOADS[args.workload]
+    dtype = getattr(torch, dtype_name)
+    s = 2 if dtype != torch.float32 else 4
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(1005)
+    x, r, dout, dres = (torch.randn(rows, dim, generator=gen).to(dtype).to(dev) for _ in range(4))
+    w = (0.5 * torch.randn(dim, generator=gen)).to(dtype).to(dev)
+    out, sres, dx = (torch.empty(rows, dim, dtype=dtype, device=dev) for _ in range(3))
+    rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    dw = torch.empty(dim, dtype=dtype, device=dev)
+    ws = torch.empty(int(nat.load().ss_rmsnorm_bwd_workspace_bytes(rows, dim)), dtype=torch.uint8, device=dev)
+    fwd = prepare_rms_norm_fwd(x, w, r, 1e-6, out, sres, rstd)
+    bwd = prepare_rms_norm_bwd(sres, w, rstd, dout, dres, dx, dw, ws)
+    fname = "rmsnorm_fwd_kernel"
+    bname = "rmsnorm_bwd_kernel + rmsnorm_dw_reduce"
+
+    def step():
+        fwd()
+        bwd()
+
+    def timed(fn, n):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = timed(step, args.steps)
+    kernel_ms = {fname: timed(fwd, args.kernel_reps), bname: timed(bwd, args.kernel_reps)}
+    print(f"[bench] kernels: " + ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in kernel_ms.items()),
+          file=sys.stderr, flush=True)
+    fwd_bytes, bwd_bytes = norm_bytes(rows, dim, s)
+    gbs = (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9
+    dom = max(kernel_ms, key=kernel_ms.get)
+    dom_bytes = fwd_bytes if dom == fname else bwd_bytes
+    achieved = dom_bytes / (kernel_ms[dom] * 1e-3) / 1e9
+    line = {
+        "metric": f"add+RMSNorm fwd+bwd GB/s (% HBM peak), rows {rows}, dim {dim}",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": {torch.float32: "f32", torch.bfloat16: "bf16"}.get(dtype, "f16"),
+        "data": "synthetic",
+        "config": {"workload": args.workload, "rows": rows, "dim": dim, "residual": True, "prenorm": True,
+                   "io_dtype": dtype_name, "weight_dtype": dtype_name},
+        "pct_hbm_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "algorithmic_bytes_per_step": fwd_bytes + bwd_bytes,
+        "kernel_us": {k: round(v * 1e3, 2) for k, v in kernel_ms.items()},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": dom_bytes},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = norm_cpu_baseline(rows, dim, dtype_name)
+        line["cpu_baseline"]["gpu_speedup"] = round(gbs / line["cpu_baseline"]["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+def norm_cpu_baseline(rows, dim, dtype_name, sample_rows=None, reps=3):
+    """The oracle's add + RMSNorm (PyTorch on this host's cores, fp32 compute from
+    the I/O dtype) forward + autograd backward on `sample_rows` rows (all of
+    them by default: well under a second), scaled with the same byte formula."""
+    import torch
+    from oracle.mamba_block_ref import add_rms_norm_ref
+
+    sample_rows = rows if sample_rows is None else sample_rows
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    dtype = getattr(torch, dtype_name)
+    gen = torch.Generator().manual_seed(1005)
+    x, r, dout, dres = (torch.randn(sample_rows, dim, generator=gen).to(dtype) for _ in range(4))
+    w = (0.5 * torch.randn(dim, generator=gen)).to(dtype)
+
+    def run():
+        xg, rg, wg = (t.clone().requires_grad_(True) for t in (x, r, w))
+        out, s = add_rms_norm_ref(xg, rg, wg)
+        torch.autograd.backward([out, s], [dout, dres])
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    s = 2 if dtype != torch.float32 else 4
+    fb, bb = norm_bytes(sample_rows, dim, s)
+    return {"value": round((fb + bb) / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{sample_rows} of {rows} rows, dim {dim}, {dtype_name}; median of {reps}",
+            "seconds_per_sample": round(t, 4)}
+
+
+def bench_model(args):
+    """Mamba block fwd+bwd or CausalLM forward; one JSON line."""
+    import torch
+    from mamba_amd.models import CausalLM, CausalLMConfig
+    from mamba_amd.modules import MambaSimple
+
+    kind, batch, seqlen, d_model, layers, vocab = MODEL_WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16
+    torch.manual_seed(1003)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    if kind == "block":
+        block = MambaSimple(d_model, state_dim=16, conv_kernel=4, expansion_factor=2, device=dev, dtype=dt)
+        x = torch.randn(batch, seqlen, d_model, device=dev, dtype=dt).requires_grad_(True)
+        dout = torch.randn(batch, seqlen, d_model, device=dev, dtype=dt)
+        params = [x] + list(block.parameters())
+
+        def step():
+            return torch.autograd.grad(block(x), params, dout)
+
+        ms = timed(step)
+        block.use_fast_path = False
+        ms_ref = timed(step) if not args.no_ref_order else None
+        metric = "Mamba block fwd+bwd tokens/s, d_model 1024, seqlen 2048"
+        config = {"workload": args.workload, "batch": batch, "seqlen": seqlen, "d_model": d_model,
+                  "d_inner": 2 * d_model, "dt_rank": block.delta_rank, "dstate": 16, "d_conv": 4,
+                  "dtype": "bf16 (A, D fp32)"}
+    else:
+        cfg = CausalLMConfig(vocab_size=vocab, model_dim=d_model, state_dim=16, conv_kernel=4,
+                             expansion_factor=2, num_layers=layers)
+        model = CausalLM(cfg, device=dev, dtype=dt).eval()
+        ids = torch.randint(0, vocab, (batch, seqlen), device=dev)
+
+        def step():
+            with torch.no_grad():
+                return model(ids)
+
+        ms = timed(step)
+        for layer in model.layers:
+            layer.mamba.use_fast_path = False
+            layer.norm.use_fast_path = False
+        model.norm.use_fast_path = False
+        ms_ref = timed(step) if not args.no_ref_order else None
+        metric = f"CausalLM forward tokens/s, {layers} layers, d_model {d_model}, seqlen {seqlen}"
+        config = {"workload": args.workload, "batch": batch, "seqlen": seqlen, "d_model": d_model,
+                  "layers": layers, "vocab": vocab, "dtype": "bf16 (A, D fp32)", "mode": "eval"}
+    tokens = batch * seqlen
+    line = {"metric": metric, "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic, random init",
+            "config": config,
+            "ref_op_order": None if ms_ref is None else {
+                "ms_per_step": round(ms_ref, 4), "value": round(tokens / (ms_ref * 1e-3), 1),
+                "speedup": round(ms_ref / ms, 3),
+                "what": "the reference's op sequence (RMSNorm and MambaSimple as PyTorch ops around "
+                        "SelectiveScanFn on the same HIP scan, residual added after each block), "
+                        "same weights and inputs"}}
+    print(json.dumps(line), flush=True)
 
 
 def algorithmic_bytes(batch, dim, dstate, seqlen, s, groups=1):
@@ -118,9 +334,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=DEFAULT,
+                    choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(NORM_WORKLOADS))
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-ref-order", action="store_true",
+                    help="block / LM workloads: skip timing the reference's op order")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only time a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -132,6 +351,12 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.workload in MODEL_WORKLOADS:
+        bench_model(args)
+        return
+    if args.workload in NORM_WORKLOADS:
+        bench_norm(args)
         return
 
     import torch

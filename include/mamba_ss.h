@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 4
+#define SS_ABI_VERSION 5
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -205,6 +205,52 @@ typedef struct ss_conv1d_bwd_args {
    recomputes the pre-activation from x, weight and bias. */
 int ss_conv1d_fwd(const ss_conv1d_args* a, void* stream);
 int ss_conv1d_bwd(const ss_conv1d_bwd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm with an optional residual add, on rows of dim elements.  Replaces
+ * RMSNorm.forward (modules/rms_norm.py:19,29-31) and the residual add that
+ * ends each block (models/causal_lm.py:31-35), fused:
+ *   s    = x + residual, rounded to dtype        (s = x without residual)
+ *   out  = s * rsqrt(mean(s^2) + eps) * (1 + weight), in fp32, rounded to dtype
+ * x, residual, out, residual_out, dout, dresidual_out, dx: (rows, dim) with
+ * unit column stride and free row strides, element type dtype; weight and
+ * dweight: (dim) contiguous, w_dtype = dtype or SS_F32; rstd: fp32 (rows).
+ * ------------------------------------------------------------------------ */
+typedef struct ss_rmsnorm_args {
+    int64_t rows, dim;
+    int32_t dtype;                       /* enum ss_dtype */
+    int32_t w_dtype;                     /* enum ss_dtype: dtype or SS_F32 */
+    float eps;
+    int32_t pad_;
+    int64_t x_row_stride, residual_row_stride, out_row_stride, residual_out_row_stride;
+    const void* x;
+    const void* residual;                /* may be NULL: s = x */
+    const void* weight;
+    void* out;
+    void* residual_out;                  /* s; may be NULL (not written); ignored without residual */
+    float* rstd;                         /* may be NULL (not written); kept for the backward */
+} ss_rmsnorm_args;
+
+typedef struct ss_rmsnorm_bwd_args {
+    int64_t rows, dim;
+    int32_t dtype, w_dtype;
+    int64_t s_row_stride, dout_row_stride, dresidual_out_row_stride, dx_row_stride;
+    const void* s;                       /* the normalised rows: residual_out, or x without residual */
+    const void* weight;
+    const float* rstd;                   /* from the forward */
+    const void* dout;
+    const void* dresidual_out;           /* may be NULL: gradient arriving at residual_out */
+    void* dx;                            /* written: gradient of s (= of x and of residual) */
+    void* dweight;                       /* written (not accumulated), w_dtype */
+    void* workspace;                     /* ss_rmsnorm_bwd_workspace_bytes(rows, dim) bytes */
+    int64_t workspace_bytes;
+} ss_rmsnorm_bwd_args;
+
+/* Forward: writes out, residual_out and rstd.  Backward: writes dx and
+   dweight; dweight is summed in a fixed order (the same bits every run). */
+int ss_rmsnorm_fwd(const ss_rmsnorm_args* a, void* stream);
+int ss_rmsnorm_bwd(const ss_rmsnorm_bwd_args* a, void* stream);
+int64_t ss_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim);
 
 #ifdef __cplusplus
 }

@@ -13,13 +13,14 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
     "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_bwd_workspace_bytes",
     "ss_fwd_kernel_name", "ss_bwd_kernel_name",
     "ss_fwd", "ss_bwd", "ss_conv1d_fwd", "ss_conv1d_bwd",
+    "ss_rmsnorm_fwd", "ss_rmsnorm_bwd", "ss_rmsnorm_bwd_workspace_bytes",
 )
 
 _i64, _i32, _p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
@@ -78,6 +79,27 @@ class Conv1dBwdArgs(ctypes.Structure):
     ]
 
 
+class RmsNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", _i64), ("dim", _i64),
+        ("dtype", _i32), ("w_dtype", _i32), ("eps", ctypes.c_float), ("pad_", _i32),
+        ("x_row_stride", _i64), ("residual_row_stride", _i64),
+        ("out_row_stride", _i64), ("residual_out_row_stride", _i64),
+        ("x", _p), ("residual", _p), ("weight", _p), ("out", _p), ("residual_out", _p), ("rstd", _p),
+    ]
+
+
+class RmsNormBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", _i64), ("dim", _i64),
+        ("dtype", _i32), ("w_dtype", _i32),
+        ("s_row_stride", _i64), ("dout_row_stride", _i64),
+        ("dresidual_out_row_stride", _i64), ("dx_row_stride", _i64),
+        ("s", _p), ("weight", _p), ("rstd", _p), ("dout", _p), ("dresidual_out", _p),
+        ("dx", _p), ("dweight", _p), ("workspace", _p), ("workspace_bytes", _i64),
+    ]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -113,6 +135,12 @@ def load():
         lib.ss_conv1d_fwd.restype = ctypes.c_int
         lib.ss_conv1d_bwd.argtypes = [ctypes.POINTER(Conv1dBwdArgs), _p]
         lib.ss_conv1d_bwd.restype = ctypes.c_int
+        lib.ss_rmsnorm_fwd.argtypes = [ctypes.POINTER(RmsNormArgs), _p]
+        lib.ss_rmsnorm_fwd.restype = ctypes.c_int
+        lib.ss_rmsnorm_bwd.argtypes = [ctypes.POINTER(RmsNormBwdArgs), _p]
+        lib.ss_rmsnorm_bwd.restype = ctypes.c_int
+        lib.ss_rmsnorm_bwd_workspace_bytes.argtypes = [_i64, _i64]
+        lib.ss_rmsnorm_bwd_workspace_bytes.restype = _i64
         lib.ss_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
         lib.ss_bwd_workspace_bytes.restype = _i64
         lib.ss_fwd.argtypes = [ctypes.POINTER(FwdArgs), _p]

@@ -247,6 +247,18 @@ int check_conv(const ss_conv1d_args* a, bool* empty) {
     return SS_OK;
 }
 
+int check_norm_common(int64_t rows, int64_t dim, int dtype, int w_dtype, const void* weight) {
+    if (rows < 0 || dim < 0)
+        return fail(SS_ERR_INVALID, "negative size (rows=%lld dim=%lld)", (long long)rows, (long long)dim);
+    if (dtype != SS_F32 && dtype != SS_BF16 && dtype != SS_F16) return fail(SS_ERR_INVALID, "unknown dtype %d", dtype);
+    if (w_dtype != dtype && w_dtype != SS_F32)
+        return fail(SS_ERR_UNSUPPORTED, "weight dtype %d must be the row dtype or fp32", w_dtype);
+    if (dim == 0) return SS_OK;
+    if (!weight) return fail(SS_ERR_INVALID, "weight is NULL");
+    if (!aligned(weight, elem_size(w_dtype))) return fail(SS_ERR_INVALID, "weight is misaligned");
+    return SS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -378,6 +390,67 @@ int ss_conv1d_bwd(const ss_conv1d_bwd_args* g, void* stream) {
         return fail(SS_ERR_INVALID, "negative stride");
     hipError_t e = ss::conv1d_launch(&g->f, g, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "conv1d backward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int64_t ss_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim) {
+    if (rows < 0 || dim < 0) {
+        fail(SS_ERR_INVALID, "negative size (rows=%lld dim=%lld)", (long long)rows, (long long)dim);
+        return -1;
+    }
+    return ss::rmsnorm_bwd_parts(rows) * dim * int64_t(sizeof(float));
+}
+
+int ss_rmsnorm_fwd(const ss_rmsnorm_args* a, void* stream) {
+    if (!a) return fail(SS_ERR_INVALID, "null argument block");
+    int rc = check_norm_common(a->rows, a->dim, a->dtype, a->w_dtype, a->weight);
+    if (rc != SS_OK) return rc;
+    if (a->rows == 0 || a->dim == 0) return ok();
+    if (!(a->eps >= 0.f)) return fail(SS_ERR_INVALID, "eps must be >= 0");
+    const size_t es = elem_size(a->dtype);
+    if (!a->x || !a->out) return fail(SS_ERR_INVALID, "%s is NULL", a->x ? "out" : "x");
+    const void* ptrs[] = {a->x, a->residual, a->out, a->residual ? a->residual_out : nullptr};
+    const int64_t rs[] = {a->x_row_stride, a->residual_row_stride, a->out_row_stride, a->residual_out_row_stride};
+    for (int i = 0; i < 4; ++i) {
+        if (!ptrs[i]) continue;
+        if (!aligned(ptrs[i], es)) return fail(SS_ERR_INVALID, "x / residual / out / residual_out is misaligned");
+        if (rs[i] < 0) return fail(SS_ERR_INVALID, "negative row stride");
+    }
+    if (a->rstd && !aligned(a->rstd, 4)) return fail(SS_ERR_INVALID, "rstd is misaligned");
+    if (a->rows > int64_t(UINT32_MAX) * 4) return fail(SS_ERR_UNSUPPORTED, "too many rows");
+    hipError_t e = ss::rmsnorm_launch(a, nullptr, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "rmsnorm forward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int ss_rmsnorm_bwd(const ss_rmsnorm_bwd_args* g, void* stream) {
+    if (!g) return fail(SS_ERR_INVALID, "null argument block");
+    int rc = check_norm_common(g->rows, g->dim, g->dtype, g->w_dtype, g->weight);
+    if (rc != SS_OK) return rc;
+    if (g->dim == 0) return ok();
+    if (g->dim > ss::kRmsNormMaxBwdDim)
+        return fail(SS_ERR_UNSUPPORTED, "dim=%lld above %lld", (long long)g->dim, (long long)ss::kRmsNormMaxBwdDim);
+    if (!g->dweight) return fail(SS_ERR_INVALID, "dweight is NULL");
+    if (!aligned(g->dweight, g->w_dtype == SS_F32 ? 4 : 2)) return fail(SS_ERR_INVALID, "dweight is misaligned");
+    const int64_t need = ss_rmsnorm_bwd_workspace_bytes(g->rows, g->dim);
+    if (need > 0 && (!g->workspace || g->workspace_bytes < need))
+        return fail(SS_ERR_INVALID, "workspace of %lld bytes needed (got %lld)", (long long)need,
+                    (long long)(g->workspace ? g->workspace_bytes : 0));
+    if (g->workspace && !aligned(g->workspace, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
+    if (g->rows > 0) {
+        const size_t es = elem_size(g->dtype);
+        if (!g->s || !g->dout || !g->dx || !g->rstd) return fail(SS_ERR_INVALID, "s / dout / dx / rstd is NULL");
+        const void* ptrs[] = {g->s, g->dout, g->dresidual_out, g->dx};
+        const int64_t rs[] = {g->s_row_stride, g->dout_row_stride, g->dresidual_out_row_stride, g->dx_row_stride};
+        for (int i = 0; i < 4; ++i) {
+            if (!ptrs[i]) continue;
+            if (!aligned(ptrs[i], es)) return fail(SS_ERR_INVALID, "s / dout / dresidual_out / dx is misaligned");
+            if (rs[i] < 0) return fail(SS_ERR_INVALID, "negative row stride");
+        }
+        if (!aligned(g->rstd, 4)) return fail(SS_ERR_INVALID, "rstd is misaligned");
+    }
+    hipError_t e = ss::rmsnorm_launch(nullptr, g, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "rmsnorm backward launch failed: %s", hipGetErrorString(e));
     return ok();
 }
 

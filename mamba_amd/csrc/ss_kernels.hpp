@@ -68,6 +68,14 @@ hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int itype, hipStream_t stream);
 // causal depthwise conv1d (+ SiLU); g == nullptr: forward, else backward
 hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, hipStream_t stream);
+// RMSNorm (+ residual); g == nullptr: forward, else backward (two kernels:
+// per-workgroup dweight rows into g->workspace, then their fixed-order sum)
+hipError_t rmsnorm_launch(const ss_rmsnorm_args* a, const ss_rmsnorm_bwd_args* g, hipStream_t stream);
+// backward workgroups (= fp32 dweight rows of workspace) for `rows` rows
+int64_t rmsnorm_bwd_parts(int64_t rows);
+constexpr int64_t kRmsNormMaxParts = 512;
+// the backward keeps one fp32 column sum per element of a row in LDS
+constexpr int64_t kRmsNormMaxBwdDim = 16384;
 // base name of the kernel template launch_fwd / launch_bwd picks for p
 const char* fwd_kernel_name(const FwdParams& p);
 const char* bwd_kernel_name(const BwdParams& p);

@@ -3,8 +3,10 @@
 Mirrors models/causal_lm.py:7-62 (CausalLMConfig, Block, CausalLM): token
 embedding, ``num_layers`` pre-norm residual blocks RMSNorm -> MambaSimple ->
 dropout, a final RMSNorm and an lm_head tied to the embedding.  The
-state_dict keys are the reference's.  ``generate`` is a stub in the
-reference (:61-62) and is not provided here.
+state_dict keys are the reference's.  On a ROCm device each block's
+residual add is fused into the next RMSNorm kernel (the residual stream is
+carried between blocks instead of being added at the end of each one).
+``generate`` is a stub in the reference (:61-62) and is not provided here.
 """
 from dataclasses import dataclass
 
@@ -53,9 +55,24 @@ class CausalLM(nn.Module):
         if config.tie_embeddings:
             self.lm_head.weight = self.embedding.weight
 
+    def _fused_residual(self, hidden_states):
+        return hidden_states.is_cuda and self.norm.use_fast_path and all(
+            layer.norm.use_fast_path for layer in self.layers)
+
     def forward(self, input_ids):
         hidden_states = self.embedding(input_ids)
-        for layer in self.layers:
-            hidden_states = layer(hidden_states)
-        hidden_states = self.norm(hidden_states)
+        if self._fused_residual(hidden_states):
+            # the same function as the loop below, with each block's residual
+            # add moved into the next RMSNorm kernel: block i computes
+            # h_{i+1} = dropout(mamba(norm(h_i))) + h_i, and norm(h_{i+1}) is
+            # one pass over (dropout(mamba(...)), h_i) that also writes h_{i+1}
+            residual = None
+            for layer in self.layers:
+                normed, residual = layer.norm(hidden_states, residual=residual, prenorm=True)
+                hidden_states = layer.dropout(layer.mamba(normed))
+            hidden_states = self.norm(hidden_states, residual=residual)
+        else:
+            for layer in self.layers:
+                hidden_states = layer(hidden_states)
+            hidden_states = self.norm(hidden_states)
         return self.lm_head(hidden_states)

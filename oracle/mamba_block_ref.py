@@ -17,7 +17,8 @@ import this module; the product path (mamba_amd) never does.
 * ``mamba_simple_ref`` is MambaSimple.forward from a dict of the reference
   module's parameters (the same names), and ``rms_norm_ref`` /
   ``causal_lm_ref`` restate modules/rms_norm.py:19-31 and
-  models/causal_lm.py:30-59.
+  models/causal_lm.py:30-59; ``add_rms_norm_ref`` is a block's residual add
+  (models/causal_lm.py:31-35) followed by the next RMSNorm.
 """
 import torch
 import torch.nn.functional as F
@@ -90,6 +91,13 @@ def rms_norm_ref(x, weight, eps=1e-6):
     xf = x.double() if x.dtype == torch.float64 else x.float()
     out = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + weight.to(xf.dtype))
     return out.to(x.dtype)
+
+
+def add_rms_norm_ref(x, residual, weight, eps=1e-6):
+    """The residual add that ends a block (models/causal_lm.py:31-35, ``hidden_states += residual``
+    in x's dtype) followed by the next block's RMSNorm: returns (rms_norm_ref(s), s), s = x + residual."""
+    s = x if residual is None else x + residual
+    return rms_norm_ref(s, weight, eps), s
 
 
 def causal_lm_ref(p, input_ids, num_layers, state_dim=16, eps=1e-6):

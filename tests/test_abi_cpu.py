@@ -59,7 +59,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 4
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 5
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -80,7 +80,8 @@ int main(void) {
 
 def test_struct_layout_matches_c_compiler(nat, lib, tmp_path):
     structs = ((nat.FwdArgs, "ss_fwd_args"), (nat.BwdArgs, "ss_bwd_args"),
-               (nat.Conv1dArgs, "ss_conv1d_args"), (nat.Conv1dBwdArgs, "ss_conv1d_bwd_args"))
+               (nat.Conv1dArgs, "ss_conv1d_args"), (nat.Conv1dBwdArgs, "ss_conv1d_bwd_args"),
+               (nat.RmsNormArgs, "ss_rmsnorm_args"), (nat.RmsNormBwdArgs, "ss_rmsnorm_bwd_args"))
     fields = [f"F({name}, {n})" for T, name in structs for n, _ in T._fields_]
     fields += [f'printf("sizeof {name} %zu\\n", sizeof({name}));' for _, name in structs]
     src = tmp_path / "probe.c"
@@ -346,3 +347,87 @@ def test_workspace_query(nat, lib):
     # 5120 channels: 320 blocks, capped at 16 slices
     b = valid_bwd(nat, batch=1, dim=5120, seqlen=64)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 16 * (16 * 64) * 4
+
+
+# --------------------------------------------------------------------- RMSNorm --
+def valid_norm(nat, rows=4, dim=768, dtype=None):
+    a = nat.RmsNormArgs()
+    a.rows, a.dim = rows, dim
+    a.dtype = nat.SS_BF16 if dtype is None else dtype
+    a.w_dtype, a.eps = a.dtype, 1e-6
+    a.x_row_stride = a.residual_row_stride = a.out_row_stride = a.residual_out_row_stride = dim
+    a.x, a.residual, a.weight, a.out, a.residual_out, a.rstd = (FAKE + 65536 * i for i in range(6))
+    return a
+
+
+def valid_norm_bwd(nat, rows=4, dim=768, dtype=None):
+    g = nat.RmsNormBwdArgs()
+    g.rows, g.dim = rows, dim
+    g.dtype = nat.SS_BF16 if dtype is None else dtype
+    g.w_dtype = g.dtype
+    g.s_row_stride = g.dout_row_stride = g.dresidual_out_row_stride = g.dx_row_stride = dim
+    g.s, g.weight, g.rstd, g.dout, g.dresidual_out, g.dx, g.dweight, g.workspace = (
+        FAKE + 65536 * i for i in range(8))
+    g.workspace_bytes = 1 << 30
+    return g
+
+
+@pytest.mark.parametrize("case", ["neg_rows", "dtype", "w_dtype", "null_x", "null_weight", "misaligned_out",
+                                  "neg_stride", "neg_eps"])
+def test_rmsnorm_fwd_rejects(nat, lib, case):
+    a = valid_norm(nat)
+    if case == "neg_rows":
+        a.rows = -1
+    elif case == "dtype":
+        a.dtype = 7
+    elif case == "w_dtype":
+        a.w_dtype = nat.SS_F16              # neither the row dtype (bf16) nor fp32
+    elif case == "null_x":
+        a.x = None
+    elif case == "null_weight":
+        a.weight = None
+    elif case == "misaligned_out":
+        a.out = FAKE + 1
+    elif case == "neg_stride":
+        a.residual_row_stride = -768
+    elif case == "neg_eps":
+        a.eps = -1.0
+    rc = lib.ss_rmsnorm_fwd(ctypes.byref(a), None)
+    assert rc in (nat.SS_ERR_INVALID, nat.SS_ERR_UNSUPPORTED)
+    assert lib.ss_last_error().decode()
+
+
+def test_rmsnorm_empty_and_bwd_rejects(nat, lib):
+    # no rows or no columns: nothing to launch
+    assert lib.ss_rmsnorm_fwd(ctypes.byref(valid_norm(nat, rows=0)), None) == nat.SS_OK
+    assert lib.ss_rmsnorm_fwd(ctypes.byref(valid_norm(nat, dim=0)), None) == nat.SS_OK
+    assert lib.ss_rmsnorm_bwd(ctypes.byref(valid_norm_bwd(nat, dim=0)), None) == nat.SS_OK
+    g = valid_norm_bwd(nat)
+    g.workspace = None
+    assert lib.ss_rmsnorm_bwd(ctypes.byref(g), None) == nat.SS_ERR_INVALID
+    assert "workspace" in lib.ss_last_error().decode()
+    g = valid_norm_bwd(nat)
+    g.workspace_bytes = 16
+    assert lib.ss_rmsnorm_bwd(ctypes.byref(g), None) == nat.SS_ERR_INVALID
+    g = valid_norm_bwd(nat, dim=20000)
+    assert lib.ss_rmsnorm_bwd(ctypes.byref(g), None) == nat.SS_ERR_UNSUPPORTED
+    g = valid_norm_bwd(nat)
+    g.rstd = None
+    assert lib.ss_rmsnorm_bwd(ctypes.byref(g), None) == nat.SS_ERR_INVALID
+    g = valid_norm_bwd(nat)
+    g.dweight = None
+    assert lib.ss_rmsnorm_bwd(ctypes.byref(g), None) == nat.SS_ERR_INVALID
+
+
+def test_rmsnorm_workspace_query(lib):
+    # one fp32 row of dim column sums per backward workgroup (8 rows each, at most 512 workgroups)
+    assert lib.ss_rmsnorm_bwd_workspace_bytes(32768, 768) == 512 * 768 * 4
+    assert lib.ss_rmsnorm_bwd_workspace_bytes(20, 768) == 3 * 768 * 4
+    assert lib.ss_rmsnorm_bwd_workspace_bytes(0, 768) == 0
+    assert lib.ss_rmsnorm_bwd_workspace_bytes(-1, 768) == -1
+
+
+def test_rmsnorm_python_boundary_refuses_cpu_tensors():
+    from mamba_amd.ops.rms_norm import rms_norm_fn
+    with pytest.raises(ValueError, match="no CPU path"):
+        rms_norm_fn(torch.randn(2, 8), torch.zeros(8))

@@ -93,6 +93,41 @@ def test_rms_norm_module_matches_oracle():
     assert torch.allclose(n(x)[0, 0], -(1 + n.weight.detach()), rtol=1e-5, atol=1e-5)
 
 
+def test_rms_norm_oracle_matches_torch_rms_norm():
+    # a library routine: F.rms_norm(x, (dim,), weight, eps) = x * rsqrt(mean(x^2) + eps) * weight
+    from oracle.mamba_block_ref import add_rms_norm_ref
+    torch.manual_seed(3)
+    w = torch.empty(48).uniform_(-0.5, 0.5)
+    x = torch.randn(7, 48) * 3
+    want = torch.nn.functional.rms_norm(x, (48,), weight=1 + w, eps=1e-6)
+    assert torch.allclose(rms_norm_ref(x, w), want, rtol=1e-6, atol=1e-6)
+    # scale invariance (eps negligible) and unit mean square with weight 0
+    assert torch.allclose(rms_norm_ref(x * 37.0, w), rms_norm_ref(x, w), rtol=1e-5, atol=1e-5)
+    assert torch.allclose(rms_norm_ref(x, torch.zeros(48)).pow(2).mean(-1), torch.ones(7), rtol=1e-5)
+    # bf16: normalised in fp32 and rounded once (not a bf16 computation)
+    xb = x.bfloat16()
+    want_b = torch.nn.functional.rms_norm(xb.float(), (48,), weight=1 + w, eps=1e-6).bfloat16()
+    assert torch.equal(rms_norm_ref(xb, w), want_b)
+    # residual add: s is the dtype's sum (rounded once), the norm is of s
+    r = torch.randn(7, 48).bfloat16()
+    out, s = add_rms_norm_ref(xb, r, w)
+    assert torch.equal(s, (xb.float() + r.float()).bfloat16())
+    assert torch.equal(out, rms_norm_ref(s, w))
+    out0, s0 = add_rms_norm_ref(xb, None, w)
+    assert s0 is xb and torch.equal(out0, rms_norm_ref(xb, w))
+
+
+def test_rms_norm_oracle_gradient_matches_finite_differences():
+    # the GPU backward is checked against autograd of rms_norm_ref in float64;
+    # gradcheck pins that autograd against central differences
+    from oracle.mamba_block_ref import add_rms_norm_ref
+    torch.manual_seed(4)
+    x = torch.randn(3, 10, dtype=torch.float64, requires_grad=True)
+    r = torch.randn(3, 10, dtype=torch.float64, requires_grad=True)
+    w = (0.3 * torch.randn(10, dtype=torch.float64)).requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda a, b, c: add_rms_norm_ref(a, b, c), (x, r, w))
+
+
 def test_state_dict_keys_are_the_references():
     # parameter names and shapes of models/causal_lm.py:21-51 and modules/mamba_simple.py:35-85
     cfg = CausalLMConfig(vocab_size=50, model_dim=24, state_dim=16, conv_kernel=4, num_layers=2)

@@ -26,7 +26,10 @@ SelectiveScanFn, the residual added after each block).
   add_rmsnorm_r32768_d768_bf16   the fused residual add + RMSNorm between
       two blocks of that model (32768 rows of 768, bf16) forward + backward;
       ``value`` is algorithmic GB/s, with a roofline line and a CPU baseline
-      as for the scan.
+      as for the scan;
+  causal_lm_24x768_b16_decode_bf16   single-token decode of that model for 16
+      sequences after a 128-token prompt; ``value`` is tokens per second of
+      the step replayed as one HIP graph (the eager step beside it).
 
 ``--calibrate-copy MIB`` instead times a plain device-to-device copy of MIB
 MiB (torch's copy kernel); under ``rocprofv3 --pmc FETCH_SIZE`` /
@@ -183,6 +186,58 @@ def norm_cpu_baseline(rows, dim, dtype_name, sample_rows=None, reps=3):
             "sample": f"{sample_rows} of {rows} rows, dim {dim}, {dtype_name}; median of {reps}",
             "seconds_per_sample": round(t, 4)}
 
+DECODE_WORKLOADS = {
+    # name: (batch, prompt, d_model, layers, vocab)
+    "causal_lm_24x768_b16_decode_bf16": (16, 128, 768, 24, 50280),
+}
+
+
+def bench_decode(args):
+    """CausalLM single-token decode (after a prompt prefill); one JSON line.
+    ``value`` is tokens per second of the graph-replayed step; the eager
+    step (one launch per kernel from Python) is reported beside it."""
+    import torch
+    from mamba_amd.models import CausalLM, CausalLMConfig, GraphedStep
+
+    batch, prompt, d_model, layers, vocab = DECODE_WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.manual_seed(1006)
+    cfg = CausalLMConfig(vocab_size=vocab, model_dim=d_model, state_dim=16, conv_kernel=4,
+                         expansion_factor=2, num_layers=layers)
+    model = CausalLM(cfg, device=dev, dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, vocab, (batch, prompt), device=dev)
+    cache = model.allocate_inference_cache(batch)
+    with torch.no_grad():
+        model(ids, inference_cache=cache)
+    tok = ids[:, -1].clone()
+
+    def timed(fn, n):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    with torch.no_grad():
+        ms_eager = timed(lambda: model.step(tok, cache), args.steps)
+    graphed = GraphedStep(model, cache, batch)
+    ms_graph = timed(lambda: graphed(tok), args.steps)
+    line = {"metric": f"CausalLM decode tokens/s, {layers} layers, d_model {d_model}, batch {batch}",
+            "value": round(batch / (ms_graph * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_graph, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic, random init",
+            "config": {"workload": args.workload, "batch": batch, "prompt": prompt, "d_model": d_model,
+                       "layers": layers, "vocab": vocab, "dtype": "bf16 (A, D fp32, state fp32)"},
+            "eager_step": {"ms_per_step": round(ms_eager, 4), "value": round(batch / (ms_eager * 1e-3), 1),
+                           "what": "the same step launched kernel by kernel from Python"},
+            "reference": "no decode path (CausalLM.generate is a stub)"}
+    print(json.dumps(line), flush=True)
+
 
 def bench_model(args):
     """Mamba block fwd+bwd or CausalLM forward; one JSON line."""
@@ -335,7 +390,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default=DEFAULT,
-                    choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(NORM_WORKLOADS))
+                    choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(NORM_WORKLOADS)
+                    + sorted(DECODE_WORKLOADS))
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-ref-order", action="store_true",
@@ -357,6 +413,9 @@ def main():
         return
     if args.workload in NORM_WORKLOADS:
         bench_norm(args)
+        return
+    if args.workload in DECODE_WORKLOADS:
+        bench_decode(args)
         return
 
     import torch

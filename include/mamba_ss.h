@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 5
+#define SS_ABI_VERSION 6
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -251,6 +251,70 @@ typedef struct ss_rmsnorm_bwd_args {
 int ss_rmsnorm_fwd(const ss_rmsnorm_args* a, void* stream);
 int ss_rmsnorm_bwd(const ss_rmsnorm_bwd_args* a, void* stream);
 int64_t ss_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim);
+
+/* ------------------------------------------------------------------------
+ * Single-token decode.  The reference has no decode path (CausalLM.generate
+ * is a stub, models/causal_lm.py:61-62); these advance, by one token, the
+ * recurrences that ss_fwd (forward_kernel.cu:216-293) and the block's conv
+ * (modules/mamba_simple.py:40-47,100-101) compute over a sequence, from a
+ * state the caller keeps between tokens.
+ *
+ * ss_state_update, per (batch b, channel d), group g = d / (dim / n_groups):
+ *   dt = delta[b, d] (+ delta_bias[d]), softplus if delta_softplus
+ *   state[b, d, n] <- exp(dt * A[d, n]) * state[b, d, n] + dt * x[b, d] * B[b, g, n]
+ *   out[b, d] = sum_n C[b, g, n] * state[b, d, n] (+ D[d] * x[b, d]) (* silu(z[b, d]))
+ * state: fp32 (batch, dim, dstate), updated in place; x, delta, z, out:
+ * (batch, dim); B, C: (batch, n_groups, dstate), element type itype; A:
+ * fp32 (dim, dstate); D, delta_bias: fp32 (dim).  All strides free.
+ * ------------------------------------------------------------------------ */
+typedef struct ss_state_update_args {
+    int64_t batch, dim, dstate, n_groups;
+    int32_t itype;                       /* enum ss_dtype */
+    int32_t has_D, has_z, has_delta_bias, delta_softplus;
+    int32_t pad_;
+    int64_t state_batch_stride, state_dim_stride, state_dstate_stride;
+    int64_t x_batch_stride, x_dim_stride;
+    int64_t delta_batch_stride, delta_dim_stride;
+    int64_t z_batch_stride, z_dim_stride;
+    int64_t out_batch_stride, out_dim_stride;
+    int64_t A_dim_stride, A_dstate_stride;
+    int64_t B_batch_stride, B_group_stride, B_dstate_stride;
+    int64_t C_batch_stride, C_group_stride, C_dstate_stride;
+    float* state;
+    const void* x;
+    const void* delta;
+    const float* A;
+    const void* B;
+    const void* C;
+    const float* D;                      /* may be NULL iff !has_D */
+    const void* z;                       /* may be NULL iff !has_z */
+    const float* delta_bias;             /* may be NULL iff !has_delta_bias */
+    void* out;
+} ss_state_update_args;
+
+/* ss_conv1d_update, per (batch b, channel d), state = the last width inputs:
+ *   conv_state[b, d, :] <- (conv_state[b, d, 1:], x[b, d])
+ *   out[b, d] = act(bias[d] + sum_k weight[d, k] * conv_state[b, d, k])
+ * x, out: (batch, dim); conv_state: (batch, dim, width), element type itype,
+ * updated in place; weight fp32 (dim, width); bias fp32 (dim).  Strides free. */
+typedef struct ss_conv1d_update_args {
+    int64_t batch, dim, width;           /* width 1..4 */
+    int32_t itype;                       /* enum ss_dtype */
+    int32_t has_bias, silu;
+    int32_t pad_;
+    int64_t x_batch_stride, x_dim_stride;
+    int64_t out_batch_stride, out_dim_stride;
+    int64_t state_batch_stride, state_dim_stride, state_width_stride;
+    int64_t w_dim_stride, w_width_stride;
+    const void* x;
+    void* conv_state;
+    const float* weight;
+    const float* bias;                   /* may be NULL iff !has_bias */
+    void* out;
+} ss_conv1d_update_args;
+
+int ss_state_update(const ss_state_update_args* a, void* stream);
+int ss_conv1d_update(const ss_conv1d_update_args* a, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
@@ -21,6 +21,7 @@ EXPORTED = (
     "ss_fwd_kernel_name", "ss_bwd_kernel_name",
     "ss_fwd", "ss_bwd", "ss_conv1d_fwd", "ss_conv1d_bwd",
     "ss_rmsnorm_fwd", "ss_rmsnorm_bwd", "ss_rmsnorm_bwd_workspace_bytes",
+    "ss_state_update", "ss_conv1d_update",
 )
 
 _i64, _i32, _p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
@@ -100,6 +101,36 @@ class RmsNormBwdArgs(ctypes.Structure):
     ]
 
 
+class StateUpdateArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("dim", _i64), ("dstate", _i64), ("n_groups", _i64),
+        ("itype", _i32), ("has_D", _i32), ("has_z", _i32), ("has_delta_bias", _i32),
+        ("delta_softplus", _i32), ("pad_", _i32),
+        ("state_batch_stride", _i64), ("state_dim_stride", _i64), ("state_dstate_stride", _i64),
+        ("x_batch_stride", _i64), ("x_dim_stride", _i64),
+        ("delta_batch_stride", _i64), ("delta_dim_stride", _i64),
+        ("z_batch_stride", _i64), ("z_dim_stride", _i64),
+        ("out_batch_stride", _i64), ("out_dim_stride", _i64),
+        ("A_dim_stride", _i64), ("A_dstate_stride", _i64),
+        ("B_batch_stride", _i64), ("B_group_stride", _i64), ("B_dstate_stride", _i64),
+        ("C_batch_stride", _i64), ("C_group_stride", _i64), ("C_dstate_stride", _i64),
+        ("state", _p), ("x", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
+        ("D", _p), ("z", _p), ("delta_bias", _p), ("out", _p),
+    ]
+
+
+class Conv1dUpdateArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("dim", _i64), ("width", _i64),
+        ("itype", _i32), ("has_bias", _i32), ("silu", _i32), ("pad_", _i32),
+        ("x_batch_stride", _i64), ("x_dim_stride", _i64),
+        ("out_batch_stride", _i64), ("out_dim_stride", _i64),
+        ("state_batch_stride", _i64), ("state_dim_stride", _i64), ("state_width_stride", _i64),
+        ("w_dim_stride", _i64), ("w_width_stride", _i64),
+        ("x", _p), ("conv_state", _p), ("weight", _p), ("bias", _p), ("out", _p),
+    ]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -135,6 +166,10 @@ def load():
         lib.ss_conv1d_fwd.restype = ctypes.c_int
         lib.ss_conv1d_bwd.argtypes = [ctypes.POINTER(Conv1dBwdArgs), _p]
         lib.ss_conv1d_bwd.restype = ctypes.c_int
+        lib.ss_state_update.argtypes = [ctypes.POINTER(StateUpdateArgs), _p]
+        lib.ss_state_update.restype = ctypes.c_int
+        lib.ss_conv1d_update.argtypes = [ctypes.POINTER(Conv1dUpdateArgs), _p]
+        lib.ss_conv1d_update.restype = ctypes.c_int
         lib.ss_rmsnorm_fwd.argtypes = [ctypes.POINTER(RmsNormArgs), _p]
         lib.ss_rmsnorm_fwd.restype = ctypes.c_int
         lib.ss_rmsnorm_bwd.argtypes = [ctypes.POINTER(RmsNormBwdArgs), _p]

@@ -393,6 +393,68 @@ int ss_conv1d_bwd(const ss_conv1d_bwd_args* g, void* stream) {
     return ok();
 }
 
+int ss_state_update(const ss_state_update_args* a, void* stream) {
+    if (!a) return fail(SS_ERR_INVALID, "null argument block");
+    if (a->batch < 0 || a->dim < 0 || a->dstate < 0 || a->n_groups < 1)
+        return fail(SS_ERR_INVALID, "bad size (batch=%lld dim=%lld dstate=%lld n_groups=%lld)", (long long)a->batch,
+                    (long long)a->dim, (long long)a->dstate, (long long)a->n_groups);
+    if (a->itype != SS_F32 && a->itype != SS_BF16 && a->itype != SS_F16)
+        return fail(SS_ERR_INVALID, "unknown itype %d", a->itype);
+    if (a->dim % a->n_groups != 0)
+        return fail(SS_ERR_INVALID, "dim=%lld is not a multiple of n_groups=%lld", (long long)a->dim,
+                    (long long)a->n_groups);
+    if (a->batch == 0 || a->dim == 0) return ok();
+    if (a->batch > int64_t(UINT32_MAX) / 2 / (a->dim > 0 ? a->dim : 1))
+        return fail(SS_ERR_UNSUPPORTED, "batch * dim is too large");
+    const size_t es = elem_size(a->itype);
+    if (!a->state || !a->x || !a->delta || !a->out || (a->dstate > 0 && (!a->A || !a->B || !a->C)))
+        return fail(SS_ERR_INVALID, "state / x / delta / A / B / C / out is NULL");
+    if ((a->has_D && !a->D) || (a->has_z && !a->z) || (a->has_delta_bias && !a->delta_bias))
+        return fail(SS_ERR_INVALID, "D / z / delta_bias is NULL but flagged present");
+    const void* p2[] = {a->x, a->delta, a->B, a->C, a->has_z ? a->z : nullptr, a->out};
+    for (const void* q : p2)
+        if (q && !aligned(q, es)) return fail(SS_ERR_INVALID, "x / delta / B / C / z / out is misaligned");
+    const void* p4[] = {a->state, a->A, a->has_D ? a->D : nullptr, a->has_delta_bias ? a->delta_bias : nullptr};
+    for (const void* q : p4)
+        if (q && !aligned(q, 4)) return fail(SS_ERR_INVALID, "state / A / D / delta_bias is misaligned");
+    const int64_t st[] = {a->state_batch_stride, a->state_dim_stride, a->state_dstate_stride, a->x_batch_stride,
+                          a->x_dim_stride, a->delta_batch_stride, a->delta_dim_stride, a->z_batch_stride,
+                          a->z_dim_stride, a->out_batch_stride, a->out_dim_stride, a->A_dim_stride,
+                          a->A_dstate_stride, a->B_batch_stride, a->B_group_stride, a->B_dstate_stride,
+                          a->C_batch_stride, a->C_group_stride, a->C_dstate_stride};
+    for (int64_t v : st)
+        if (v < 0) return fail(SS_ERR_INVALID, "negative stride");
+    hipError_t e = ss::state_update_launch(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "state update launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int ss_conv1d_update(const ss_conv1d_update_args* a, void* stream) {
+    if (!a) return fail(SS_ERR_INVALID, "null argument block");
+    if (a->batch < 0 || a->dim < 0)
+        return fail(SS_ERR_INVALID, "negative size (batch=%lld dim=%lld)", (long long)a->batch, (long long)a->dim);
+    if (a->width < 1 || a->width > 4) return fail(SS_ERR_UNSUPPORTED, "width=%lld outside [1, 4]", (long long)a->width);
+    if (a->itype != SS_F32 && a->itype != SS_BF16 && a->itype != SS_F16)
+        return fail(SS_ERR_INVALID, "unknown itype %d", a->itype);
+    if (a->batch == 0 || a->dim == 0) return ok();
+    if (a->batch > int64_t(UINT32_MAX) / 2 / a->dim) return fail(SS_ERR_UNSUPPORTED, "batch * dim is too large");
+    const size_t es = elem_size(a->itype);
+    if (!a->x || !a->conv_state || !a->weight || !a->out || (a->has_bias && !a->bias))
+        return fail(SS_ERR_INVALID, "x / conv_state / weight / bias / out is NULL");
+    if (!aligned(a->x, es) || !aligned(a->conv_state, es) || !aligned(a->out, es))
+        return fail(SS_ERR_INVALID, "x / conv_state / out is misaligned");
+    if (!aligned(a->weight, 4) || (a->has_bias && !aligned(a->bias, 4)))
+        return fail(SS_ERR_INVALID, "weight / bias is misaligned");
+    const int64_t st[] = {a->x_batch_stride, a->x_dim_stride, a->out_batch_stride, a->out_dim_stride,
+                          a->state_batch_stride, a->state_dim_stride, a->state_width_stride,
+                          a->w_dim_stride, a->w_width_stride};
+    for (int64_t v : st)
+        if (v < 0) return fail(SS_ERR_INVALID, "negative stride");
+    hipError_t e = ss::conv_update_launch(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "conv1d update launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
 int64_t ss_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim) {
     if (rows < 0 || dim < 0) {
         fail(SS_ERR_INVALID, "negative size (rows=%lld dim=%lld)", (long long)rows, (long long)dim);

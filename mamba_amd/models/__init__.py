@@ -1,3 +1,3 @@
-from .causal_lm import Block, CausalLM, CausalLMConfig
+from .causal_lm import Block, CausalLM, CausalLMConfig, GraphedStep
 
-__all__ = ["Block", "CausalLM", "CausalLMConfig"]
+__all__ = ["Block", "CausalLM", "CausalLMConfig", "GraphedStep"]

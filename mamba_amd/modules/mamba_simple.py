@@ -12,13 +12,20 @@ forward paths compute the same function:
 * ``use_fast_path=False``: the reference's own sequence of PyTorch ops
   around ``SelectiveScanFn`` (modules/mamba_simple.py:95-149), with the scan
   on the HIP library.
+
+Decoding (absent in the reference, whose CausalLM.generate is a stub):
+``allocate_inference_cache`` gives a (conv_state, ssm_state) pair,
+``forward(hidden, inference_cache=...)`` fills it from a whole prompt, and
+``step`` advances the block by one token on the HIP state-update kernels.
 """
 import math
 
 import torch
 import torch.nn as nn
 
-from ..ops.selective_scan_interface import SelectiveScanFn, mamba_inner_fn
+from ..ops.causal_conv1d import causal_conv1d_update
+from ..ops.selective_scan_interface import SelectiveScanFn, mamba_inner_fn, mamba_inner_prefill
+from ..ops.selective_state_update import selective_state_update
 
 
 class MambaSimple(nn.Module):
@@ -78,13 +85,21 @@ class MambaSimple(nn.Module):
         self.D = nn.Parameter(torch.ones(self.inner_dim, device=device))
         self.output_proj = nn.Linear(self.inner_dim, model_dim, bias=bias, **fk)
 
-    def forward(self, hidden_states):
-        """(batch, seqlen, model_dim) -> (batch, seqlen, model_dim)."""
+    def forward(self, hidden_states, inference_cache=None):
+        """(batch, seqlen, model_dim) -> (batch, seqlen, model_dim).
+
+        With ``inference_cache`` (a (conv_state, ssm_state) pair from
+        allocate_inference_cache) the pair is left holding the state after the
+        last token, for ``step``; this needs the fast path on a ROCm device."""
+        if inference_cache is not None:
+            if not (self.use_fast_path and hidden_states.is_cuda):
+                raise ValueError("MambaSimple: filling an inference cache needs the fast path on a ROCm device")
+            return self._forward_fast(hidden_states, inference_cache)
         if self.use_fast_path and hidden_states.is_cuda:
             return self._forward_fast(hidden_states)
         return self._forward_reference(hidden_states)
 
-    def _forward_fast(self, hidden_states):
+    def _forward_fast(self, hidden_states, inference_cache=None):
         batch, seqlen, _ = hidden_states.shape
         # xz = W_in @ h^T: (2 * inner_dim, batch * seqlen), viewed as (batch, 2 * inner_dim, seqlen)
         xz = self.input_proj.weight @ hidden_states.reshape(batch * seqlen, self.model_dim).t()
@@ -92,9 +107,59 @@ class MambaSimple(nn.Module):
             xz = xz + self.input_proj.bias[:, None]
         xz = xz.view(2 * self.inner_dim, batch, seqlen).permute(1, 0, 2)
         A = -torch.exp(self.log_A.float())
-        return mamba_inner_fn(xz, self.short_conv.weight, self.short_conv.bias, self.ssm_param_proj.weight,
-                              self.delta_proj.weight, self.output_proj.weight, self.output_proj.bias, A,
-                              D=self.D.float(), delta_bias=self.delta_proj.bias.float(), delta_softplus=True)
+        args = (xz, self.short_conv.weight, self.short_conv.bias, self.ssm_param_proj.weight,
+                self.delta_proj.weight, self.output_proj.weight, self.output_proj.bias, A)
+        kw = dict(D=self.D.float(), delta_bias=self.delta_proj.bias.float(), delta_softplus=True)
+        if inference_cache is not None:
+            conv_state, ssm_state = inference_cache
+            return mamba_inner_prefill(*args, **kw, conv_state=conv_state, ssm_state=ssm_state)
+        return mamba_inner_fn(*args, **kw)
+
+    def allocate_inference_cache(self, batch_size, dtype=None, device=None):
+        """(conv_state (batch, inner_dim, conv_kernel) in the weights' dtype, ssm_state
+        (batch, inner_dim, state_dim) fp32), zero: the state before a sequence starts."""
+        device = self.input_proj.weight.device if device is None else device
+        dtype = self.input_proj.weight.dtype if dtype is None else dtype
+        conv_state = torch.zeros(batch_size, self.inner_dim, self.conv_kernel, dtype=dtype, device=device)
+        ssm_state = torch.zeros(batch_size, self.inner_dim, self.state_dim, dtype=torch.float32, device=device)
+        return conv_state, ssm_state
+
+    def step(self, hidden_states, conv_state, ssm_state):
+        """One token: hidden_states (batch, model_dim) or (batch, 1, model_dim) -> the same
+        shape; conv_state and ssm_state are advanced in place."""
+        squeeze = hidden_states.dim() == 3
+        h = hidden_states.reshape(-1, self.model_dim)
+        xz = torch.nn.functional.linear(h, self.input_proj.weight, self.input_proj.bias)   # (batch, 2 * inner)
+        x, z = xz[:, :self.inner_dim], xz[:, self.inner_dim:]
+        A, D, dt_bias, conv_w, conv_b = self._decode_params()
+        x = causal_conv1d_update(x, conv_state, conv_w, conv_b, "silu")
+        x_db = torch.nn.functional.linear(x, self.ssm_param_proj.weight)             # (batch, R + 2N)
+        R, N = self.delta_rank, self.state_dim
+        dt = torch.nn.functional.linear(x_db[:, :R], self.delta_proj.weight)         # bias goes in the update
+        y = selective_state_update(ssm_state, x, dt, A, x_db[:, R:R + N], x_db[:, R + N:], D, z=z,
+                                   dt_bias=dt_bias, dt_softplus=True)
+        out = self.output_proj(y)
+        return out.unsqueeze(1) if squeeze else out
+
+    def _decode_params(self):
+        """A = -exp(log_A), D, the delta bias and the conv weight / bias in fp32, computed
+        once and reused by every step until one of those parameters changes (their
+        version counters move on any in-place update, an optimizer step included)."""
+        params = [self.log_A, self.D, self.delta_proj.bias, self.short_conv.weight]
+        if self.short_conv.bias is not None:
+            params.append(self.short_conv.bias)
+        key = tuple((p.data_ptr(), p._version) for p in params)
+        cached = getattr(self, "_decode_cache", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                w = self.short_conv.weight
+                vals = (-torch.exp(self.log_A.float()), self.D.float().contiguous(),
+                        self.delta_proj.bias.float().contiguous(),
+                        w.reshape(w.shape[0], w.shape[-1]).float().contiguous(),
+                        self.short_conv.bias.float().contiguous() if self.short_conv.bias is not None else None)
+            self._decode_cache = (key, vals)
+            cached = self._decode_cache
+        return cached[1]
 
     def _forward_reference(self, hidden_states):
         # the reference's op sequence (modules/mamba_simple.py:95-149)

@@ -117,3 +117,33 @@ class CausalConv1dFn(torch.autograd.Function):
 def causal_conv1d_fn(x, weight, bias=None, activation=None):
     """Causal depthwise conv1d with optional SiLU; see the module docstring."""
     return CausalConv1dFn.apply(x, weight, bias, activation)
+
+
+def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None, out=None):
+    """One decode step of the causal conv: conv_state (batch, dim, width) holds the
+    last width inputs; it is shifted by one with x (batch, dim) appended, in place,
+    and out[b, d] = act(bias[d] + sum_k weight[d, k] * conv_state[b, d, k]) is
+    returned in x's dtype.  Equals step t of causal_conv1d_fn when conv_state
+    held inputs t - width .. t - 1 (zeros before the sequence start)."""
+    lib = nat.load()
+    silu = _silu_flag(activation)
+    _require(x.dim() == 2 and x.device.type == "cuda", "x must be (batch, dim) on a ROCm GPU device (no CPU path)")
+    _require(x.dtype in _ITYPES, f"unsupported dtype {x.dtype}")
+    batch, dim = x.shape
+    w, b = _params32(weight, bias, dim, x.device)
+    _require(conv_state.shape == (batch, dim, w.shape[1]) and conv_state.dtype == x.dtype
+             and conv_state.device == x.device,
+             f"conv_state must be ({batch}, {dim}, {w.shape[1]}) of x's dtype, got {tuple(conv_state.shape)}")
+    if out is None:
+        out = torch.empty(batch, dim, dtype=x.dtype, device=x.device)
+    a = nat.Conv1dUpdateArgs()
+    a.batch, a.dim, a.width = batch, dim, w.shape[1]
+    a.itype, a.has_bias, a.silu = _ITYPES[x.dtype], int(b is not None), int(silu)
+    a.x_batch_stride, a.x_dim_stride = x.stride(0), x.stride(1)
+    a.out_batch_stride, a.out_dim_stride = out.stride(0), out.stride(1)
+    a.state_batch_stride, a.state_dim_stride, a.state_width_stride = conv_state.stride()
+    a.w_dim_stride, a.w_width_stride = w.stride(0), w.stride(1)
+    a.x, a.conv_state, a.weight, a.bias, a.out = _ptr(x), _ptr(conv_state), _ptr(w), _ptr(b), _ptr(out)
+    with torch.cuda.device(x.device):
+        nat.check(lib.ss_conv1d_update(ctypes.byref(a), _stream(x.device)), "causal_conv1d_update")
+    return out

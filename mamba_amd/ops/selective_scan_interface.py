@@ -145,6 +145,74 @@ def _cm_view(buf, batch, L):
     return buf.view(buf.shape[0], batch, L).permute(1, 0, 2)
 
 
+def _inner_forward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+                   out_proj_bias, A, D, delta_bias, B_proj_bias, C_proj_bias, delta_softplus):
+    """The Mamba block's forward between the projections (see MambaInnerFn); returns
+    (out (batch, seqlen, out_features), dict of the intermediates the backward keeps).
+    xz: (batch, 2 * dim, seqlen) with unit seqlen stride."""
+    from .causal_conv1d import causal_conv1d_fwd
+    batch, two_d, L = xz.shape
+    dim = two_d // 2
+    R = delta_proj_weight.shape[1]
+    N = A.shape[-1]
+    dt, dev = xz.dtype, xz.device
+    BL = batch * L
+    x, z = xz[:, :dim], xz[:, dim:]
+
+    conv_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+    conv_out = _cm_view(conv_buf, batch, L)
+    causal_conv1d_fwd(x, conv1d_weight, conv1d_bias, silu=True, out=conv_out)
+    x_dblT = x_proj_weight.to(dt) @ conv_buf                          # (R + 2N, b l)
+    if B_proj_bias is not None:
+        x_dblT[R:R + N] += B_proj_bias.to(dt)[:, None]
+    if C_proj_bias is not None:
+        x_dblT[R + N:] += C_proj_bias.to(dt)[:, None]
+    delta_buf = delta_proj_weight.to(dt) @ x_dblT[:R]                # (dim, b l)
+    delta = _cm_view(delta_buf, batch, L)
+    Bv = _cm_view(x_dblT[R:R + N], batch, L).unsqueeze(1)           # (batch, 1, N, L)
+    Cv = _cm_view(x_dblT[R + N:R + 2 * N], batch, L).unsqueeze(1)
+    A32 = A.float().contiguous()
+    D32 = D.float().contiguous() if D is not None else None
+    db32 = delta_bias.float().contiguous() if delta_bias is not None else None
+
+    out_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+    y_buf = torch.empty(dim, BL, dtype=dt, device=dev)
+    xck = torch.empty((batch, selective_scan.n_chunks(L), dim, N), dtype=torch.float32, device=dev)
+    selective_scan.forward_into(conv_out, delta, A32, Bv, Cv, D32, db32, delta_softplus,
+                                _cm_view(out_buf, batch, L), xck, z=z, y=_cm_view(y_buf, batch, L))
+    out_w = out_proj_weight.to(dt)
+    res = torch.nn.functional.linear(out_buf.t(), out_w,
+                                     out_proj_bias.to(dt) if out_proj_bias is not None else None)
+    return res.view(batch, L, -1), {
+        "conv_buf": conv_buf, "x_dblT": x_dblT, "delta_buf": delta_buf, "A32": A32, "D32": D32, "db32": db32,
+        "xck": xck, "y_buf": y_buf, "out_buf": out_buf, "dims": (batch, dim, L, R, N)}
+
+
+def mamba_inner_prefill(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+                        out_proj_bias, A, D=None, delta_bias=None, B_proj_bias=None, C_proj_bias=None,
+                        delta_softplus=True, conv_state=None, ssm_state=None):
+    """mamba_inner_fn's forward (no autograd) that also leaves the decode state of the
+    sequence's end: conv_state (batch, dim, width) receives the last `width` inputs of
+    the conv (zeros before the sequence start) and ssm_state (batch, dim, dstate) fp32
+    the scan's state after the last step, so that decoding continues from there."""
+    if xz.shape[-1] > 1 and xz.stride(-1) != 1:
+        xz = xz.contiguous()
+    with torch.no_grad():
+        res, t = _inner_forward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                                out_proj_weight, out_proj_bias, A, D, delta_bias, B_proj_bias, C_proj_bias,
+                                delta_softplus)
+        batch, dim, L, _, _ = t["dims"]
+        if ssm_state is not None:
+            ssm_state.copy_(t["xck"][:, -1])                         # the last chunk ends at step L - 1
+        if conv_state is not None:
+            W = conv_state.shape[-1]
+            x = xz[:, :dim]
+            tail = x[..., max(0, L - W):]
+            conv_state.zero_()
+            conv_state[..., W - tail.shape[-1]:].copy_(tail)
+    return res
+
+
 class MambaInnerFn(torch.autograd.Function):
     """The Mamba block between in- and out-projection, with the scan fused.
 
@@ -168,49 +236,19 @@ class MambaInnerFn(torch.autograd.Function):
     def forward(ctx, xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
                 out_proj_weight, out_proj_bias, A, B=None, C=None, D=None, delta_bias=None,
                 B_proj_bias=None, C_proj_bias=None, delta_softplus=True):
-        from .causal_conv1d import causal_conv1d_fwd
         if B is not None or C is not None:
             raise ValueError("mamba_inner_fn: B and C must come from x_proj (pass B=None, C=None)")
         if xz.shape[-1] > 1 and xz.stride(-1) != 1:
             xz = xz.contiguous()
-        batch, two_d, L = xz.shape
-        dim = two_d // 2
-        R = delta_proj_weight.shape[1]
-        N = A.shape[-1]
-        dt, dev = xz.dtype, xz.device
-        BL = batch * L
-        x, z = xz[:, :dim], xz[:, dim:]
-
-        conv_buf = torch.empty(dim, BL, dtype=dt, device=dev)
-        conv_out = _cm_view(conv_buf, batch, L)
-        causal_conv1d_fwd(x, conv1d_weight, conv1d_bias, silu=True, out=conv_out)
-        x_dblT = x_proj_weight.to(dt) @ conv_buf                          # (R + 2N, b l)
-        if B_proj_bias is not None:
-            x_dblT[R:R + N] += B_proj_bias.to(dt)[:, None]
-        if C_proj_bias is not None:
-            x_dblT[R + N:] += C_proj_bias.to(dt)[:, None]
-        delta_buf = delta_proj_weight.to(dt) @ x_dblT[:R]                # (dim, b l)
-        delta = _cm_view(delta_buf, batch, L)
-        Bv = _cm_view(x_dblT[R:R + N], batch, L).unsqueeze(1)           # (batch, 1, N, L)
-        Cv = _cm_view(x_dblT[R + N:R + 2 * N], batch, L).unsqueeze(1)
-        A32 = A.float().contiguous()
-        D32 = D.float().contiguous() if D is not None else None
-        db32 = delta_bias.float().contiguous() if delta_bias is not None else None
-
-        out_buf = torch.empty(dim, BL, dtype=dt, device=dev)
-        y_buf = torch.empty(dim, BL, dtype=dt, device=dev)
-        xck = torch.empty((batch, selective_scan.n_chunks(L), dim, N), dtype=torch.float32, device=dev)
-        selective_scan.forward_into(conv_out, delta, A32, Bv, Cv, D32, db32, delta_softplus,
-                                    _cm_view(out_buf, batch, L), xck, z=z, y=_cm_view(y_buf, batch, L))
-        out_w = out_proj_weight.to(dt)
-        res = torch.nn.functional.linear(out_buf.t(), out_w,
-                                         out_proj_bias.to(dt) if out_proj_bias is not None else None)
+        res, t = _inner_forward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
+                                out_proj_weight, out_proj_bias, A, D, delta_bias, B_proj_bias, C_proj_bias,
+                                delta_softplus)
         ctx.save_for_backward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
-                              conv_buf, x_dblT, delta_buf, A32, D32, db32, xck, y_buf, out_buf,
-                              A, D, delta_bias, out_proj_bias, B_proj_bias, C_proj_bias)
+                              t["conv_buf"], t["x_dblT"], t["delta_buf"], t["A32"], t["D32"], t["db32"], t["xck"],
+                              t["y_buf"], t["out_buf"], A, D, delta_bias, out_proj_bias, B_proj_bias, C_proj_bias)
         ctx.delta_softplus = delta_softplus
-        ctx.dims = (batch, dim, L, R, N)
-        return res.view(batch, L, -1)
+        ctx.dims = t["dims"]
+        return res
 
     @staticmethod
     def backward(ctx, dres):

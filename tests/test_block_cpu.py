@@ -128,6 +128,52 @@ def test_rms_norm_oracle_gradient_matches_finite_differences():
     assert torch.autograd.gradcheck(lambda a, b, c: add_rms_norm_ref(a, b, c), (x, r, w))
 
 
+@pytest.mark.parametrize("groups,with_z,with_D", [(1, True, True), (2, False, True), (1, True, False)])
+def test_state_update_oracle_replays_the_scan(groups, with_z, with_D):
+    # a step applied token after token from a zero state is the scan: every output and
+    # the last state of selective_scan_ref (a different formulation: exp of the whole
+    # (L, N) grid, then a sequential sum)
+    from oracle.decode_ref import selective_state_update_ref
+    from oracle.selective_scan_ref import selective_scan_ref
+    torch.manual_seed(5)
+    batch, dim, N, L = 2, 8, 4, 13
+    u = torch.randn(batch, dim, L, dtype=torch.float64)
+    delta = torch.randn(batch, dim, L, dtype=torch.float64)
+    z = torch.randn(batch, dim, L, dtype=torch.float64) if with_z else None
+    A = -torch.rand(dim, N, dtype=torch.float64) * 2
+    B = torch.randn(batch, groups, N, L, dtype=torch.float64)
+    C = torch.randn(batch, groups, N, L, dtype=torch.float64)
+    D = torch.randn(dim, dtype=torch.float64) if with_D else None
+    bias = torch.randn(dim, dtype=torch.float64) * 0.3
+    want, last = selective_scan_ref(u, delta, A, B, C, D, z=z, delta_bias=bias, delta_softplus=True,
+                                    return_last_state=True, compute_dtype=torch.float64)
+    h = torch.zeros(batch, dim, N, dtype=torch.float64)
+    outs = []
+    for t in range(L):
+        y, h = selective_state_update_ref(h, u[..., t], delta[..., t], A, B[..., t], C[..., t], D,
+                                          z=z[..., t] if with_z else None, dt_bias=bias, dt_softplus=True)
+        outs.append(y)
+    assert torch.allclose(torch.stack(outs, -1), want, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(h, last, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("width", [1, 2, 4])
+def test_conv_update_oracle_replays_the_conv(width):
+    from oracle.decode_ref import causal_conv1d_update_ref
+    torch.manual_seed(6)
+    x = torch.randn(2, 5, 9, dtype=torch.float64)
+    w = torch.randn(5, width, dtype=torch.float64)
+    b = torch.randn(5, dtype=torch.float64)
+    want = causal_conv1d_ref(x, w, b, activation="silu")
+    st = torch.zeros(2, 5, width, dtype=torch.float64)
+    outs = []
+    for t in range(x.shape[-1]):
+        y, st = causal_conv1d_update_ref(x[..., t], st, w, b, "silu")
+        outs.append(y)
+    assert torch.allclose(torch.stack(outs, -1), want, rtol=1e-12, atol=1e-12)
+    assert torch.equal(st, x[..., -width:])                 # the state is the last width inputs
+
+
 def test_state_dict_keys_are_the_references():
     # parameter names and shapes of models/causal_lm.py:21-51 and modules/mamba_simple.py:35-85
     cfg = CausalLMConfig(vocab_size=50, model_dim=24, state_dim=16, conv_kernel=4, num_layers=2)

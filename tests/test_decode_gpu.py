@@ -1,0 +1,192 @@
+"""GPU parity of single-token decode, through the HIP library.
+
+* ss_state_update against the float64 step oracle: dstate 16 (16-byte state
+  path) and 5 (element path), a strided state, 1 and 2 groups, with and
+  without D / z / bias, fp32 / bf16 / fp16 I/O;
+* ss_conv1d_update against the step oracle: widths 1-4, with and without
+  bias and SiLU; the shifted state is bit-exact;
+* token-by-token state updates from a zero state reproduce
+  selective_scan_fn over the sequence on the GPU (outputs and last state);
+* MambaSimple and CausalLM: prefill of a prompt (filling the decode cache
+  from the parallel forward) followed by step() on the remaining tokens
+  gives the logits of forward() over the whole sequence; greedy generate()
+  agrees with forward() on its own output;
+* GraphedStep (the step captured into a HIP graph): six replays, with eager
+  work and synchronisations between them, bit-identical to the eager step
+  (logits and cache).
+
+Tolerances: fp32 1e-4 (outputs of a step, relative to the largest
+magnitude where stated), bf16 / fp16 2e-2.
+"""
+import sys
+
+import pytest
+import torch
+
+from oracle.decode_ref import causal_conv1d_update_ref, selective_state_update_ref
+from tests._util import assert_close
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _say(msg):
+    print(f"\n[decode] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+SU_CASES = [
+    # batch, dim, dstate, groups, dtype, z, D, bias, strided state
+    (3, 48, 16, 1, torch.float32, True, True, True, False),
+    (2, 64, 16, 2, torch.bfloat16, True, True, True, False),
+    (4, 32, 5, 1, torch.float16, False, True, False, False),
+    (1, 16, 16, 1, torch.float32, False, False, True, True),
+    (16, 1536, 16, 1, torch.bfloat16, True, True, True, False),
+]
+
+
+@pytest.mark.parametrize("case", SU_CASES, ids=[f"b{c[0]}-d{c[1]}-n{c[2]}-g{c[3]}-{str(c[4]).split('.')[-1]}"
+                                                f"{'-z' if c[5] else ''}{'-D' if c[6] else ''}"
+                                                f"{'-bias' if c[7] else ''}{'-strided' if c[8] else ''}"
+                                                for c in SU_CASES])
+def test_state_update_matches_oracle(case):
+    from mamba_amd.ops.selective_state_update import selective_state_update
+    batch, dim, N, G, dt_, with_z, with_D, with_bias, strided = case
+    _say(f"state update {case}")
+    gen = torch.Generator().manual_seed(200 + dim + N)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    x, dt, z = r(batch, dim).to(dt_), r(batch, dim).to(dt_), r(batch, dim).to(dt_)
+    A = -torch.rand(dim, N, generator=gen) * 3
+    B, C = r(batch, G, N).to(dt_), r(batch, G, N).to(dt_)
+    D = r(dim)
+    bias = r(dim) * 0.5
+    state0 = r(batch, dim, N)
+    if strided:   # every other dstate element of a wider buffer
+        big = torch.zeros(batch, dim, 2 * N, device=DEV)
+        big[..., ::2] = state0.to(DEV)
+        st = big[..., ::2]
+    else:
+        st = state0.to(DEV).clone()
+    out = selective_state_update(st, x.to(DEV), dt.to(DEV), A.to(DEV), B.to(DEV), C.to(DEV),
+                                 D.to(DEV) if with_D else None, z=z.to(DEV) if with_z else None,
+                                 dt_bias=bias.to(DEV) if with_bias else None, dt_softplus=True)
+    want_out, want_st = selective_state_update_ref(state0, x, dt, A, B, C, D if with_D else None,
+                                                   z=z if with_z else None, dt_bias=bias if with_bias else None,
+                                                   dt_softplus=True)
+    tol = TOL[dt_]
+    assert_close(st.cpu(), want_st, 1e-5, 1e-5, "state")
+    assert_close(out.cpu(), want_out.double(), tol, tol, "out")
+
+
+@pytest.mark.parametrize("width,bias,act,dt_", [(4, True, "silu", torch.float32), (3, False, None, torch.float32),
+                                                (1, True, "silu", torch.bfloat16), (2, True, "silu", torch.float16),
+                                                (4, False, "silu", torch.bfloat16)])
+def test_conv_update_matches_oracle(width, bias, act, dt_):
+    from mamba_amd.ops.causal_conv1d import causal_conv1d_update
+    _say(f"conv update width {width} bias {bias} act {act} {dt_}")
+    gen = torch.Generator().manual_seed(300 + width)
+    batch, dim = 3, 40
+    x = torch.randn(batch, dim, generator=gen).to(dt_)
+    st0 = torch.randn(batch, dim, width, generator=gen).to(dt_)
+    w = torch.randn(dim, 1, width, generator=gen)
+    b = torch.randn(dim, generator=gen) if bias else None
+    st = st0.to(DEV).clone()
+    out = causal_conv1d_update(x.to(DEV), st, w.to(DEV), b.to(DEV) if bias else None, act)
+    want_out, want_st = causal_conv1d_update_ref(x.double(), st0.double(), w.double(),
+                                                 b.double() if bias else None, act)
+    assert torch.equal(st.cpu(), want_st.to(dt_)), "the conv state is shifted, not recomputed"
+    tol = TOL[dt_]
+    assert_close(out.cpu(), want_out, tol, tol, "out")
+
+
+def test_state_updates_replay_the_scan():
+    from mamba_amd.ops.selective_scan_interface import selective_scan_fn
+    from mamba_amd.ops.selective_state_update import selective_state_update
+    _say("token-by-token updates vs selective_scan_fn")
+    torch.manual_seed(9)
+    batch, dim, N, L = 2, 64, 16, 40
+    u, delta, z = (torch.randn(batch, dim, L, device=DEV) for _ in range(3))
+    A = -torch.rand(dim, N, device=DEV) * 3
+    B, C = torch.randn(batch, 1, N, L, device=DEV), torch.randn(batch, 1, N, L, device=DEV)
+    D, bias = torch.randn(dim, device=DEV), 0.3 * torch.randn(dim, device=DEV)
+    want, last = selective_scan_fn(u, delta, A, B, C, D, z=z, delta_bias=bias, delta_softplus=True,
+                                   return_last_state=True)
+    st = torch.zeros(batch, dim, N, device=DEV)
+    outs = [selective_state_update(st, u[..., t], delta[..., t], A, B[..., t], C[..., t], D, z=z[..., t],
+                                   dt_bias=bias, dt_softplus=True) for t in range(L)]
+    got = torch.stack(outs, -1)
+    scale = float(want.abs().max())
+    assert_close(got.cpu(), want.cpu(), 1e-4, 1e-4 * scale, "outputs")
+    assert_close(st.cpu(), last.cpu(), 1e-4, 1e-4 * float(last.abs().max()), "last state")
+
+
+@pytest.mark.parametrize("dt_", [torch.float32, torch.bfloat16])
+def test_causal_lm_prefill_and_step_match_forward(dt_):
+    from mamba_amd.models import CausalLM, CausalLMConfig
+    _say(f"CausalLM prefill + step vs forward, {dt_}")
+    torch.manual_seed(13)
+    cfg = CausalLMConfig(vocab_size=101, model_dim=64, state_dim=16, num_layers=2, dropout_rate=0.0)
+    lm = CausalLM(cfg).to(DEV).to(dt_).eval()
+    with torch.no_grad():
+        for layer in lm.layers:
+            layer.norm.weight.uniform_(-0.3, 0.3)
+    ids = torch.randint(0, cfg.vocab_size, (3, 50), device=DEV)
+    P = 37                                              # prompt length (not a multiple of 16 or of the conv width)
+    with torch.no_grad():
+        full = lm(ids).float()
+        cache = lm.allocate_inference_cache(3)
+        pre = lm(ids[:, :P], inference_cache=cache).float()
+        steps = [lm.step(ids[:, t], cache).float() for t in range(P, ids.shape[1])]
+    scale = float(full.abs().max())
+    tol = TOL[dt_]
+    assert_close(pre.cpu(), full[:, :P].cpu(), tol, tol * scale, "prefill logits")
+    assert_close(torch.stack(steps, 1).cpu(), full[:, P:].cpu(), tol, tol * scale, "step logits")
+
+
+def test_generate_greedy_agrees_with_forward():
+    from mamba_amd.models import CausalLM, CausalLMConfig
+    _say("greedy generate vs forward")
+    torch.manual_seed(14)
+    cfg = CausalLMConfig(vocab_size=97, model_dim=64, state_dim=16, num_layers=2, dropout_rate=0.0)
+    lm = CausalLM(cfg).to(DEV).eval()
+    prompt = torch.randint(0, cfg.vocab_size, (2, 20), device=DEV)
+    out = lm.generate(prompt, max_new_tokens=12, temperature=0)
+    assert out.shape == (2, 32) and torch.equal(out[:, :20], prompt)
+    with torch.no_grad():
+        logits = lm(out).float()
+    top2 = logits[:, 19:31].topk(2, dim=-1).values
+    clear = (top2[..., 0] - top2[..., 1]) > 1e-3        # positions without a near tie
+    assert torch.equal(logits[:, 19:31].argmax(-1)[clear], out[:, 20:32][clear])
+    assert clear.float().mean() > 0.8
+    # sampling: the right shape, tokens in range
+    g = torch.Generator(device=DEV).manual_seed(0)
+    s = lm.generate(prompt, max_new_tokens=5, temperature=0.8, generator=g)
+    assert s.shape == (2, 25) and int(s.max()) < cfg.vocab_size and int(s.min()) >= 0
+
+
+def test_graphed_step_replays_match_eager():
+    # several replays, with eager work and synchronisations between them, each
+    # checked against the eager step on an identical cache
+    from mamba_amd.models import CausalLM, CausalLMConfig, GraphedStep
+    _say("graph-captured step vs eager step")
+    torch.manual_seed(15)
+    cfg = CausalLMConfig(vocab_size=89, model_dim=64, state_dim=16, num_layers=2, dropout_rate=0.0)
+    lm = CausalLM(cfg).to(DEV).eval()
+    prompt = torch.randint(0, cfg.vocab_size, (4, 24), device=DEV)
+    cache_g = lm.allocate_inference_cache(4)
+    cache_e = lm.allocate_inference_cache(4)
+    with torch.no_grad():
+        lm(prompt, inference_cache=cache_g)
+        lm(prompt, inference_cache=cache_e)
+    step = GraphedStep(lm, cache_g, 4)
+    for t in range(6):
+        ids = torch.randint(0, cfg.vocab_size, (4,), device=DEV)
+        got = step(ids).float().clone()
+        torch.cuda.synchronize()
+        with torch.no_grad():
+            want = lm.step(ids, cache_e).float()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {t} differs from the eager step"
+        for (c1, s1), (c2, s2) in zip(cache_g, cache_e):
+            assert torch.equal(c1, c2) and torch.equal(s1, s2), f"cache after replay {t}"

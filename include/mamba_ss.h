@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 6
+#define SS_ABI_VERSION 7
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -81,11 +81,16 @@ typedef struct ss_fwd_args {
     const float* delta_bias; /* may be NULL iff !has_delta_bias */
     const void* z;           /* may be NULL iff !has_z */
     void* out;
+    /* checkpoints for the backward.  Required by ss_bwd; ss_fwd may be given
+       NULL (a forward that no backward follows): no checkpoints are written. */
     float* x;
     /* pre-gate output y = sum_n C h + D u, same layout as out.  Written by
        ss_fwd when has_z and y != NULL; required (read) by ss_bwd when has_z. */
     void* y;
     int64_t y_batch_stride, y_dim_stride;
+    /* ss_fwd only, may be NULL: fp32 (batch, dim, dstate) contiguous, receives
+       the state h after the last step (what decoding continues from). */
+    float* last_state;
 } ss_fwd_args;
 
 typedef struct ss_bwd_args {

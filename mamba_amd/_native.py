@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
@@ -43,6 +43,7 @@ class FwdArgs(ctypes.Structure):
         ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
         ("D", _p), ("delta_bias", _p), ("z", _p), ("out", _p), ("x", _p),
         ("y", _p), ("y_batch_stride", _i64), ("y_dim_stride", _i64),
+        ("last_state", _p),
     ]
 
 

@@ -71,7 +71,7 @@ int check_fwd_common(const ss_fwd_args* a, bool* empty) {
         {a->u, "u", true, es}, {a->delta, "delta", true, es}, {a->A, "A", true, 4},
         {a->B, "B", true, a->is_var_B ? es : 4}, {a->C, "C", true, a->is_var_C ? es : 4},
         {a->D, "D", a->has_D != 0, 4}, {a->delta_bias, "delta_bias", a->has_delta_bias != 0, 4},
-        {a->z, "z", a->has_z != 0, es}, {a->x, "x", true, 4},
+        {a->z, "z", a->has_z != 0, es}, {a->x, "x", false, 4}, {a->last_state, "last_state", false, 4},
     };
     for (const P& q : ptrs) {
         if (q.need && !q.p) return fail(SS_ERR_INVALID, "%s is NULL", q.name);
@@ -133,6 +133,7 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.z = a->has_z ? a->z : nullptr;
     p.out = a->out; p.x = a->x;
     p.y = a->has_z ? a->y : nullptr;
+    p.last_state = a->last_state;
     p.y_bs = a->y_batch_stride; p.y_ds = a->y_dim_stride;
     return p;
 }
@@ -162,6 +163,7 @@ int check_bwd(const ss_bwd_args* a, bool* empty) {
         {a->dC, "dC", true, 4}, {a->dD, "dD", a->f.has_D != 0, 4},
         {a->ddelta_bias, "ddelta_bias", a->f.has_delta_bias != 0, 4},
         {a->f.y, "y (saved pre-gate output)", a->f.has_z != 0, es},
+        {a->f.x, "x", true, 4},
     };
     for (const P& q : ptrs) {
         if (q.need && !q.p) return fail(SS_ERR_INVALID, "%s is NULL", q.name);

@@ -378,6 +378,12 @@ constexpr int kRsrcWord3 = 0x00020000;   // gfx9-family raw buffer, 32-bit data 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, kRsrcWord3);
 }
+// As make_rsrc, or, when !live, a resource of zero bytes: the hardware's range
+// check then drops every store through it (and loads return 0), so an
+// optional output costs no branch in the loop and no memory traffic.
+__device__ __forceinline__ rsrc_t make_rsrc_opt(const void* base, bool live) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, live ? -1 : 0, kRsrcWord3);
+}
 // Element (voff + soff bytes) of an IT array as float.
 template <typename T>
 __device__ __forceinline__ float bload(rsrc_t r, uint32_t voff, uint32_t soff) {

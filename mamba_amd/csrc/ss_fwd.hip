@@ -50,8 +50,8 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
     const IT* Cv_base = static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs;
     const float* Bc_base = static_cast<const float*>(p.B) + c * p.B_gs;  // constant B: (dim, dstate)
     const float* Cc_base = static_cast<const float*>(p.C) + c * p.C_gs;
-    // x: (batch, chunk, dim, dstate)
-    float* xrow = p.x + (b * p.n_chunks * p.dim + c) * N;
+    // x: (batch, chunk, dim, dstate); not written when null
+    float* xrow = p.x ? p.x + (b * p.n_chunks * p.dim + c) * N : nullptr;
     const int64_t x_chunk_stride = p.dim * N;
 
     const float Dv = p.D ? p.D[c] : 0.f;
@@ -166,7 +166,8 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
             });
             h[s] = hs;
             const bool chunk_end = ((t0 + kT) % kChunk == 0) || (t0 + kT >= L);
-            if (chunk_end && cval && n < N) xrow[(t0 / kChunk) * x_chunk_stride + n] = hs;
+            if (chunk_end && cval && n < N && p.x) xrow[(t0 / kChunk) * x_chunk_stride + n] = hs;
+            if (t0 + kT >= L && cval && n < N && p.last_state) p.last_state[(b * p.dim + c) * N + n] = hs;
         }
         row_transpose_write(wbuf + slot * kTrWave, yp, j, r);
         pend_t = t0 + r;
@@ -254,9 +255,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     // out / y are written with 16-byte stores, which take their advance in the
     // resource base and no uniform offset (see bstore4)
     IT* const go = static_cast<IT*>(p.out) + b * p.o_bs + c0 * p.o_ds;
-    IT* const gy = kZ ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : go;
+    // without a y (or x) buffer the stores go through a zero-byte resource
+    // and are dropped: a forward that no backward follows writes neither
+    const bool save_y = kZ && p.y != nullptr, save_x = p.x != nullptr;
+    IT* const gy = save_y ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : go;
     // x: (batch, chunk, dim, dstate)
-    const rsrc_t Rx = make_rsrc(p.x + (b * p.n_chunks * p.dim + c0) * kT);
+    const rsrc_t Rx = make_rsrc_opt(save_x ? p.x + (b * p.n_chunks * p.dim + c0) * kT : nullptr, save_x);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
     const uint32_t oz = uint32_t(row * p.z_ds + 4 * r) * es;
@@ -303,7 +307,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
         if constexpr (kZ) {
-            bstore4<IT>(make_rsrc(gy + int64_t(sc) * kSC), oy, y);
+            bstore4<IT>(make_rsrc_opt(gy + int64_t(sc) * kSC, save_y), oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);
@@ -395,13 +399,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         yo[(kQ - 1) * kT + r] = sum16(ys);
         finish_super(nsc - 1);
     }
+    if (p.last_state) p.last_state[(b * p.dim + c) * kT + r] = h;
 }
 
 bool fwd_fast_ok(const FwdParams& p) {
     // every byte offset the kernel forms stays below 2^32: rows and seqlen
     // below 2^26 elements, and the checkpoint offset (chunk x dim x 64 B)
     return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kSC && p.seqlen % kSC == 0 &&
-           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec && (!p.has_z || p.y != nullptr) &&
+           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec &&
            small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns}) &&
            p.seqlen * p.dim < (int64_t(1) << 30);
 }

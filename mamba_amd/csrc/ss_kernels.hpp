@@ -23,6 +23,7 @@ struct FwdParams {
     const float* D; const float* delta_bias; const void* z;
     void* out; float* x;
     void* y;                                  // pre-gate output (z gate only); may be null in forward
+    float* last_state;                        // forward: h after the last step, (batch, dim, dstate); may be null
 };
 
 struct BwdParams {

@@ -92,16 +92,26 @@ class SelectiveScanZFn(torch.autograd.Function):
         A = A.float()
         D = D.float().contiguous() if D is not None else None
         delta_bias = delta_bias.float().contiguous() if delta_bias is not None else None
-        res = selective_scan.forward(u, delta, A, B, C, D, delta_bias, delta_softplus, z=z)
-        out, x = res[0], res[1]
-        y = res[2] if z is not None else None
+        # the checkpoints x and the pre-gate output y exist for the backward:
+        # without a gradient to compute they are neither allocated nor written
+        need_bwd = any(ctx.needs_input_grad)
+        batch, dim, seqlen = u.shape
+        dstate = A.shape[1]
+        out = torch.empty_like(delta, memory_format=torch.contiguous_format)
+        x = (torch.empty((batch, selective_scan.n_chunks(seqlen), dim, dstate), dtype=torch.float32,
+                         device=u.device) if need_bwd else None)
+        y = torch.empty_like(out) if z is not None and need_bwd else None
+        last_state = None
+        if return_last_state:
+            last_state = (torch.empty if seqlen > 0 else torch.zeros)(
+                (batch, dim, dstate), dtype=torch.float32, device=u.device)
+        selective_scan.forward_into(u, delta, A, B, C, D, delta_bias, delta_softplus, out, x, z=z, y=y,
+                                    last_state=last_state)
         ctx.delta_softplus = delta_softplus
         ctx.has_z = z is not None
-        ctx.save_for_backward(u, delta, A, B, C, D, delta_bias, z, x, y)
-        ctx.mark_non_differentiable(x)
+        if need_bwd:
+            ctx.save_for_backward(u, delta, A, B, C, D, delta_bias, z, x, y)
         if return_last_state:
-            # x is (batch, n_chunks, dim, dstate); its last chunk holds h at the last step
-            last_state = x[:, -1] if x.shape[1] > 0 else x.new_zeros(x.shape[0], x.shape[2], x.shape[3])
             ctx.mark_non_differentiable(last_state)
             return out, last_state
         return out
@@ -146,10 +156,13 @@ def _cm_view(buf, batch, L):
 
 
 def _inner_forward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
-                   out_proj_bias, A, D, delta_bias, B_proj_bias, C_proj_bias, delta_softplus):
+                   out_proj_bias, A, D, delta_bias, B_proj_bias, C_proj_bias, delta_softplus, save=True,
+                   last_state=None):
     """The Mamba block's forward between the projections (see MambaInnerFn); returns
     (out (batch, seqlen, out_features), dict of the intermediates the backward keeps).
-    xz: (batch, 2 * dim, seqlen) with unit seqlen stride."""
+    xz: (batch, 2 * dim, seqlen) with unit seqlen stride.  Without ``save`` the scan
+    writes no checkpoints and no pre-gate output (nothing for a backward);
+    ``last_state`` (fp32 (batch, dim, dstate) contiguous) receives the final state."""
     from .causal_conv1d import causal_conv1d_fwd
     batch, two_d, L = xz.shape
     dim = two_d // 2
@@ -176,10 +189,12 @@ def _inner_forward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_wei
     db32 = delta_bias.float().contiguous() if delta_bias is not None else None
 
     out_buf = torch.empty(dim, BL, dtype=dt, device=dev)
-    y_buf = torch.empty(dim, BL, dtype=dt, device=dev)
-    xck = torch.empty((batch, selective_scan.n_chunks(L), dim, N), dtype=torch.float32, device=dev)
+    y_buf = torch.empty(dim, BL, dtype=dt, device=dev) if save else None
+    xck = (torch.empty((batch, selective_scan.n_chunks(L), dim, N), dtype=torch.float32, device=dev)
+           if save else None)
     selective_scan.forward_into(conv_out, delta, A32, Bv, Cv, D32, db32, delta_softplus,
-                                _cm_view(out_buf, batch, L), xck, z=z, y=_cm_view(y_buf, batch, L))
+                                _cm_view(out_buf, batch, L), xck, z=z,
+                                y=_cm_view(y_buf, batch, L) if save else None, last_state=last_state)
     out_w = out_proj_weight.to(dt)
     res = torch.nn.functional.linear(out_buf.t(), out_w,
                                      out_proj_bias.to(dt) if out_proj_bias is not None else None)
@@ -198,12 +213,16 @@ def mamba_inner_prefill(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_pro
     if xz.shape[-1] > 1 and xz.stride(-1) != 1:
         xz = xz.contiguous()
     with torch.no_grad():
+        last = None
+        if ssm_state is not None:
+            direct = ssm_state.dtype == torch.float32 and ssm_state.is_contiguous() and xz.shape[-1] > 0
+            last = ssm_state if direct else torch.zeros(ssm_state.shape, dtype=torch.float32, device=xz.device)
         res, t = _inner_forward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
                                 out_proj_weight, out_proj_bias, A, D, delta_bias, B_proj_bias, C_proj_bias,
-                                delta_softplus)
+                                delta_softplus, save=False, last_state=last)
         batch, dim, L, _, _ = t["dims"]
-        if ssm_state is not None:
-            ssm_state.copy_(t["xck"][:, -1])                         # the last chunk ends at step L - 1
+        if ssm_state is not None and last is not ssm_state:
+            ssm_state.copy_(last)
         if conv_state is not None:
             W = conv_state.shape[-1]
             x = xz[:, :dim]
@@ -240,9 +259,12 @@ class MambaInnerFn(torch.autograd.Function):
             raise ValueError("mamba_inner_fn: B and C must come from x_proj (pass B=None, C=None)")
         if xz.shape[-1] > 1 and xz.stride(-1) != 1:
             xz = xz.contiguous()
+        save = any(ctx.needs_input_grad)
         res, t = _inner_forward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
                                 out_proj_weight, out_proj_bias, A, D, delta_bias, B_proj_bias, C_proj_bias,
-                                delta_softplus)
+                                delta_softplus, save=save)
+        if not save:
+            return res
         ctx.save_for_backward(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
                               t["conv_buf"], t["x_dblT"], t["delta_buf"], t["A32"], t["D32"], t["db32"], t["xck"],
                               t["y_buf"], t["out_buf"], A, D, delta_bias, out_proj_bias, B_proj_bias, C_proj_bias)

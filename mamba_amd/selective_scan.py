@@ -120,34 +120,48 @@ def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y):
-    _require(out is not None and x is not None, "out and x are required")
+def _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y, last_state=None):
+    _require(out is not None, "out is required")
     _check_seq_tensor("out", out, u.shape, delta.dtype, u.device)
     batch, dim, seqlen = u.shape
-    _require(x.dtype == torch.float32 and x.is_contiguous() and x.device == u.device
-             and tuple(x.shape) == (batch, n_chunks(seqlen), dim, A.shape[1]),
-             "x must be a contiguous fp32 (batch, n_chunks, dim, dstate) tensor")
+    if x is not None:
+        _require(x.dtype == torch.float32 and x.is_contiguous() and x.device == u.device
+                 and tuple(x.shape) == (batch, n_chunks(seqlen), dim, A.shape[1]),
+                 "x must be a contiguous fp32 (batch, n_chunks, dim, dstate) tensor")
     if y is not None:
         _check_seq_tensor("y", y, u.shape, delta.dtype, u.device)
-    return _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
+    if last_state is not None:
+        _require(last_state.dtype == torch.float32 and last_state.is_contiguous() and last_state.device == u.device
+                 and tuple(last_state.shape) == (batch, dim, A.shape[1]),
+                 "last_state must be a contiguous fp32 (batch, dim, dstate) tensor")
+    a = _fill_fwd_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, z, out, x, y)
+    a.last_state = _ptr(last_state)
+    return a
 
 
-def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
+def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None,
+                 last_state=None):
     """Forward into caller-allocated ``out`` (delta's dtype), ``x`` (fp32
-    (batch, n_chunks, dim, dstate) contiguous) and, with ``z``, ``y``."""
+    (batch, n_chunks, dim, dstate) contiguous) and, with ``z``, ``y``.
+
+    ``x`` and ``y`` are what the backward needs; either may be None for a
+    forward that no backward follows (they are then not written at all).
+    ``last_state`` (fp32 (batch, dim, dstate), optional) receives the state
+    after the last step."""
     lib = nat.load()
-    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y)
+    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y, last_state)
     with torch.cuda.device(u.device):
         nat.check(lib.ss_fwd(ctypes.byref(a), _stream(u.device)), "selective_scan.forward")
 
 
-def prepare_forward(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
+def prepare_forward(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None,
+                    last_state=None):
     """Validates the arguments of ``forward_into`` once and returns a callable
     that launches the same forward again, on the stream that is current now,
     with no host-side work beyond the C call (the tensors must stay alive
     and keep their storage).  For repeated launches over fixed buffers."""
     lib = nat.load()
-    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y)
+    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y, last_state)
     dev = u.device
     stream = torch.cuda.current_stream(dev)
     handle = ctypes.c_void_p(stream.cuda_stream)

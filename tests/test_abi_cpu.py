@@ -59,7 +59,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 6
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 7
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -173,7 +173,7 @@ FWD_BREAKS = [
     ("zero groups", lambda a: setattr(a, "n_groups", 0), "INVALID", "n_groups"),
     ("wrong n_chunks", lambda a: setattr(a, "n_chunks", 6), "INVALID", "n_chunks"),
     ("u NULL", lambda a: setattr(a, "u", None), "INVALID", "u is NULL"),
-    ("x NULL", lambda a: setattr(a, "x", None), "INVALID", "x is NULL"),
+    ("last_state misaligned", lambda a: setattr(a, "last_state", FAKE + 2), "INVALID", "last_state is misaligned"),
     ("out NULL", lambda a: setattr(a, "out", None), "INVALID", "out is NULL"),
     ("D NULL with has_D", lambda a: setattr(a, "D", None), "INVALID", "D is NULL"),
     ("z NULL with has_z", lambda a: setattr(a, "z", None), "INVALID", "z is NULL"),
@@ -201,6 +201,7 @@ def test_fwd_check_rejects(nat, lib, case):
 
 
 BWD_BREAKS = [
+    ("x NULL", lambda b: setattr(b.f, "x", None), "x is NULL"),
     ("dout NULL", lambda b: setattr(b, "dout", None), "dout is NULL"),
     ("du NULL", lambda b: setattr(b, "du", None), "du is NULL"),
     ("dz NULL with has_z", lambda b: setattr(b, "dz", None), "dz is NULL"),
@@ -210,6 +211,15 @@ BWD_BREAKS = [
     ("misaligned dA", lambda b: setattr(b, "dA", FAKE + 65536 + 2), "dA is misaligned"),
     ("negative dout stride", lambda b: setattr(b, "dout_dim_stride", -5), "negative stride"),
 ]
+
+
+def test_forward_without_checkpoints_is_valid(nat, lib):
+    # a forward that no backward follows passes no x (and no y); last_state is optional
+    a = valid_fwd(nat)
+    a.x, a.y = None, None
+    assert lib.ss_fwd_check(ctypes.byref(a)) == nat.SS_OK, lib.ss_last_error()
+    a.last_state = FAKE + 8 * 4096
+    assert lib.ss_fwd_check(ctypes.byref(a)) == nat.SS_OK, lib.ss_last_error()
 
 
 @pytest.mark.parametrize("case", [c[0] for c in BWD_BREAKS])

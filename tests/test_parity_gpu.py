@@ -153,6 +153,36 @@ def test_fast_path_strided_z_and_last_state():
         assert_close(g[k].grad.cpu(), rgrads[k], 1e-3, 1e-3, f"d{k}")
 
 
+@pytest.mark.parametrize("shape", [(2, 64, 16, 256, torch.float32), (2, 48, 16, 100, torch.bfloat16),
+                                   (1, 32, 4, 70, torch.float32)],
+                         ids=["fast-f32", "general-bf16", "general-n4"])
+def test_forward_without_checkpoints(shape):
+    """A forward that no backward follows (x, y not given) writes the same out,
+    and last_state equals the last checkpoint, on the fast and general kernels."""
+    from mamba_amd import selective_scan as ss
+    batch, dim, N, L, dt = shape
+    print(f"\n[parity] forward without checkpoints b{batch}-d{dim}-n{N}-l{L} {dt}", flush=True)
+    x = make_inputs(batch, dim, N, L, seed=21, dtype=dt)
+    dev = torch.device("cuda:0")
+    t = {k: x[k].to(dev) for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")}
+    args = (t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], True)
+    out1 = torch.empty_like(t["delta"])
+    y1 = torch.empty_like(out1)
+    xck = torch.empty((batch, ss.n_chunks(L), dim, N), dtype=torch.float32, device=dev)
+    ss.forward_into(*args, out1, xck, z=t["z"], y=y1)
+    out2 = torch.full_like(out1, float("nan"))
+    last = torch.full((batch, dim, N), float("nan"), device=dev)
+    ss.forward_into(*args, out2, None, z=t["z"], y=None, last_state=last)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2), "out must not depend on whether checkpoints are kept"
+    assert torch.equal(last, xck[:, -1]), "last_state is the state after the last step"
+    with torch.no_grad():
+        from mamba_amd.ops.selective_scan_interface import selective_scan_fn
+        out3, last3 = selective_scan_fn(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], z=t["z"],
+                                        delta_bias=t["delta_bias"], delta_softplus=True, return_last_state=True)
+    assert torch.equal(out3, out1) and torch.equal(last3, last)
+
+
 def test_backward_with_and_without_workspace():
     """The dB / dC slices (workspace) and direct accumulation give the same gradients."""
     from mamba_amd import selective_scan as ss

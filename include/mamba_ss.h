@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 7
+#define SS_ABI_VERSION 8
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -91,6 +91,13 @@ typedef struct ss_fwd_args {
     /* ss_fwd only, may be NULL: fp32 (batch, dim, dstate) contiguous, receives
        the state h after the last step (what decoding continues from). */
     float* last_state;
+    /* ss_fwd only, optional device scratch of ss_fwd_workspace_bytes() bytes,
+       16-byte aligned.  With it, a forward with too few (batch, channel)
+       rows to fill the GPU (small batch, long sequence) scans segments of
+       the sequence in parallel and joins them; NULL gives the serial scan.
+       Results agree to rounding.  Calls that overlap must not share it. */
+    void* workspace;
+    int64_t workspace_bytes;
 } ss_fwd_args;
 
 typedef struct ss_bwd_args {
@@ -154,6 +161,12 @@ int ss_bwd_check(const ss_bwd_args* a);
    work.  The reference needs none: its backward adds every channel's dB / dC
    into the output directly (backward_kernel.cu:457-479). */
 int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a);
+
+/* Bytes of workspace ss_fwd can use for these arguments (0: none), or -1
+   (with ss_last_error set) when the arguments fail the checks.  No device
+   work.  No counterpart in the reference, whose forward has one block per
+   (batch, channel) row and no sequence parallelism. */
+int64_t ss_fwd_workspace_bytes(const ss_fwd_args* a);
 
 /* Base name of the kernel that ss_fwd / ss_bwd would launch for these
    arguments ("ss_fwd_fast", "ss_fwd_kernel", "ss_bwd_fast", "ss_bwd_kernel"),

@@ -13,11 +13,11 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
-    "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_bwd_workspace_bytes",
+    "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_bwd_workspace_bytes", "ss_fwd_workspace_bytes",
     "ss_fwd_kernel_name", "ss_bwd_kernel_name",
     "ss_fwd", "ss_bwd", "ss_conv1d_fwd", "ss_conv1d_bwd",
     "ss_rmsnorm_fwd", "ss_rmsnorm_bwd", "ss_rmsnorm_bwd_workspace_bytes",
@@ -43,7 +43,7 @@ class FwdArgs(ctypes.Structure):
         ("u", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
         ("D", _p), ("delta_bias", _p), ("z", _p), ("out", _p), ("x", _p),
         ("y", _p), ("y_batch_stride", _i64), ("y_dim_stride", _i64),
-        ("last_state", _p),
+        ("last_state", _p), ("workspace", _p), ("workspace_bytes", _i64),
     ]
 
 
@@ -177,6 +177,8 @@ def load():
         lib.ss_rmsnorm_bwd.restype = ctypes.c_int
         lib.ss_rmsnorm_bwd_workspace_bytes.argtypes = [_i64, _i64]
         lib.ss_rmsnorm_bwd_workspace_bytes.restype = _i64
+        lib.ss_fwd_workspace_bytes.argtypes = [ctypes.POINTER(FwdArgs)]
+        lib.ss_fwd_workspace_bytes.restype = _i64
         lib.ss_bwd_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs)]
         lib.ss_bwd_workspace_bytes.restype = _i64
         lib.ss_fwd.argtypes = [ctypes.POINTER(FwdArgs), _p]

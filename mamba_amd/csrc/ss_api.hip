@@ -134,6 +134,7 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.out = a->out; p.x = a->x;
     p.y = a->has_z ? a->y : nullptr;
     p.last_state = a->last_state;
+    p.nseg = 1;
     p.y_bs = a->y_batch_stride; p.y_ds = a->y_dim_stride;
     return p;
 }
@@ -295,10 +296,28 @@ int ss_fwd(const ss_fwd_args* a, void* stream) {
     int rc = check_fwd(a, &empty);
     if (rc != SS_OK) return rc;
     if (empty) return ok();
-    const ss::FwdParams p = make_fwd_params(a);
+    ss::FwdParams p = make_fwd_params(a);
+    if (a->workspace) {
+        if (!aligned(a->workspace, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
+        const int nseg = ss::fwd_segments(p);
+        if (nseg > 1 && a->workspace_bytes >= ss::fwd_seg_bytes(p, nseg)) {
+            p.nseg = nseg;
+            p.seg_h = static_cast<float*>(a->workspace);
+            p.seg_s = p.seg_h + p.batch * nseg * p.dim * 16;
+        }
+    }
     hipError_t e = ss::launch_fwd(p, a->itype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "forward launch failed: %s", hipGetErrorString(e));
     return ok();
+}
+
+int64_t ss_fwd_workspace_bytes(const ss_fwd_args* a) {
+    bool empty = false;
+    if (check_fwd(a, &empty) != SS_OK) return -1;
+    ok();
+    if (empty) return 0;
+    const ss::FwdParams p = make_fwd_params(a);
+    return ss::fwd_seg_bytes(p, ss::fwd_segments(p));
 }
 
 int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a) {

@@ -238,12 +238,18 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const int j = lane >> 4;
     const int row = w * kRows + j;                 // this lane's channel row in the workgroup
     const int64_t nblk = p.dim / kChPerWG;
+    // logical workgroup (b, seg, channel block), channel block fastest: the
+    // workgroups of one segment of one batch row read the same B / C
     const int64_t blk = xcd_block_id();
-    const int64_t b = blk / nblk;
+    const int nseg = p.nseg;
+    const int64_t bs = blk / nblk;
+    const int64_t b = bs / nseg;
+    const int seg = int(bs % nseg);
     const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
-    const int nsc = int(p.seqlen / kSC);           // below 2^20
+    const int nsc_seg = int(p.seqlen / kSC) / nseg;   // super-chunks per segment (below 2^20)
+    const int sc0 = seg * nsc_seg, sc1 = sc0 + nsc_seg;
 
     // buffer resources at the workgroup's rows; lane (row, r) owns steps
     // 4r..4r+3 of channel c0 + row and, for the B / C staging, of state row
@@ -296,7 +302,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) yoff[m] = 4 * ((r >> 2) ^ m) + (r & 3);
 
+    // the state entering this segment: the earlier segments' end states
+    // (each scanned from zero) joined in order, h <- exp(A sum delta') h + h_end
     float h = 0.f;
+    for (int s2 = 0; s2 < seg; ++s2) {
+        const int64_t si = (b * nseg + s2) * p.dim + c;
+        h = __builtin_fmaf(__builtin_amdgcn_exp2f(a2 * p.seg_s[si]), h, p.seg_h[si * kT + r]);
+    }
     float4 pu = make_float4(0.f, 0.f, 0.f, 0.f), pz = pu;   // u, z of the previous super-chunk
 
     // out / y of super-chunk sc (its 64 sums are in yo)
@@ -329,13 +341,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     };
 
     Super S;
-    fetch(0, S);
+    fetch(sc0, S);
     stage(S, 0);
-    for (int sc = 0; sc < nsc; ++sc) {
-        const int buf = sc & 1;
+    for (int sc = sc0; sc < sc1; ++sc) {
+        const int buf = (sc - sc0) & 1;
         lds_barrier();   // B / C tile of sc staged
         const float4 cu = S.u, cd = S.d, cz = S.z;
-        fetch(sc + 1 < nsc ? sc + 1 : nsc - 1, S);
+        fetch(sc + 1 < sc1 ? sc + 1 : sc1 - 1, S);
 
         float4 dt, dtu;
         {
@@ -373,7 +385,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             // the previous chunk's sums (chunk 4 sc + q - 1) into the regroup area
             yo[((q + kQ - 1) % kQ) * kT + r] = sum16(ys);
             if constexpr (q == 0) {
-                finish_super(sc > 0 ? sc - 1 : 0);
+                finish_super(sc > sc0 ? sc - 1 : sc0);   // (at sc0 a placeholder, rewritten later)
                 pu = cu;     // this super-chunk's u, z wait for its outputs
                 pz = cz;
             }
@@ -397,9 +409,123 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         float ys[kT];
         read_tile(ys);
         yo[(kQ - 1) * kT + r] = sum16(ys);
-        finish_super(nsc - 1);
+        finish_super(sc1 - 1);
     }
-    if (p.last_state) p.last_state[(b * p.dim + c) * kT + r] = h;
+    if (p.last_state && seg == nseg - 1) p.last_state[(b * p.dim + c) * kT + r] = h;
+}
+
+// Pass A of the sequence-parallel forward: workgroup (b, seg, 16 channels)
+// scans segment seg (nseg - 1 of them: the last segment's end state is not
+// needed) from a zero state with the fast kernel's lane layout and
+// arithmetic, but only the state recurrence (no C, no outputs), and writes
+// the state after the segment's last step to seg_h and the segment's sum of
+// delta' to seg_s.  About three fifths of a full scan's work per step.
+template <typename IT>
+__global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams p) {
+    __shared__ __attribute__((aligned(16))) float s_b[2 * 16 * kSC];               // [buf][n][64 steps]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane & 15;
+    const int j = lane >> 4;
+    const int row = w * kRows + j;
+    const int64_t nblk = p.dim / kChPerWG;
+    const int nsa = p.nseg - 1;                    // segments scanned here
+    const int64_t blk = xcd_block_id();
+    const int64_t bs = blk / nblk;
+    const int64_t b = bs / nsa;
+    const int seg = int(bs % nsa);
+    const int64_t c0 = (blk % nblk) * kChPerWG;
+    const int64_t c = c0 + row;
+    const int64_t g = c0 / p.dpg;
+    const int nsc_seg = int(p.seqlen / kSC) / p.nseg;
+    const int sc0 = seg * nsc_seg, sc1 = sc0 + nsc_seg;
+
+    const rsrc_t Ru = make_rsrc(static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds);
+    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
+    const rsrc_t RB = make_rsrc(static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs);
+    constexpr uint32_t es = sizeof(IT);
+    const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
+    const uint32_t oB = uint32_t(row * p.B_ns + 4 * r) * es;
+
+    const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
+    const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
+    const bool softplus = p.softplus != 0;
+
+    struct Seg { float4 u, d, B; };
+    auto fetch = [&](int sc, Seg& S) {
+        const uint32_t so = uint32_t(sc * kSC) * es;
+        S.u = bload4<IT>(Ru, ou, so);
+        S.d = bload4<IT>(Rd, od, so);
+        S.B = bload4<IT>(RB, oB, so);
+    };
+    auto stage = [&](const Seg& S, int buf) {
+        *reinterpret_cast<float4*>(s_b + buf * 16 * kSC + bc64_slot(row, r)) = S.B;
+    };
+
+    float h = 0.f, dsum = 0.f;
+    Seg S;
+    fetch(sc0, S);
+    stage(S, 0);
+    for (int sc = sc0; sc < sc1; ++sc) {
+        const int buf = (sc - sc0) & 1;
+        lds_barrier();   // B tile of sc staged
+        const float4 cu = S.u, cd = S.d;
+        fetch(sc + 1 < sc1 ? sc + 1 : sc1 - 1, S);
+        float4 dt, dtu;
+        {
+            const float p0 = cd.x + bias, p1 = cd.y + bias, p2 = cd.z + bias, p3 = cd.w + bias;
+            dt = softplus ? make_float4(softplus20(p0), softplus20(p1), softplus20(p2), softplus20(p3))
+                          : make_float4(p0, p1, p2, p3);
+            dtu = make_float4(dt.x * cu.x, dt.y * cu.y, dt.z * cu.z, dt.w * cu.w);
+        }
+        dsum += (dt.x + dt.y) + (dt.z + dt.w);
+        dpp_sources_ready4(dt, dtu);
+        const float* sB = s_b + buf * 16 * kSC;
+        static_for<kQ>([&](auto Q) {
+            constexpr int q = decltype(Q)::value;
+            float Bq[kT];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
+                Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
+            }
+            float a[kT];
+            static_for<kT>([&](auto K) {
+                constexpr int k = decltype(K)::value;
+                a[k] = __builtin_amdgcn_exp2f(row_bcast<4 * q + k / 4>(f4get(dt, k % 4)) * a2);
+            });
+            static_for<kT>([&](auto K) {
+                constexpr int k = decltype(K)::value;
+                h = __builtin_fmaf(a[k], h, bmul<4 * q + k / 4>(f4get(dtu, k % 4), Bq[k]));
+            });
+        });
+        stage(S, buf ^ 1);
+    }
+    const int64_t si = (b * p.nseg + seg) * p.dim + c;
+    p.seg_h[si * kT + r] = h;
+    dsum = row_allsum(dsum);                       // the row's 16 lanes hold 4 steps each
+    if (r == 0) p.seg_s[si] = dsum;
+}
+
+// Segments for the forward: enough that batch x channel blocks x segments
+// reaches kSegTargetWGs workgroups (three per CU), each segment a whole
+// number of at least kSegMinSC super-chunks; 1 (serial) when the batch
+// already fills the GPU or the fast path does not apply.
+bool fwd_fast_ok(const FwdParams& p);
+constexpr int64_t kSegTargetWGs = 768;
+constexpr int kSegMinSC = 4;
+constexpr int kSegMax = 64;
+int fwd_segments(const FwdParams& p) {
+    if (!fwd_fast_ok(p)) return 1;
+    const int64_t wgs = p.batch * (p.dim / kChPerWG);
+    const int64_t nsc = p.seqlen / kSC;
+    int nseg = 1;
+    while (wgs * nseg < kSegTargetWGs && 2 * nseg <= kSegMax && nsc % (2 * nseg) == 0 &&
+           nsc / (2 * nseg) >= kSegMinSC)
+        nseg *= 2;
+    return nseg;
 }
 
 bool fwd_fast_ok(const FwdParams& p) {
@@ -419,8 +545,16 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
     const int spl = int((p.dstate + 15) / 16);
     const bool vbc = p.var_B && p.var_C;
     if (fwd_fast_ok(p)) {
-        if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((ss_fwd_fast<IT, false>), grid, block, 0, stream, p);
+        const int nseg = p.nseg > 1 ? p.nseg : 1;
+        if (nseg > 1) {
+            hipLaunchKernelGGL((ss_fwd_seg_state<IT>), dim3(unsigned(nblk * p.batch * (nseg - 1))), block, 0,
+                               stream, p);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        const dim3 sgrid(unsigned(nblk * p.batch * nseg));
+        if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true>), sgrid, block, 0, stream, p);
+        else hipLaunchKernelGGL((ss_fwd_fast<IT, false>), sgrid, block, 0, stream, p);
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, false>), grid, block, 0, stream, p);

@@ -24,7 +24,19 @@ struct FwdParams {
     void* out; float* x;
     void* y;                                  // pre-gate output (z gate only); may be null in forward
     float* last_state;                        // forward: h after the last step, (batch, dim, dstate); may be null
+    // sequence-parallel forward (fast path): the sequence is cut into nseg
+    // equal segments scanned by separate workgroups; seg_h (batch, nseg,
+    // dim, 16) holds each segment's end state from a zero start and seg_s
+    // (batch, nseg, dim) its sum of delta' (nseg 1: the serial scan)
+    int32_t nseg;
+    float* seg_h;
+    float* seg_s;
 };
+// segments the forward uses for p (1: serial), and the workspace they need
+int fwd_segments(const FwdParams& p);
+inline int64_t fwd_seg_bytes(const FwdParams& p, int nseg) {
+    return nseg > 1 ? p.batch * nseg * p.dim * 17 * int64_t(sizeof(float)) : 0;
+}
 
 struct BwdParams {
     FwdParams f;

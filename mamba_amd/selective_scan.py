@@ -139,29 +139,62 @@ def _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x,
     return a
 
 
+def _attach_fwd_workspace(lib, a, workspace, device):
+    """Sets the forward's optional workspace: "auto" allocates what the library
+    asks for (torch's caching allocator; none for most shapes), a tensor is
+    used as given, None runs the serial scan.  Returns the tensor to keep."""
+    if isinstance(workspace, str):
+        _require(workspace == "auto", f"workspace must be 'auto', None or a tensor, got {workspace!r}")
+        n = int(lib.ss_fwd_workspace_bytes(ctypes.byref(a)))
+        if n < 0:
+            nat.check(nat.SS_ERR_INVALID, "selective_scan.forward")
+        workspace = torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
+    if workspace is not None:
+        _require(workspace.is_cuda and workspace.is_contiguous(), "workspace must be a contiguous GPU tensor")
+        a.workspace, a.workspace_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
+    return workspace
+
+
 def forward_into(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None,
-                 last_state=None):
+                 last_state=None, workspace="auto"):
     """Forward into caller-allocated ``out`` (delta's dtype), ``x`` (fp32
     (batch, n_chunks, dim, dstate) contiguous) and, with ``z``, ``y``.
 
     ``x`` and ``y`` are what the backward needs; either may be None for a
     forward that no backward follows (they are then not written at all).
     ``last_state`` (fp32 (batch, dim, dstate), optional) receives the state
-    after the last step."""
+    after the last step.  ``workspace`` ("auto", a tensor or None) lets a
+    forward with few (batch, channel) rows scan sequence segments in
+    parallel (see ``forward_workspace_bytes``)."""
     lib = nat.load()
     a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y, last_state)
+    ws = _attach_fwd_workspace(lib, a, workspace, u.device)
     with torch.cuda.device(u.device):
         nat.check(lib.ss_fwd(ctypes.byref(a), _stream(u.device)), "selective_scan.forward")
+    del ws   # the caching allocator keeps it valid for the work queued on this stream
+
+
+def forward_workspace_bytes(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None):
+    """Bytes of scratch ``forward_into`` can use for these tensors (0: none;
+    nonzero when the batch has too few channel rows to fill the GPU and the
+    sequence is long enough to cut into segments)."""
+    lib = nat.load()
+    a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y)
+    n = lib.ss_fwd_workspace_bytes(ctypes.byref(a))
+    if n < 0:
+        nat.check(nat.SS_ERR_INVALID, "selective_scan.forward_workspace_bytes")
+    return int(n)
 
 
 def prepare_forward(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, *, z=None, y=None,
-                    last_state=None):
+                    last_state=None, workspace="auto"):
     """Validates the arguments of ``forward_into`` once and returns a callable
     that launches the same forward again, on the stream that is current now,
     with no host-side work beyond the C call (the tensors must stay alive
     and keep their storage).  For repeated launches over fixed buffers."""
     lib = nat.load()
     a = _fwd_into_args(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x, z, y, last_state)
+    ws = _attach_fwd_workspace(lib, a, workspace, u.device)
     dev = u.device
     stream = torch.cuda.current_stream(dev)
     handle = ctypes.c_void_p(stream.cuda_stream)
@@ -170,6 +203,7 @@ def prepare_forward(u, delta, A, B, C, D, delta_bias, use_delta_softplus, out, x
     def launch():
         nat.check(lib.ss_fwd(ref, handle), "selective_scan.forward")
     launch.args = a
+    launch.workspace = ws
     return launch
 
 

@@ -59,7 +59,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 7
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 8
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -442,3 +442,18 @@ def test_rmsnorm_python_boundary_refuses_cpu_tensors():
     from mamba_amd.ops.rms_norm import rms_norm_fn
     with pytest.raises(ValueError, match="no CPU path"):
         rms_norm_fn(torch.randn(2, 8), torch.zeros(8))
+
+
+def test_forward_workspace_query(nat, lib):
+    # sequence segments only when batch x (dim / 16) is below 768 workgroups, the
+    # fast path applies and segments keep at least 4 x 64 steps
+    a = valid_fwd(nat, batch=1, dim=1536, seqlen=32768)
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 1 * 8 * 1536 * 17 * 4      # 96 blocks -> 8 segments
+    a = valid_fwd(nat, batch=8, dim=1536, seqlen=2048)
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 0                           # 768 blocks already
+    a = valid_fwd(nat, batch=1, dim=64, seqlen=4096)
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 1 * 16 * 64 * 17 * 4       # 4 blocks: 64 / 16 = 4 sc each
+    a = valid_fwd(nat, batch=1, dim=64, seqlen=100)
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 0                           # general kernel: serial
+    a.u = None
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == -1

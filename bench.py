@@ -17,6 +17,8 @@ reference's own op order run on the same GPU, not against the CPU):
   mamba_block_b8_l2048_d1024_bf16   MambaSimple block (d_model 1024, d_inner
       2048, dt_rank 64, dstate 16, conv 4) forward + backward, bf16 weights
       and activations, fp32 A / D, hidden states ~ N(0, 1) of (8, 2048, 1024);
+  mamba_block_b1_l32768_d1024_bf16  the same block on one sequence of 32768
+      (long-context training: the scan runs in sequence segments);
   causal_lm_24x768_b16_l2048_bf16   CausalLM (24 layers, d_model 768, vocab
       50280) forward in eval mode on token ids of (16, 2048);
   causal_lm_24x768_b1_l32768_bf16   the same model on one sequence of 32768.
@@ -60,6 +62,7 @@ DEFAULT = "ss_fwd_bwd_b8_d1536_n16_l2048_f32"
 MODEL_WORKLOADS = {
     # name: (kind, batch, seqlen, d_model, layers, vocab)
     "mamba_block_b8_l2048_d1024_bf16": ("block", 8, 2048, 1024, 1, 0),
+    "mamba_block_b1_l32768_d1024_bf16": ("block", 1, 32768, 1024, 1, 0),
     "causal_lm_24x768_b16_l2048_bf16": ("lm", 16, 2048, 768, 24, 50280),
     "causal_lm_24x768_b1_l32768_bf16": ("lm", 1, 32768, 768, 24, 50280),
 }
@@ -274,7 +277,7 @@ def bench_model(args):
         ms = timed(step)
         block.use_fast_path = False
         ms_ref = timed(step) if not args.no_ref_order else None
-        metric = "Mamba block fwd+bwd tokens/s, d_model 1024, seqlen 2048"
+        metric = f"Mamba block fwd+bwd tokens/s, d_model {d_model}, seqlen {seqlen}"
         config = {"workload": args.workload, "batch": batch, "seqlen": seqlen, "d_model": d_model,
                   "d_inner": 2 * d_model, "dt_rank": block.delta_rank, "dstate": 16, "d_conv": 4,
                   "dtype": "bf16 (A, D fp32)"}

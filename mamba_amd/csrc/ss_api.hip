@@ -214,14 +214,19 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
 
 // Workspace layout for p: slices and bytes (0 when the fast backward does
 // not use one: other kernel, one slice, or dB / dC not 16-byte aligned).
-int64_t ws_bytes_for(const ss::BwdParams& p, int* slices) {
+// Backward workspace: the dB / dC slices (when they apply), then the
+// sequence-segment carries (when they apply).  *slice_bytes: the first part.
+int64_t ws_bytes_for(const ss::BwdParams& p, int* slices, int* nseg, int64_t* slice_bytes) {
     *slices = ss::bwd_ws_slices(p);
+    *slice_bytes = 0;
     if (*slices <= 1 || !aligned(p.dB, 16) || !aligned(p.dC, 16)) {
         *slices = 1;
-        return 0;
+    } else {
+        const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * p.f.seqlen;
+        *slice_bytes = int64_t(2) * *slices * stride * int64_t(sizeof(float));
     }
-    const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * p.f.seqlen;
-    return int64_t(2) * *slices * stride * int64_t(sizeof(float));
+    *nseg = ss::bwd_segments(p);
+    return *slice_bytes + ss::fwd_seg_bytes(p.f, *nseg);
 }
 
 int check_conv(const ss_conv1d_args* a, bool* empty) {
@@ -325,8 +330,9 @@ int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a) {
     if (check_bwd(a, &empty) != SS_OK) return -1;
     ok();
     if (empty) return 0;
-    int slices = 1;
-    return ws_bytes_for(make_bwd_params(a), &slices);
+    int slices = 1, nseg = 1;
+    int64_t slice_bytes = 0;
+    return ws_bytes_for(make_bwd_params(a), &slices, &nseg, &slice_bytes);
 }
 
 const char* ss_fwd_kernel_name(const ss_fwd_args* a) {
@@ -365,16 +371,24 @@ int ss_bwd(const ss_bwd_args* a, void* stream) {
         return ok();
     }
     ss::BwdParams p = make_bwd_params(a);
-    int slices = 1;
-    const int64_t need = ws_bytes_for(p, &slices);
+    int slices = 1, nseg = 1;
+    int64_t slice_bytes = 0;
+    const int64_t need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
     if (need > 0 && a->workspace) {
         if (a->workspace_bytes < need)
             return fail(SS_ERR_INVALID, "workspace of %lld bytes, %lld needed", (long long)a->workspace_bytes,
                         (long long)need);
         if (!aligned(a->workspace, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
-        p.ws = static_cast<float*>(a->workspace);
-        p.ws_slices = slices;
-        p.ws_stride = need / int64_t(sizeof(float)) / (2 * slices);
+        if (slice_bytes > 0) {
+            p.ws = static_cast<float*>(a->workspace);
+            p.ws_slices = slices;
+            p.ws_stride = slice_bytes / int64_t(sizeof(float)) / (2 * slices);
+        }
+        if (nseg > 1) {
+            p.f.nseg = nseg;
+            p.f.seg_h = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + slice_bytes);
+            p.f.seg_s = p.f.seg_h + p.f.batch * nseg * p.f.dim * 16;
+        }
     }
     hipError_t e = ss::launch_bwd(p, a->f.itype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));

@@ -411,14 +411,20 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const int j = lane >> 4;
     const int row = w * kRows + j;
     const int64_t nblk = p.dim / kChPerWG;
+    // logical workgroup (b, seg, channel block), channel block fastest
     const int64_t blk = xcd_block_id();
-    const int64_t b = blk / nblk;
+    const int nseg = p.nseg;
+    const int64_t bs = blk / nblk;
+    const int64_t b = bs / nseg;
+    const int seg = int(bs % nseg);
     const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
     const int64_t L = p.seqlen;
     const int64_t G = p.dim / p.dpg;
     const int nck = int(L / kT);     // even; below 2^22 (seqlen < 2^26)
+    // this workgroup's chunks [k0, k1), an even number starting at an even index
+    const int k0 = seg * (nck / nseg), k1 = k0 + nck / nseg;
 
     // Buffer resources at the workgroup's rows; lane (row, r) owns step r of
     // channel c0 + row and, for the B / C staging, step r of state row.  The
@@ -519,7 +525,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         flush_commit(ck, v);
     };
 
+    // the adjoint carry entering this segment from the right: the later
+    // segments' carries (each from a zero start) joined right to left,
+    // carry <- exp(A sum delta') carry + G
     float gacar = 0.f, dA_acc = 0.f, dD_acc = 0.f, db_acc = 0.f;
+    for (int s2 = nseg - 1; s2 > seg; --s2) {
+        const int64_t si = (b * nseg + s2) * p.dim + c;
+        gacar = __builtin_fmaf(__builtin_amdgcn_exp2f(a2 * p.seg_s[si]), gacar, p.seg_h[si * kT + r]);
+    }
 
     // One chunk: `cur` holds its inputs (fetched two chunks ago) and is
     // refilled with chunk ck - 2; `nxt` holds chunk ck - 1, staged at the end.
@@ -529,7 +542,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         constexpr int buf = decltype(BUF)::value;
         lds_barrier();   // B / C tile of ck staged; dB / dC partials of ck + 1 complete
         const Chunk cur = cur_in;
-        fetch(ck > 1 ? ck - 2 : 0, cur_in);
+        fetch(ck > k0 + 1 ? ck - 2 : k0, cur_in);
 
         // B / C of this lane's state for the 16 steps of the chunk
         float Bq[kT], Cq[kT];
@@ -562,7 +575,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         });
         // the LDS reads issued above have had the decay factors to land
         __builtin_amdgcn_sched_barrier(0);
-        flush_commit(ck + 1 < nck ? ck + 1 : nck - 1, fv);
+        flush_commit(ck + 1 < k1 ? ck + 1 : k1 - 1, fv);
         float hcur = h0;
         static_for<kT>([&](auto K) {
             constexpr int k = decltype(K)::value;
@@ -658,20 +671,20 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         stage(nxt, buf ^ 1);
     };
 
-    // chunks nck - 1, nck - 2 first; two buffers of inputs alternate roles
+    // chunks k1 - 1, k1 - 2 first; two buffers of inputs alternate roles
     Chunk PA, PB;
-    fetch(nck - 1, PA);
-    fetch(nck - 2, PB);
-    // the first flush (of the nonexistent chunk nck) adds these zeros to chunk nck - 1
+    fetch(k1 - 1, PA);
+    fetch(k1 - 2, PB);
+    // the first flush (of the nonexistent chunk k1) adds these zeros to chunk k1 - 1
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s_wg[i * kThreads + tid] = 0.f;     // buffer nck & 1 = 0
+    for (int i = 0; i < 8; ++i) s_wg[i * kThreads + tid] = 0.f;     // buffer k1 & 1 = 0
     stage(PA, 1);
-    for (int ck = nck - 1; ck > 0; ck -= 2) {   // nck is even: ck odd, then even
+    for (int ck = k1 - 1; ck > k0; ck -= 2) {   // k0, k1 even: ck odd, then even
         chunk(ck, PA, PB, std::integral_constant<int, 1>{});
         chunk(ck - 1, PB, PA, std::integral_constant<int, 0>{});
     }
     lds_barrier();
-    flush(0, 0);
+    flush(k0, 0);
 
     // ---- per-channel and per-(channel, state) sums over time and batch
     dD_acc = row_allsum(dD_acc);
@@ -681,6 +694,112 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         if (q.ddelta_bias) atomicAdd(q.ddelta_bias + c, db_acc);
     }
     atomicAdd(q.dA + c * kT + r, dA_acc);
+}
+
+// Pass A of the sequence-parallel backward: workgroup (b, seg, 16 channels)
+// runs the adjoint recurrence over segment seg (segments 1 .. nseg - 1: the
+// carry of the first segment leaves the sequence) from a zero carry, last
+// step first, with the fast backward's lane layout and arithmetic but
+// nothing else (no recomputed state, no gradients), and writes the carry it
+// leaves at the segment's first step, g_t a_t, to seg_h and the segment's
+// sum of delta' to seg_s.
+template <typename IT, bool kZ>
+__global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams q) {
+    __shared__ __attribute__((aligned(16))) float s_c[2 * 16 * kT];                  // [buf][n][t]
+    const FwdParams& p = q.f;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int r = lane & 15;
+    const int j = lane >> 4;
+    const int row = w * kRows + j;
+    const int64_t nblk = p.dim / kChPerWG;
+    const int nsa = p.nseg - 1;
+    const int64_t blk = xcd_block_id();
+    const int64_t bs = blk / nblk;
+    const int64_t b = bs / nsa;
+    const int seg = int(bs % nsa) + 1;
+    const int64_t c0 = (blk % nblk) * kChPerWG;
+    const int64_t c = c0 + row;
+    const int64_t g = c0 / p.dpg;
+    const int nck_seg = int(p.seqlen / kT) / p.nseg;
+    const int k0 = seg * nck_seg, k1 = k0 + nck_seg;
+
+    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
+    const rsrc_t Ro = make_rsrc(static_cast<const IT*>(q.dout) + b * q.do_bs + c0 * q.do_ds);
+    const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
+    const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
+    constexpr uint32_t es = sizeof(IT);
+    const uint32_t od = uint32_t(row * p.dl_ds + r) * es, oo = uint32_t(row * q.do_ds + r) * es;
+    const uint32_t oz = uint32_t(row * p.z_ds + r) * es, oC = uint32_t(row * p.C_ns + r) * es;
+
+    const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
+    const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
+    const bool softplus = p.softplus != 0;
+
+    struct Ck { float d, o, z, C; };
+    auto fetch = [&](int ck, Ck& P) {
+        const uint32_t so = uint32_t(ck * kT) * es;
+        P.d = bload<IT>(Rd, od, so);
+        P.o = bload<IT>(Ro, oo, so);
+        P.z = kZ ? bload<IT>(Rz, oz, so) : 0.f;
+        P.C = bload<IT>(RC, oC, so);
+    };
+    auto stage = [&](const Ck& P, int buf) { s_c[buf * 16 * kT + bc_slot(row, r)] = P.C; };
+
+    float ga = 0.f, dsum = 0.f;
+    Ck P;
+    fetch(k1 - 1, P);
+    stage(P, 0);
+    for (int ck = k1 - 1; ck >= k0; --ck) {
+        const int buf = (k1 - 1 - ck) & 1;
+        lds_barrier();   // C tile of ck staged
+        const Ck cur = P;
+        fetch(ck > k0 ? ck - 1 : k0, P);
+        float Cq[kT];
+        const float* sC = s_c + buf * 16 * kT;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 vc = *reinterpret_cast<const float4*>(sC + bc_slot(r, 4 * i));
+            Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
+        }
+        const float pre = cur.d + bias;
+        float dt = softplus ? softplus20(pre) : pre;
+        float dy = kZ ? cur.o * cur.z * sigmoidf_(cur.z) : cur.o;
+        dsum += dt;
+        dpp_sources_ready(dt, dy, dsum);
+        float as[kT];
+        static_for<kT>([&](auto K) {
+            constexpr int k = decltype(K)::value;
+            as[k] = __builtin_amdgcn_exp2f(row_bcast<k>(dt) * a2);
+        });
+        static_for<kT>([&](auto K) {
+            constexpr int k = kT - 1 - decltype(K)::value;
+            float gv = ga;
+            bfmac<k>(gv, dy, Cq[k]);             // g_t = a_{t+1} g_{t+1} + dy_t C_t
+            ga = gv * as[k];
+        });
+        stage(P, buf ^ 1);
+    }
+    const int64_t si = (b * p.nseg + seg) * p.dim + c;
+    p.seg_h[si * kT + r] = ga;
+    dsum = row_allsum(dsum);                       // the row's 16 lanes hold one step each
+    if (r == 0) p.seg_s[si] = dsum;
+}
+
+bool bwd_fast_ok(const BwdParams& q);
+
+// Segments for the backward: as for the forward (enough for 768
+// workgroups), each segment an even number of at least 16 chunks.
+int bwd_segments(const BwdParams& q) {
+    if (!bwd_fast_ok(q)) return 1;
+    const FwdParams& p = q.f;
+    const int64_t wgs = p.batch * (p.dim / kChPerWG);
+    const int64_t nck = p.seqlen / kT;
+    int nseg = 1;
+    while (wgs * nseg < 768 && 2 * nseg <= 64 && nck % (4 * nseg) == 0 && nck / (2 * nseg) >= 16) nseg *= 2;
+    return nseg;
 }
 
 bool bwd_fast_ok(const BwdParams& q) {
@@ -795,8 +914,15 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     if (fast) {
         const int64_t n4 = sliced ? p.ws_stride / 4 : 0;
         const unsigned rgrid = unsigned(n4 > 0 ? (n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048 : 1);
-        if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((ss_bwd_fast<IT, false>), grid, block, 0, stream, p);
+        const int nseg = p.f.nseg > 1 ? p.f.nseg : 1;
+        if (nseg > 1) {
+            const dim3 agrid(unsigned(nblk * p.f.batch * (nseg - 1)));
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_seg_carry<IT, true>), agrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_seg_carry<IT, false>), agrid, block, 0, stream, p);
+        }
+        const dim3 sgrid(unsigned(nblk * p.f.batch * nseg));
+        if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true>), sgrid, block, 0, stream, p);
+        else hipLaunchKernelGGL((ss_bwd_fast<IT, false>), sgrid, block, 0, stream, p);
         if (sliced) {
             hipLaunchKernelGGL(ss_ws_reduce, dim3(rgrid), dim3(256), 0, stream,
                                reinterpret_cast<const float4*>(p.ws), int(p.ws_slices), n4,

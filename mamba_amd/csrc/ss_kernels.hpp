@@ -24,10 +24,11 @@ struct FwdParams {
     void* out; float* x;
     void* y;                                  // pre-gate output (z gate only); may be null in forward
     float* last_state;                        // forward: h after the last step, (batch, dim, dstate); may be null
-    // sequence-parallel forward (fast path): the sequence is cut into nseg
-    // equal segments scanned by separate workgroups; seg_h (batch, nseg,
-    // dim, 16) holds each segment's end state from a zero start and seg_s
-    // (batch, nseg, dim) its sum of delta' (nseg 1: the serial scan)
+    // sequence-parallel scan (fast paths): the sequence is cut into nseg
+    // equal segments handled by separate workgroups; seg_h (batch, nseg,
+    // dim, 16) holds each segment's end state (forward) or adjoint carry
+    // (backward) from a zero start and seg_s (batch, nseg, dim) its sum of
+    // delta' (nseg 1: the serial scan)
     int32_t nseg;
     float* seg_h;
     float* seg_s;
@@ -60,6 +61,10 @@ struct BwdParams {
 
 // dB / dC slices the fast backward uses for p (1: add into dB / dC directly)
 int bwd_ws_slices(const BwdParams& p);
+// sequence segments the fast backward uses for p (1: serial); its pass A
+// writes each segment's adjoint carry to f.seg_h and its sum of delta' to
+// f.seg_s (the forward's layout and sizes, fwd_seg_bytes)
+int bwd_segments(const BwdParams& p);
 // arrays one clearing launch handles (workspace + five accumulators)
 constexpr int kZeroSegs = 6;
 // clears the accumulators of p (zero_grads) and nothing else: a call with

@@ -358,6 +358,9 @@ def test_workspace_query(nat, lib):
     # 5120 channels: 320 blocks, capped at 16 slices
     b = valid_bwd(nat, batch=1, dim=5120, seqlen=64)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 16 * (16 * 64) * 4
+    # one long sequence: 8 dB / dC slices, then 8 sequence segments (96 blocks -> 768 workgroups)
+    b = valid_bwd(nat, batch=1, dim=1536, seqlen=32768)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 8 * (16 * 32768) * 4 + 1 * 8 * 1536 * 17 * 4
 
 
 # --------------------------------------------------------------------- RMSNorm --

@@ -241,6 +241,43 @@ def test_sequence_parallel_forward_then_backward_matches_oracle():
     assert_close(last.cpu(), rlast, 1e-3, 1e-3, "last_state (forward only)")
 
 
+@pytest.mark.parametrize("shape", [(1, 64, 16, 4096, torch.float32), (1, 1536, 16, 8192, torch.bfloat16)],
+                         ids=["b1-d64-l4096-f32", "b1-d1536-l8192-bf16"])
+def test_sequence_parallel_backward(shape):
+    """Small batches: the backward's segments (adjoint carries scanned in parallel
+    and joined) give the serial backward's gradients (to rounding)."""
+    from mamba_amd import selective_scan as ss
+    batch, dim, N, L, dt = shape
+    print(f"\n[parity] sequence-parallel backward b{batch}-d{dim}-l{L} {dt}", flush=True)
+    x = make_inputs(batch, dim, N, L, seed=33, dtype=dt)
+    dev = torch.device("cuda:0")
+    t = {k: x[k].to(dev) for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias", "dout")}
+    out = torch.empty_like(t["delta"])
+    y = torch.empty_like(out)
+    xck = torch.empty((batch, ss.n_chunks(L), dim, N), dtype=torch.float32, device=dev)
+    ss.forward_into(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], True, out, xck,
+                    z=t["z"], y=y)
+    res = {}
+    for mode in ("serial", "segments"):
+        g = [torch.empty_like(t["u"]), torch.empty_like(t["delta"]),
+             torch.empty(t["A"].shape, device=dev), torch.empty(t["B"].shape, device=dev),
+             torch.empty(t["C"].shape, device=dev), torch.empty(t["D"].shape, device=dev),
+             torch.empty(t["delta_bias"].shape, device=dev), torch.empty_like(t["z"])]
+        args = (t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], t["dout"], xck, True,
+                *g[:7])
+        if mode == "segments":
+            need = ss.workspace_bytes(*args, z=t["z"], y=y, dz=g[7])
+            ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        else:
+            ws = None
+        ss.backward_into(*args, z=t["z"], y=y, dz=g[7], workspace=ws, zero_grads=True)
+        res[mode] = [v.float().cpu() for v in g]
+    tol = 1e-4 if dt == torch.float32 else 2e-2
+    for name, a, b in zip(("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"), res["segments"],
+                          res["serial"]):
+        assert_close(a, b, tol, tol * max(1.0, float(b.abs().max())), name)
+
+
 def test_backward_with_and_without_workspace():
     """The dB / dC slices (workspace) and direct accumulation give the same gradients."""
     from mamba_amd import selective_scan as ss

@@ -9,8 +9,9 @@ Prints one JSON line.  ``value`` is the algorithmic HBM bytes of one
 forward + backward (inputs read and outputs written once, no checkpoints or
 scratch) divided by the measured time per step, in GB/s.  ``roofline``
 describes the dominant kernel, timed with HIP events on the stream it runs
-on; ``cpu_baseline`` times the CPU oracle (pure-PyTorch selective_scan_ref)
-on a bounded slice of the same workload on this host's cores.
+on; ``cpu_baseline`` times the C restatement of the reference's algorithm
+(oracle/ss_oracle.c, float64) on the same workload (or its first batch rows)
+on this host's cores.
 
 Other workloads (``--workload``; one JSON line each, reported against the
 reference's own op order run on the same GPU, not against the CPU):
@@ -330,39 +331,58 @@ def algorithmic_bytes(batch, dim, dstate, seqlen, s, groups=1):
     return fwd, bwd
 
 
-def cpu_baseline(dtype_name, seqlen, dstate, min_seconds=10.0, max_dim=1536):
-    """Times the CPU oracle (fwd + autograd bwd) on 1 batch row x `d` channels
-    at the full sequence length, on this host's cores.  `d` starts at 192 and
-    is doubled until one run takes at least `min_seconds` (bounded by
-    `max_dim`), so the sample is a few seconds to a few tens of seconds."""
+def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
+    """Times the C restatement of the reference's algorithm (oracle/ss_oracle.c:
+    the reference kernels' arithmetic in float64, plain loops) forward +
+    backward on this host's cores: one task per (batch row, 96-channel slice),
+    run by a pool of up to 16 threads (the C calls release the GIL).  A
+    one-slice calibration run estimates the time; the sample is the whole
+    workload when that takes at most `max_seconds`, else its first batch
+    rows.  GB/s uses the same byte formula (and I/O dtype) as ``value``."""
     import torch
-    from oracle.selective_scan_ref import make_inputs, selective_scan_ref
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    torch.set_num_threads(cores)
-    names = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
-    b, d = 1, 192
-    while True:
-        x = make_inputs(b, d, dstate, seqlen, seed=1001, dtype=getattr(torch, dtype_name))
-        ins = {k: x[k].clone().requires_grad_(True) for k in names}
-        t0 = time.perf_counter()
-        out = selective_scan_ref(ins["u"], ins["delta"], ins["A"], ins["B"], ins["C"], ins["D"],
-                                 z=ins["z"], delta_bias=ins["delta_bias"], delta_softplus=True)
-        out.backward(x["dout"])
-        dt = time.perf_counter() - t0
-        print(f"[bench] cpu oracle batch {b} x dim {d}: {dt:.2f} s", file=sys.stderr, flush=True)
-        if dt >= min_seconds or d * 2 > max_dim:
-            break
-        d *= 2
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import c_oracle
+    from oracle.selective_scan_ref import make_inputs
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    slice_ch = 96 if dim % 96 == 0 else dim
+    x = {k: (v.double() if v is not None else None)
+         for k, v in make_inputs(batch, dim, dstate, seqlen, seed=1001, dtype=torch.float32).items()}
+
+    def task(bi, lo):
+        hi = lo + slice_ch
+        ch = lambda t: t[bi:bi + 1, lo:hi].contiguous()
+        u, dl, z, do = ch(x["u"]), ch(x["delta"]), ch(x["z"]), ch(x["dout"])
+        A, D, bias = x["A"][lo:hi].contiguous(), x["D"][lo:hi].contiguous(), x["delta_bias"][lo:hi].contiguous()
+        B, C = x["B"][bi:bi + 1].contiguous(), x["C"][bi:bi + 1].contiguous()
+        c_oracle.fwd(u, dl, A, B, C, D, z=z, delta_bias=bias, delta_softplus=True)
+        c_oracle.bwd(u, dl, A, B, C, D, z=z, delta_bias=bias, delta_softplus=True, dout=do)
+
+    t0 = time.perf_counter()
+    task(0, 0)
+    per_task = time.perf_counter() - t0
+    tasks_per_row = dim // slice_ch
+    rows = batch
+    while rows > 1 and rows * tasks_per_row * per_task / threads > max_seconds:
+        rows //= 2
+    tasks = [(bi, k * slice_ch) for bi in range(rows) for k in range(tasks_per_row)]
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(lambda a: task(*a), tasks))
+    dt = time.perf_counter() - t0
+    print(f"[bench] cpu C oracle: {len(tasks)} tasks of {slice_ch} channels on {threads} threads: {dt:.2f} s",
+          file=sys.stderr, flush=True)
     s = 2 if dtype_name != "float32" else 4
-    fwd_b, bwd_b = algorithmic_bytes(b, d, dstate, seqlen, s)
+    fwd_b, bwd_b = algorithmic_bytes(rows, dim, dstate, seqlen, s)
     return {
         "value": round((fwd_b + bwd_b) / dt / 1e9, 4),
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
-        "sample": f"selective_scan_ref (pure PyTorch) fwd+bwd on batch {b} x dim {d} x seqlen {seqlen} "
-                  f"x dstate {dstate} ({dtype_name}), one run of {dt:.2f} s; same byte formula as value",
-        "elems_per_s": round(b * d * seqlen / dt, 1),
+        "sample": f"oracle/ss_oracle.c (float64 C restatement of the reference kernels) fwd+bwd on batch {rows} "
+                  f"x dim {dim} x seqlen {seqlen} x dstate {dstate}, {len(tasks)} tasks of {slice_ch} channels "
+                  f"on {threads} threads, {dt:.2f} s; same byte formula as value",
+        "elems_per_s": round(rows * dim * seqlen / dt, 1),
         "seconds": round(dt, 3),
     }
 
@@ -545,7 +565,7 @@ def main():
         "cpu_baseline": None,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(dtype_name, seqlen, dstate)
+        line["cpu_baseline"] = cpu_baseline(dtype_name, batch, dim, seqlen, dstate)
         line["cpu_baseline"]["gpu_speedup"] = round(gbs / line["cpu_baseline"]["value"], 1)
     print(json.dumps(line), flush=True)
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 8
+#define SS_ABI_VERSION 9
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -333,6 +333,26 @@ typedef struct ss_conv1d_update_args {
 
 int ss_state_update(const ss_state_update_args* a, void* stream);
 int ss_conv1d_update(const ss_conv1d_update_args* a, void* stream);
+
+/* Decode-size linear layer on the matrix cores, nn.Linear's layout:
+ *   y[b, n] = sum_k x[b, k] * weight[n, k] (+ bias[n])
+ * for the few rows of a single-token step (the block's projections).  x, y:
+ * (batch, n_out / k_in) rows; weight: (n_out, k_in) rows; unit column
+ * strides, row strides multiples of 4 elements, 8-byte aligned bases; k_in a
+ * multiple of 16; dtype bf16 or fp16; bias of that dtype or fp32.  No
+ * counterpart in the reference (it has no decode path). */
+typedef struct ss_decode_linear_args {
+    int64_t batch, n_out, k_in;
+    int32_t dtype;                       /* SS_BF16 or SS_F16: x, weight, y */
+    int32_t bias_dtype;                  /* dtype or SS_F32 (ignored without bias) */
+    int64_t x_row_stride, w_row_stride, y_row_stride;
+    const void* x;
+    const void* weight;
+    const void* bias;                    /* may be NULL */
+    void* y;
+} ss_decode_linear_args;
+
+int ss_decode_linear(const ss_decode_linear_args* a, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
@@ -21,7 +21,7 @@ EXPORTED = (
     "ss_fwd_kernel_name", "ss_bwd_kernel_name",
     "ss_fwd", "ss_bwd", "ss_conv1d_fwd", "ss_conv1d_bwd",
     "ss_rmsnorm_fwd", "ss_rmsnorm_bwd", "ss_rmsnorm_bwd_workspace_bytes",
-    "ss_state_update", "ss_conv1d_update",
+    "ss_state_update", "ss_conv1d_update", "ss_decode_linear",
 )
 
 _i64, _i32, _p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
@@ -132,6 +132,15 @@ class Conv1dUpdateArgs(ctypes.Structure):
     ]
 
 
+class DecodeLinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("n_out", _i64), ("k_in", _i64),
+        ("dtype", _i32), ("bias_dtype", _i32),
+        ("x_row_stride", _i64), ("w_row_stride", _i64), ("y_row_stride", _i64),
+        ("x", _p), ("weight", _p), ("bias", _p), ("y", _p),
+    ]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -167,6 +176,8 @@ def load():
         lib.ss_conv1d_fwd.restype = ctypes.c_int
         lib.ss_conv1d_bwd.argtypes = [ctypes.POINTER(Conv1dBwdArgs), _p]
         lib.ss_conv1d_bwd.restype = ctypes.c_int
+        lib.ss_decode_linear.argtypes = [ctypes.POINTER(DecodeLinearArgs), _p]
+        lib.ss_decode_linear.restype = ctypes.c_int
         lib.ss_state_update.argtypes = [ctypes.POINTER(StateUpdateArgs), _p]
         lib.ss_state_update.restype = ctypes.c_int
         lib.ss_conv1d_update.argtypes = [ctypes.POINTER(Conv1dUpdateArgs), _p]

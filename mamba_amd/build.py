@@ -14,7 +14,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "libmamba_ss.so")
 ARCH = os.environ.get("MAMBA_AMD_ARCH", "gfx950")
-SOURCES = ["ss_api.hip", "ss_fwd.hip", "ss_bwd.hip", "conv1d.hip", "rms_norm.hip", "decode.hip"]
+SOURCES = ["ss_api.hip", "ss_fwd.hip", "ss_bwd.hip", "conv1d.hip", "rms_norm.hip", "decode.hip", "decode_linear.hip"]
 
 
 def hipcc():

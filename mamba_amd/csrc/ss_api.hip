@@ -490,6 +490,32 @@ int ss_conv1d_update(const ss_conv1d_update_args* a, void* stream) {
     return ok();
 }
 
+int ss_decode_linear(const ss_decode_linear_args* a, void* stream) {
+    if (!a) return fail(SS_ERR_INVALID, "null argument block");
+    if (a->batch < 0 || a->n_out < 0 || a->k_in < 0)
+        return fail(SS_ERR_INVALID, "negative size (batch=%lld n_out=%lld k_in=%lld)", (long long)a->batch,
+                    (long long)a->n_out, (long long)a->k_in);
+    if (a->dtype != SS_BF16 && a->dtype != SS_F16)
+        return fail(SS_ERR_UNSUPPORTED, "dtype %d: the matrix-core path takes bf16 or fp16", a->dtype);
+    if (a->bias && a->bias_dtype != a->dtype && a->bias_dtype != SS_F32)
+        return fail(SS_ERR_UNSUPPORTED, "bias dtype %d must be the row dtype or fp32", a->bias_dtype);
+    if (a->k_in % 16 != 0) return fail(SS_ERR_UNSUPPORTED, "k_in=%lld is not a multiple of 16", (long long)a->k_in);
+    if (a->batch == 0 || a->n_out == 0) return ok();
+    if (a->k_in == 0) return fail(SS_ERR_UNSUPPORTED, "k_in=0");
+    if ((a->n_out + 15) / 16 > INT32_MAX || (a->batch + 15) / 16 > 65535)
+        return fail(SS_ERR_UNSUPPORTED, "n_out or batch too large");
+    if (!a->x || !a->weight || !a->y) return fail(SS_ERR_INVALID, "x / weight / y is NULL");
+    if (!aligned(a->x, 8) || !aligned(a->weight, 8) || !aligned(a->y, 2))
+        return fail(SS_ERR_INVALID, "x / weight must be 8-byte aligned, y 2-byte aligned");
+    if (a->bias && !aligned(a->bias, a->bias_dtype == SS_F32 ? 4 : 2)) return fail(SS_ERR_INVALID, "bias is misaligned");
+    if (a->x_row_stride < a->k_in || a->w_row_stride < a->k_in || a->y_row_stride < a->n_out ||
+        a->x_row_stride % 4 || a->w_row_stride % 4)
+        return fail(SS_ERR_INVALID, "row strides must cover the rows, x / weight strides multiples of 4");
+    hipError_t e = ss::decode_linear_launch(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "decode linear launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
 int64_t ss_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim) {
     if (rows < 0 || dim < 0) {
         fail(SS_ERR_INVALID, "negative size (rows=%lld dim=%lld)", (long long)rows, (long long)dim);

@@ -89,6 +89,8 @@ hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, h
 // single-token decode: selective-scan state update and conv1d state update
 hipError_t state_update_launch(const ss_state_update_args* a, hipStream_t stream);
 hipError_t conv_update_launch(const ss_conv1d_update_args* a, hipStream_t stream);
+// decode-size linear layer (matrix cores)
+hipError_t decode_linear_launch(const ss_decode_linear_args* a, hipStream_t stream);
 // RMSNorm (+ residual); g == nullptr: forward, else backward (two kernels:
 // per-workgroup dweight rows into g->workspace, then their fixed-order sum)
 hipError_t rmsnorm_launch(const ss_rmsnorm_args* a, const ss_rmsnorm_bwd_args* g, hipStream_t stream);

@@ -105,16 +105,21 @@ class CausalLM(nn.Module):
         return self.lm_head(self.norm(hidden_states, residual=residual))
 
     @torch.no_grad()
-    def generate(self, input_ids, max_new_tokens=50, temperature=1.0, generator=None):
+    def generate(self, input_ids, max_new_tokens=50, temperature=1.0, generator=None, use_graph=None):
         """input_ids (batch, seqlen) -> (batch, seqlen + max_new_tokens): the prompt is
         run once (filling the decode cache), then one token at a time is sampled
         from softmax(logits / temperature) (temperature 0: the argmax) and fed back
-        through ``step``.  The reference declares this method without a body
+        through ``step``.  ``use_graph`` (default: on a ROCm device when at least 8
+        tokens are generated) replays the step as one captured HIP graph
+        (``GraphedStep``).  The reference declares this method without a body
         (models/causal_lm.py:61-62)."""
         if max_new_tokens <= 0:
             return input_ids
         cache = self.allocate_inference_cache(input_ids.shape[0], device=input_ids.device)
         logits = self(input_ids, inference_cache=cache)[:, -1]
+        if use_graph is None:
+            use_graph = input_ids.is_cuda and max_new_tokens >= 8
+        step = GraphedStep(self, cache, input_ids.shape[0]) if use_graph else (lambda ids: self.step(ids, cache))
         tokens = [input_ids]
         for i in range(max_new_tokens):
             if temperature == 0:
@@ -124,7 +129,7 @@ class CausalLM(nn.Module):
                 nxt = torch.multinomial(probs, 1, generator=generator)[:, 0]
             tokens.append(nxt[:, None])
             if i + 1 < max_new_tokens:
-                logits = self.step(nxt, cache)
+                logits = step(nxt)
         return torch.cat(tokens, dim=1)
 
 

@@ -24,6 +24,7 @@ import torch
 import torch.nn as nn
 
 from ..ops.causal_conv1d import causal_conv1d_update
+from ..ops.decode_linear import decode_linear
 from ..ops.selective_scan_interface import SelectiveScanFn, mamba_inner_fn, mamba_inner_prefill
 from ..ops.selective_state_update import selective_state_update
 
@@ -129,16 +130,16 @@ class MambaSimple(nn.Module):
         shape; conv_state and ssm_state are advanced in place."""
         squeeze = hidden_states.dim() == 3
         h = hidden_states.reshape(-1, self.model_dim)
-        xz = torch.nn.functional.linear(h, self.input_proj.weight, self.input_proj.bias)   # (batch, 2 * inner)
+        xz = decode_linear(h, self.input_proj.weight, self.input_proj.bias)          # (batch, 2 * inner)
         x, z = xz[:, :self.inner_dim], xz[:, self.inner_dim:]
         A, D, dt_bias, conv_w, conv_b = self._decode_params()
         x = causal_conv1d_update(x, conv_state, conv_w, conv_b, "silu")
-        x_db = torch.nn.functional.linear(x, self.ssm_param_proj.weight)             # (batch, R + 2N)
+        x_db = decode_linear(x, self.ssm_param_proj.weight)                          # (batch, R + 2N)
         R, N = self.delta_rank, self.state_dim
-        dt = torch.nn.functional.linear(x_db[:, :R], self.delta_proj.weight)         # bias goes in the update
+        dt = decode_linear(x_db[:, :R], self.delta_proj.weight)                     # bias goes in the update
         y = selective_state_update(ssm_state, x, dt, A, x_db[:, R:R + N], x_db[:, R + N:], D, z=z,
                                    dt_bias=dt_bias, dt_softplus=True)
-        out = self.output_proj(y)
+        out = decode_linear(y, self.output_proj.weight, self.output_proj.bias)
         return out.unsqueeze(1) if squeeze else out
 
     def _decode_params(self):

@@ -59,7 +59,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 8
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 9
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -82,7 +82,8 @@ def test_struct_layout_matches_c_compiler(nat, lib, tmp_path):
     structs = ((nat.FwdArgs, "ss_fwd_args"), (nat.BwdArgs, "ss_bwd_args"),
                (nat.Conv1dArgs, "ss_conv1d_args"), (nat.Conv1dBwdArgs, "ss_conv1d_bwd_args"),
                (nat.RmsNormArgs, "ss_rmsnorm_args"), (nat.RmsNormBwdArgs, "ss_rmsnorm_bwd_args"),
-               (nat.StateUpdateArgs, "ss_state_update_args"), (nat.Conv1dUpdateArgs, "ss_conv1d_update_args"))
+               (nat.StateUpdateArgs, "ss_state_update_args"), (nat.Conv1dUpdateArgs, "ss_conv1d_update_args"),
+               (nat.DecodeLinearArgs, "ss_decode_linear_args"))
     fields = [f"F({name}, {n})" for T, name in structs for n, _ in T._fields_]
     fields += [f'printf("sizeof {name} %zu\\n", sizeof({name}));' for _, name in structs]
     src = tmp_path / "probe.c"

@@ -190,3 +190,39 @@ def test_graphed_step_replays_match_eager():
         assert torch.equal(got, want), f"replay {t} differs from the eager step"
         for (c1, s1), (c2, s2) in zip(cache_g, cache_e):
             assert torch.equal(c1, c2) and torch.equal(s1, s2), f"cache after replay {t}"
+
+
+LIN_CASES = [
+    # batch, k_in, n_out, dtype, bias dtype (None: no bias), x as a column slice of a wider tensor
+    (16, 768, 3072, torch.bfloat16, None, False),
+    (16, 1536, 80, torch.bfloat16, None, False),
+    (16, 48, 1536, torch.bfloat16, None, True),
+    (5, 64, 37, torch.bfloat16, torch.float32, False),
+    (33, 128, 100, torch.float16, torch.float16, False),
+    (64, 1024, 50, torch.bfloat16, torch.bfloat16, True),
+]
+
+
+@pytest.mark.parametrize("case", LIN_CASES, ids=[f"b{c[0]}-k{c[1]}-n{c[2]}-{str(c[3]).split('.')[-1]}"
+                                                  f"{'-bias' if c[4] is not None else ''}{'-slice' if c[5] else ''}"
+                                                  for c in LIN_CASES])
+def test_decode_linear_matches_fp32_product(case):
+    # the matrix-core kernel (operand layouts, K split over waves, tails in n and batch)
+    # against the same product in fp32
+    from mamba_amd.ops.decode_linear import _fits, decode_linear
+    batch, k, n, dt, bdt, sliced = case
+    _say(f"decode linear {case}")
+    gen = torch.Generator().manual_seed(400 + k + n)
+    if sliced:
+        wide = torch.randn(batch, k + 32, generator=gen).to(dt).to(DEV)
+        x = wide[:, 16:16 + k]
+    else:
+        x = torch.randn(batch, k, generator=gen).to(dt).to(DEV)
+    w = (torch.randn(n, k, generator=gen) / k ** 0.5).to(dt).to(DEV)
+    b = torch.randn(n, generator=gen).to(bdt).to(DEV) if bdt is not None else None
+    assert _fits(x, w, b), "this case must take the HIP kernel"
+    y = decode_linear(x, w, b)
+    want = x.float() @ w.float().t() + (b.float() if b is not None else 0.0)
+    assert y.dtype == dt and y.shape == (batch, n)
+    scale = float(want.abs().max())
+    assert_close(y.float().cpu(), want.cpu(), 1e-2, 1e-2 * scale, "y")

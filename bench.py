@@ -426,7 +426,8 @@ def main():
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE {world}); the selective scan would shard by batch or channel "
-              "(see DESIGN.md), which is not built here.", file=sys.stderr)
+              "with one exchange of dA / dD / delta-bias (or dB / dC) gradients, which is not built here.",
+              file=sys.stderr)
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)

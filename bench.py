@@ -22,7 +22,9 @@ reference's own op order run on the same GPU, not against the CPU):
       (long-context training: the scan runs in sequence segments);
   causal_lm_24x768_b16_l2048_bf16   CausalLM (24 layers, d_model 768, vocab
       50280) forward in eval mode on token ids of (16, 2048);
-  causal_lm_24x768_b1_l32768_bf16   the same model on one sequence of 32768.
+  causal_lm_24x768_b1_l32768_bf16   the same model on one sequence of 32768;
+  causal_lm_24x768_b8_l2048_train_bf16  a training step of that model (forward,
+      cross-entropy, backward, AdamW; dropout 0.15 as configured) on (8, 2048).
 ``value`` is tokens per second; ``ref_op_order`` gives the same step with
 the reference's op sequence (RMSNorm and MambaSimple as PyTorch ops around
 SelectiveScanFn, the residual added after each block).
@@ -66,6 +68,7 @@ MODEL_WORKLOADS = {
     "mamba_block_b1_l32768_d1024_bf16": ("block", 1, 32768, 1024, 1, 0),
     "causal_lm_24x768_b16_l2048_bf16": ("lm", 16, 2048, 768, 24, 50280),
     "causal_lm_24x768_b1_l32768_bf16": ("lm", 1, 32768, 768, 24, 50280),
+    "causal_lm_24x768_b8_l2048_train_bf16": ("lm_train", 8, 2048, 768, 24, 50280),
 }
 
 NORM_WORKLOADS = {
@@ -282,6 +285,31 @@ def bench_model(args):
         config = {"workload": args.workload, "batch": batch, "seqlen": seqlen, "d_model": d_model,
                   "d_inner": 2 * d_model, "dt_rank": block.delta_rank, "dstate": 16, "d_conv": 4,
                   "dtype": "bf16 (A, D fp32)"}
+    elif kind == "lm_train":
+        cfg = CausalLMConfig(vocab_size=vocab, model_dim=d_model, state_dim=16, conv_kernel=4,
+                             expansion_factor=2, num_layers=layers)
+        model = CausalLM(cfg, device=dev, dtype=dt).train()
+        ids = torch.randint(0, vocab, (batch, seqlen + 1), device=dev)
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+
+        def step():
+            logits = model(ids[:, :-1])
+            loss = torch.nn.functional.cross_entropy(logits.reshape(-1, vocab).float(), ids[:, 1:].reshape(-1))
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            opt.step()
+            return loss
+
+        ms = timed(step)
+        for layer in model.layers:
+            layer.mamba.use_fast_path = False
+            layer.norm.use_fast_path = False
+        model.norm.use_fast_path = False
+        ms_ref = timed(step) if not args.no_ref_order else None
+        metric = f"CausalLM training tokens/s, {layers} layers, d_model {d_model}, seqlen {seqlen}"
+        config = {"workload": args.workload, "batch": batch, "seqlen": seqlen, "d_model": d_model,
+                  "layers": layers, "vocab": vocab, "dtype": "bf16 (A, D fp32)",
+                  "step": "forward, cross-entropy, backward, AdamW", "dropout": cfg.dropout_rate}
     else:
         cfg = CausalLMConfig(vocab_size=vocab, model_dim=d_model, state_dim=16, conv_kernel=4,
                              expansion_factor=2, num_layers=layers)

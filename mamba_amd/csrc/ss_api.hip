@@ -134,6 +134,8 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.out = a->out; p.x = a->x;
     p.y = a->has_z ? a->y : nullptr;
     p.last_state = a->last_state;
+    p.x_records = p.x ? -1 : 0;
+    p.y_records = p.y ? -1 : 0;
     p.nseg = 1;
     p.y_bs = a->y_batch_stride; p.y_ds = a->y_dim_stride;
     return p;

@@ -378,11 +378,14 @@ constexpr int kRsrcWord3 = 0x00020000;   // gfx9-family raw buffer, 32-bit data 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, kRsrcWord3);
 }
-// As make_rsrc, or, when !live, a resource of zero bytes: the hardware's range
-// check then drops every store through it (and loads return 0), so an
-// optional output costs no branch in the loop and no memory traffic.
-__device__ __forceinline__ rsrc_t make_rsrc_opt(const void* base, bool live) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, live ? -1 : 0, kRsrcWord3);
+// As make_rsrc with nrec bytes: -1 for the whole range, or 0 for a resource
+// of zero bytes, through which the hardware's range check drops every store
+// (and loads return 0), so an optional output costs no branch in the loop
+// and no memory traffic.  nrec must be uniform and come from a kernel
+// argument: a record count the compiler selects in a VGPR makes every
+// access through the resource a waterfall loop.
+__device__ __forceinline__ rsrc_t make_rsrc_n(const void* base, int nrec) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrec, kRsrcWord3);
 }
 // Element (voff + soff bytes) of an IT array as float.
 template <typename T>

@@ -264,9 +264,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     // without a y (or x) buffer the stores go through a zero-byte resource
     // and are dropped: a forward that no backward follows writes neither
     const bool save_y = kZ && p.y != nullptr, save_x = p.x != nullptr;
+    const int y_records = kZ ? p.y_records : 0;
     IT* const gy = save_y ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : go;
     // x: (batch, chunk, dim, dstate)
-    const rsrc_t Rx = make_rsrc_opt(save_x ? p.x + (b * p.n_chunks * p.dim + c0) * kT : nullptr, save_x);
+    const rsrc_t Rx = make_rsrc_n(save_x ? p.x + (b * p.n_chunks * p.dim + c0) * kT : nullptr, p.x_records);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
     const uint32_t oz = uint32_t(row * p.z_ds + 4 * r) * es;
@@ -319,7 +320,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
         if constexpr (kZ) {
-            bstore4<IT>(make_rsrc_opt(gy + int64_t(sc) * kSC, save_y), oy, y);
+            bstore4<IT>(make_rsrc_n(gy + int64_t(sc) * kSC, y_records), oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);

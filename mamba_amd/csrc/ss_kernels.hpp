@@ -24,6 +24,11 @@ struct FwdParams {
     void* out; float* x;
     void* y;                                  // pre-gate output (z gate only); may be null in forward
     float* last_state;                        // forward: h after the last step, (batch, dim, dstate); may be null
+    // buffer record counts of the x and y stores of the fast forward: -1
+    // (the whole range) when the buffer is there, 0 when it is not (the
+    // hardware range check then drops every store); set by the host, so the
+    // resources stay scalar
+    int32_t x_records, y_records;
     // sequence-parallel scan (fast paths): the sequence is cut into nseg
     // equal segments handled by separate workgroups; seg_h (batch, nseg,
     // dim, 16) holds each segment's end state (forward) or adjoint carry

@@ -17,7 +17,11 @@ asm must keep:
   whose uniform offset is a register, so the kernels avoid that form; the
   check covers every wide store;
 * no packed fp32 VALU ops (v_pk_fma_f32, v_pk_mul_f32, v_pk_add_f32): the
-  library is built with them disabled.
+  library is built with them disabled;
+* no waterfall loop inside a scan kernel's main loop: a buffer resource or
+  uniform offset the compiler holds in VGPRs makes every access through it a
+  loop of v_readfirstlane / v_cmp / s_and_saveexec / s_cbranch_execnz, which
+  in the per-chunk loop costs dozens of issue slots per chunk.
 
 The scan is linear over each function's instruction stream, the order the
 compiler laid out; a branch instruction counts as one wait state like any
@@ -94,6 +98,72 @@ def functions(disasm):
         if text and not text.endswith(":"):
             cur.append(text)
     return out
+
+
+def function_code(disasm):
+    """{name: [(address, instruction text), ...]} from llvm-objdump output;
+    branch instructions keep their target as "<name+0xoff>"."""
+    out, cur, start = {}, None, 0
+    for line in disasm.splitlines():
+        m = re.match(r"^([0-9a-f]+) <(\S+)>:", line)
+        if m:
+            start = int(m.group(1), 16)
+            cur = out.setdefault(m.group(2), [])
+            continue
+        if cur is None:
+            continue
+        parts = line.split("//", 1)
+        text = parts[0].strip()
+        if not text or text.endswith(":") or len(parts) < 2:
+            continue
+        m = re.match(r"\s*([0-9A-Fa-f]+):", parts[1])
+        if not m:
+            continue
+        t = re.search(r"<\S+\+0x([0-9a-f]+)>", parts[1])
+        cur.append((int(m.group(1), 16), text + (f" <{start + int(t.group(1), 16)}>" if t else "")))
+    return out
+
+
+def _target(text):
+    m = re.search(r"<(\d+)>$", text)
+    return int(m.group(1)) if m else None
+
+
+def loops(code):
+    """(start, end) address ranges closed by a backward branch.  Blocks the
+    compiler places after s_endpgm jump back into the body without forming
+    a loop; branches from there are left out."""
+    out = []
+    for addr, text in code:
+        if text.startswith("s_endpgm"):
+            break
+        if text.startswith(("s_branch", "s_cbranch")):
+            t = _target(text)
+            if t is not None and t <= addr:
+                out.append((t, addr))
+    return out
+
+
+def waterfall_loops(code):
+    """Backward s_cbranch_execnz loops whose body reads a lane into an SGPR
+    (v_readfirstlane) and narrows exec (s_and_saveexec): the compiler's
+    waterfall loops around a VGPR-held resource or offset."""
+    out = []
+    for t, end in loops(code):
+        body = [text for addr, text in code if t <= addr <= end]
+        if body and body[-1].startswith("s_cbranch_execnz") and \
+                any(x.startswith("v_readfirstlane") for x in body) and any("saveexec" in x for x in body):
+            out.append((t, end))
+    return out
+
+
+def waterfalls_in_main_loop(code):
+    """Waterfall loops inside the function's largest loop."""
+    ls = loops(code)
+    if not ls:
+        return []
+    s0, e0 = max(ls, key=lambda r: r[1] - r[0])
+    return [(s, e) for s, e in waterfall_loops(code) if s0 <= s and e <= e0 and (s, e) != (s0, e0)]
 
 
 def _split(text):

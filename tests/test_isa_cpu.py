@@ -40,6 +40,46 @@ def test_no_hazards_and_no_packed_fp32(funcs):
     assert not problems, "\n".join(f"{k}: {m}" for k, m in problems[:20])
 
 
+@pytest.fixture(scope="module")
+def code():
+    return isa_check.function_code(isa_check.disassemble(LIB, tempfile.mkdtemp()))
+
+
+def test_no_waterfall_loop_in_the_scan_main_loops(code):
+    """The fast scan kernels keep every buffer resource and uniform offset of
+    their per-chunk loop in SGPRs (no waterfall loop inside the main loop)."""
+    fast = [f for f in code if "ss_fwd_fast" in f or "ss_bwd_fast" in f]
+    assert len(fast) >= 4
+    bad = {f: isa_check.waterfalls_in_main_loop(code[f]) for f in fast}
+    assert not any(bad.values()), {f: v for f, v in bad.items() if v}
+
+
+def test_waterfall_check_finds_a_planted_one():
+    """A waterfall loop planted inside a main loop is found; the same loop
+    after the main loop is not counted."""
+    def asm(lines, start=0x1000):
+        out = [f"{start:016x} <k>:"]
+        for i, t in enumerate(lines):
+            a = start + 4 * i
+            tgt = ""
+            if t.startswith(("s_branch", "s_cbranch")):
+                tgt = f" <k+0x{4 * int(t.split('@')[1]):x}>"
+                t = t.split("@")[0]
+            out.append(f"\t{t}   // {a:012X}: 00000000{tgt}")
+        return "\n".join(out)
+    wf = ["v_readfirstlane_b32 s4, v0", "v_cmp_eq_u32_e32 vcc, s4, v0", "s_and_saveexec_b64 s[2:3], vcc",
+          "buffer_store_dword v1, v2, s[4:7], 0 offen", "s_xor_b64 exec, exec, s[2:3]"]
+    inside = ["v_mul_f32_e32 v1, v1, v3"] + wf + ["s_cbranch_execnz @1", "v_add_f32_e32 v1, v1, v3",
+                                                   "s_cbranch_scc1 @0", "s_endpgm"]
+    code_in = isa_check.function_code(asm(inside))["k"]
+    assert len(isa_check.waterfalls_in_main_loop(code_in)) == 1
+    after = ["v_mul_f32_e32 v1, v1, v3", "v_add_f32_e32 v1, v1, v3", "s_cbranch_scc1 @0"] + wf + \
+            ["s_cbranch_execnz @3", "s_endpgm"]
+    code_after = isa_check.function_code(asm(after))["k"]
+    assert len(isa_check.waterfall_loops(code_after)) == 1
+    assert isa_check.waterfalls_in_main_loop(code_after) == []
+
+
 def test_checker_catches_planted_hazards():
     """The checker itself flags a DPP read 1 wait state after the write, a
     transcendental result read at once, and a packed fp32 op."""

@@ -415,8 +415,8 @@ def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
     }
 
 
-def calibrate_copy(mib, reps=5):
-    """Copies `mib` MiB device to device `reps` times; prints one JSON line."""
+def time_copy(mib, reps=5):
+    """Copies `mib` MiB device to device `reps` times; (bytes copied, ms per copy)."""
     import torch
     n = mib * (1 << 20) // 4
     src = torch.randn(n, device="cuda:0")
@@ -430,7 +430,13 @@ def calibrate_copy(mib, reps=5):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    nbytes = n * 4
+    del src, dst
+    return n * 4, ms
+
+
+def calibrate_copy(mib, reps=5):
+    """Copies `mib` MiB device to device `reps` times; prints one JSON line."""
+    nbytes, ms = time_copy(mib, reps)
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "ms": round(ms, 5),
                       "GB/s (read + write)": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
@@ -593,6 +599,12 @@ def main():
         },
         "cpu_baseline": None,
     }
+    # the rate against what this GPU moves in a plain 1 GiB device-to-device
+    # copy (read + write bytes), beside the published peak
+    cb, cms = time_copy(1024)
+    copy_gbs = 2 * cb / (cms * 1e-3) / 1e9
+    line["copy_gbs"] = round(copy_gbs, 1)
+    line["pct_of_copy"] = round(100.0 * gbs / copy_gbs, 2)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(dtype_name, batch, dim, seqlen, dstate)
         line["cpu_baseline"]["gpu_speedup"] = round(gbs / line["cpu_baseline"]["value"], 1)

@@ -7,12 +7,13 @@
 //   pre[b, d, t] = bias[d] + sum_k w[d, k] * x[b, d, t - (width - 1) + k]   (x = 0 before t = 0)
 //   out = silu(pre) or pre
 //
-// Layout: a workgroup of 256 threads covers 1024 consecutive steps of one
-// (batch, channel) row (grid x: rows, grid y: 1024-step segments); each
-// thread 4 consecutive steps.  Rows are read with
-// 4-element vector loads when they are 4-element aligned (seqlen and the
-// strides multiples of 4), element by element otherwise.  The 3-step halo
-// before a thread's steps comes from the previous vector (an L1 / L2 hit).
+// Layout: a workgroup of 256 threads covers 256 VW consecutive steps of one
+// (batch, channel) row (grid x: rows, grid y: segments); each thread VW
+// consecutive steps, one 16-byte vector: VW = 4 for fp32, 8 for 16-bit
+// types when rows are 8-element aligned (4 when they are only 4-element
+// aligned).  Rows that are not vector aligned are read element by element
+// (4 steps per thread).  The 3-step halo before a thread's steps comes from
+// the previous vector (an L1 / L2 hit).
 // The op is HBM-bound: one read of x, one write of out (forward); reads of
 // x and dout, one write of dx, and per-workgroup sums of dweight / dbias
 // (backward).
@@ -28,12 +29,10 @@ namespace ss {
 namespace {
 
 constexpr int kCT = 256;            // threads per workgroup
-constexpr int kCV = 4;              // steps per thread
-constexpr int kCSeg = kCT * kCV;    // steps per workgroup
 
 struct ConvParams {
     int64_t batch, dim, seqlen;
-    int32_t width, has_bias, silu, vec;
+    int32_t width, has_bias, silu, vec;         // vec: elements per vector access (4 or 8), 0 for element access
     int64_t x_bs, x_ds, o_bs, o_ds, w_ds, w_ks;
     int64_t do_bs, do_ds, dx_bs, dx_ds;
     const void* x; const float* w; const float* bias; void* out;
@@ -48,20 +47,29 @@ __device__ __forceinline__ float ld(const IT* p, int64_t i, int64_t n) {
     return (i >= 0 && i < n) ? v : 0.f;
 }
 
-// 4 consecutive elements starting at i (a multiple of 4, 4-element aligned
-// row); zeros outside [0, n) (n is a multiple of 4 on this path)
-template <typename IT>
-__device__ __forceinline__ void ld4(const IT* p, int64_t i, int64_t n, float (&o)[4]) {
+// VW consecutive elements starting at i (a multiple of VW, VW-element
+// aligned row, VW * sizeof(IT) <= 16); zeros outside [0, n) (n is a multiple
+// of VW on this path)
+template <typename IT, int VW>
+__device__ __forceinline__ void ldv(const IT* p, int64_t i, int64_t n, float (&o)[VW]) {
     const bool in = i >= 0 && i < n;
     const int64_t c = in ? i : 0;
     if constexpr (sizeof(IT) == 4) {
+        static_assert(VW == 4, "fp32 rows: 4 elements per vector");
         const float4 v = *reinterpret_cast<const float4*>(p + c);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(p + c);
-        const uint32_t w[2] = {v.x, v.y};
+        uint32_t w[VW / 2];
+        if constexpr (VW == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p + c);
+            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else {
+            static_assert(VW == 4, "16-bit rows: 4 or 8 elements per vector");
+            const uint2 v = *reinterpret_cast<const uint2*>(p + c);
+            w[0] = v.x; w[1] = v.y;
+        }
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
+        for (int k = 0; k < VW / 2; ++k) {
             if constexpr (__is_same(IT, bf16_t)) {
                 o[2 * k] = __uint_as_float(w[k] << 16);
                 o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
@@ -71,45 +79,58 @@ __device__ __forceinline__ void ld4(const IT* p, int64_t i, int64_t n, float (&o
             }
         }
     }
-    if (!in) { o[0] = 0.f; o[1] = 0.f; o[2] = 0.f; o[3] = 0.f; }
-}
-
-template <typename IT>
-__device__ __forceinline__ void st4(IT* p, float (&v)[4]) {
-    if constexpr (sizeof(IT) == 4) {
-        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-    } else if constexpr (__is_same(IT, bf16_t)) {
-        *reinterpret_cast<uint2*>(p) = make_uint2(io<bf16_t>::pack2(v[0], v[1]), io<bf16_t>::pack2(v[2], v[3]));
-    } else {
-        uint2 o;
-        o.x = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[0]))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[1]))) << 16);
-        o.y = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[2]))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[3]))) << 16);
-        *reinterpret_cast<uint2*>(p) = o;
+    if (!in) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) o[k] = 0.f;
     }
 }
 
-// x[t0 - 4 .. t0 + 4 * extra + 3] into xs[0 .. 4 + 4 * extra + 3]
-template <typename IT, bool kVec, int kExtra>
-__device__ __forceinline__ void load_window(const IT* row, int64_t t0, int64_t L, float (&xs)[8 + 4 * kExtra]) {
-    if constexpr (kVec) {
+template <typename IT, int VW>
+__device__ __forceinline__ void stv(IT* p, const float (&v)[VW]) {
+    if constexpr (sizeof(IT) == 4) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+        uint32_t o[VW / 2];
+#pragma unroll
+        for (int k = 0; k < VW / 2; ++k) {
+            if constexpr (__is_same(IT, bf16_t)) {
+                o[k] = io<bf16_t>::pack2(v[2 * k], v[2 * k + 1]);
+            } else {
+                o[k] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[2 * k]))) |
+                       (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[2 * k + 1]))) << 16);
+            }
+        }
+        if constexpr (VW == 8) *reinterpret_cast<uint4*>(p) = make_uint4(o[0], o[1], o[2], o[3]);
+        else *reinterpret_cast<uint2*>(p) = make_uint2(o[0], o[1]);
+    }
+}
+
+// x[t0 - VW .. t0 + VW * (1 + extra) - 1] into xs (VW = 0: element loads
+// of the same window with VW = 4)
+template <typename IT, int VW, int kExtra>
+__device__ __forceinline__ void load_window(const IT* row, int64_t t0, int64_t L,
+                                            float (&xs)[(VW ? VW : 4) * (2 + kExtra)]) {
+    constexpr int V = VW ? VW : 4;
+    if constexpr (VW != 0) {
 #pragma unroll
         for (int q = 0; q < 2 + kExtra; ++q) {
-            float v[4];
-            ld4<IT>(row, t0 - 4 + 4 * q, L, v);
+            float v[VW];
+            ldv<IT, VW>(row, t0 - VW + VW * q, L, v);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) xs[4 * q + k] = v[k];
+            for (int k = 0; k < VW; ++k) xs[VW * q + k] = v[k];
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8 + 4 * kExtra; ++i) xs[i] = ld<IT>(row, t0 - 4 + i, L);
+        for (int i = 0; i < V * (2 + kExtra); ++i) xs[i] = ld<IT>(row, t0 - V + i, L);
     }
 }
 
-template <typename IT, bool kVec>
+template <typename IT, int VW>
 __global__ __launch_bounds__(kCT) void conv1d_fwd_kernel(const ConvParams p) {
+    constexpr int V = VW ? VW : 4;                      // steps per thread
     const int64_t row_id = blockIdx.x;                  // b * dim + d
     const int64_t b = row_id / p.dim, d = row_id % p.dim;
-    const int64_t t0 = int64_t(blockIdx.y) * kCSeg + threadIdx.x * kCV;
+    const int64_t t0 = int64_t(blockIdx.y) * (kCT * V) + threadIdx.x * V;
     if (t0 >= p.seqlen) return;                         // no barrier in this kernel
     const IT* xr = static_cast<const IT*>(p.x) + b * p.x_bs + d * p.x_ds;
     IT* orow = static_cast<IT*>(p.out) + b * p.o_bs + d * p.o_ds;
@@ -118,31 +139,32 @@ __global__ __launch_bounds__(kCT) void conv1d_fwd_kernel(const ConvParams p) {
     for (int k = 0; k < p.width; ++k) w[4 - p.width + k] = p.w[d * p.w_ds + k * p.w_ks];
     const float bias = p.has_bias ? p.bias[d] : 0.f;
 
-    float xs[8];
-    load_window<IT, kVec, 0>(xr, t0, p.seqlen, xs);
-    float o[4];
+    float xs[2 * V];                                    // x[t0 - V .. t0 + V - 1]
+    load_window<IT, VW, 0>(xr, t0, p.seqlen, xs);
+    float o[V];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < V; ++i) {
         float acc = bias;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc = __builtin_fmaf(w[k], xs[i + 1 + k], acc);
+        for (int k = 0; k < 4; ++k) acc = __builtin_fmaf(w[k], xs[V + i - 3 + k], acc);
         o[i] = p.silu ? acc * sigmoidf_(acc) : acc;
     }
-    if constexpr (kVec) {
-        st4<IT>(orow + t0, o);
+    if constexpr (VW != 0) {
+        stv<IT, VW>(orow + t0, o);
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < V; ++i)
             if (t0 + i < p.seqlen) io<IT>::store(orow + t0 + i, o[i]);
     }
 }
 
-template <typename IT, bool kVec>
+template <typename IT, int VW>
 __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
+    constexpr int V = VW ? VW : 4;                      // steps per thread
     __shared__ float red[kCT / 64][5];
     const int64_t row_id = blockIdx.x;
     const int64_t b = row_id / p.dim, d = row_id % p.dim;
-    const int64_t t0 = int64_t(blockIdx.y) * kCSeg + threadIdx.x * kCV;
+    const int64_t t0 = int64_t(blockIdx.y) * (kCT * V) + threadIdx.x * V;
     const bool live = t0 < p.seqlen;
     const int64_t tl = live ? t0 : 0;                   // dead threads still join the reduction
     const IT* xr = static_cast<const IT*>(p.x) + b * p.x_bs + d * p.x_ds;
@@ -153,29 +175,29 @@ __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
     for (int k = 0; k < p.width; ++k) w[4 - p.width + k] = p.w[d * p.w_ds + k * p.w_ks];
     const float bias = p.has_bias ? p.bias[d] : 0.f;
 
-    // x[t0 - 4 .. t0 + 7], dout[t0 .. t0 + 7]
-    float xs[12];
-    load_window<IT, kVec, 1>(xr, tl, p.seqlen, xs);
-    float gs[8];
-    if constexpr (kVec) {
-        float v[4];
-        ld4<IT>(gr, tl, p.seqlen, v);
+    // x[t0 - V .. t0 + 2 V - 1], dout[t0 .. t0 + 2 V - 1]
+    float xs[3 * V];
+    load_window<IT, VW, 1>(xr, tl, p.seqlen, xs);
+    float gs[2 * V];
+    if constexpr (VW != 0) {
+        float v[VW];
+        ldv<IT, VW>(gr, tl, p.seqlen, v);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) gs[k] = v[k];
-        ld4<IT>(gr, tl + 4, p.seqlen, v);
+        for (int k = 0; k < VW; ++k) gs[k] = v[k];
+        ldv<IT, VW>(gr, tl + VW, p.seqlen, v);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) gs[4 + k] = v[k];
+        for (int k = 0; k < VW; ++k) gs[VW + k] = v[k];
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) gs[i] = ld<IT>(gr, tl + i, p.seqlen);
+        for (int i = 0; i < 2 * V; ++i) gs[i] = ld<IT>(gr, tl + i, p.seqlen);
     }
-    // dpre at t0 .. t0 + 7 (zero beyond seqlen: gs is zero there)
-    float dp[8];
+    // dpre at t0 .. t0 + 2 V - 1 (zero beyond seqlen: gs is zero there)
+    float dp[2 * V];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 2 * V; ++i) {
         float pre = bias;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) pre = __builtin_fmaf(w[k], xs[i + 1 + k], pre);
+        for (int k = 0; k < 4; ++k) pre = __builtin_fmaf(w[k], xs[V + i - 3 + k], pre);
         float g = gs[i];
         if (p.silu) {
             const float s = sigmoidf_(pre);
@@ -184,33 +206,38 @@ __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
         dp[i] = g;
     }
     // dx[t] = sum_k w[k] * dpre[t + 3 - k] (taps right-aligned)
-    float dxo[4];
+    float dxo[V];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < V; ++i) {
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc = __builtin_fmaf(w[k], dp[i + 3 - k], acc);
         dxo[i] = acc;
     }
     if (live) {
-        if constexpr (kVec) {
-            st4<IT>(dxr + t0, dxo);
+        if constexpr (VW != 0) {
+            stv<IT, VW>(dxr + t0, dxo);
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < V; ++i)
                 if (t0 + i < p.seqlen) io<IT>::store(dxr + t0 + i, dxo[i]);
         }
     }
-    // dw[k] += sum_t dpre[t] * x[t - 3 + k], dbias += sum_t dpre[t], over this thread's 4 steps
+    // dw[k] += sum_t dpre[t] * x[t - 3 + k], dbias += sum_t dpre[t], over this thread's V steps
     float part[5];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(dp[i], xs[i + 1 + k], acc);
+        for (int i = 0; i < V; ++i) acc = __builtin_fmaf(dp[i], xs[V + i - 3 + k], acc);
         part[k] = live ? acc : 0.f;
     }
-    part[4] = live ? dp[0] + dp[1] + dp[2] + dp[3] : 0.f;
+    {
+        float sb = 0.f;
+#pragma unroll
+        for (int i = 0; i < V; ++i) sb += dp[i];
+        part[4] = live ? sb : 0.f;
+    }
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
         float v = part[k];
@@ -238,15 +265,23 @@ __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
     }
 }
 
+template <typename IT, int VW>
+void launch_vw(const ConvParams& p, bool bwd, hipStream_t stream) {
+    constexpr int V = VW ? VW : 4;
+    const dim3 grid(unsigned(p.batch * p.dim), unsigned((p.seqlen + kCT * V - 1) / (kCT * V)));
+    if (bwd) hipLaunchKernelGGL((conv1d_bwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
+    else hipLaunchKernelGGL((conv1d_fwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
+}
+
 template <typename IT>
 hipError_t launch_t(const ConvParams& p, bool bwd, hipStream_t stream) {
-    const dim3 grid(unsigned(p.batch * p.dim), unsigned((p.seqlen + kCSeg - 1) / kCSeg));
-    if (bwd) {
-        if (p.vec) hipLaunchKernelGGL((conv1d_bwd_kernel<IT, true>), grid, dim3(kCT), 0, stream, p);
-        else hipLaunchKernelGGL((conv1d_bwd_kernel<IT, false>), grid, dim3(kCT), 0, stream, p);
+    if constexpr (sizeof(IT) == 4) {
+        if (p.vec) launch_vw<IT, 4>(p, bwd, stream);
+        else launch_vw<IT, 0>(p, bwd, stream);
     } else {
-        if (p.vec) hipLaunchKernelGGL((conv1d_fwd_kernel<IT, true>), grid, dim3(kCT), 0, stream, p);
-        else hipLaunchKernelGGL((conv1d_fwd_kernel<IT, false>), grid, dim3(kCT), 0, stream, p);
+        if (p.vec == 8) launch_vw<IT, 8>(p, bwd, stream);
+        else if (p.vec == 4) launch_vw<IT, 4>(p, bwd, stream);
+        else launch_vw<IT, 0>(p, bwd, stream);
     }
     return hipGetLastError();
 }
@@ -271,18 +306,28 @@ hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, h
     p.w_ds = a->w_dim_stride; p.w_ks = a->w_width_stride;
     p.x = a->x; p.w = a->weight; p.bias = a->has_bias ? a->bias : nullptr; p.out = a->out;
     const size_t es = a->itype == SS_F32 ? 4 : 2;
-    auto al = [&](const void* q) { return (reinterpret_cast<uintptr_t>(q) % (4 * es)) == 0; };
-    bool vec = p.seqlen % 4 == 0 && al(a->x) && p.x_bs % 4 == 0 && p.x_ds % 4 == 0;
     if (g) {
         p.do_bs = g->dout_batch_stride; p.do_ds = g->dout_dim_stride;
         p.dx_bs = g->dx_batch_stride; p.dx_ds = g->dx_dim_stride;
         p.dout = g->dout; p.dx = g->dx; p.dw = g->dweight; p.dbias = a->has_bias ? g->dbias : nullptr;
-        vec = vec && al(g->dout) && al(g->dx) && p.do_bs % 4 == 0 && p.do_ds % 4 == 0 &&
-              p.dx_bs % 4 == 0 && p.dx_ds % 4 == 0;
-    } else {
-        vec = vec && al(a->out) && p.o_bs % 4 == 0 && p.o_ds % 4 == 0;
     }
-    p.vec = vec;
+    // every row of every tensor the launch touches starts on an n-element
+    // boundary and seqlen is a multiple of n (so each n-step vector is
+    // wholly inside or wholly outside a row)
+    auto rows_aligned = [&](int64_t n) {
+        auto al = [&](const void* q) { return (reinterpret_cast<uintptr_t>(q) % (n * es)) == 0; };
+        bool ok = p.seqlen % n == 0 && al(a->x) && p.x_bs % n == 0 && p.x_ds % n == 0;
+        if (g) {
+            ok = ok && al(g->dout) && al(g->dx) && p.do_bs % n == 0 && p.do_ds % n == 0 &&
+                 p.dx_bs % n == 0 && p.dx_ds % n == 0;
+        } else {
+            ok = ok && al(a->out) && p.o_bs % n == 0 && p.o_ds % n == 0;
+        }
+        return ok;
+    };
+    // 16-byte vectors: 8 steps of a 16-bit type, 4 of fp32; 8-byte vectors of
+    // a 16-bit type when rows are only 4-element aligned
+    p.vec = (es == 2 && rows_aligned(8)) ? 8 : (rows_aligned(4) ? 4 : 0);
     return launch_conv(p, a->itype, g != nullptr, stream);
 }
 

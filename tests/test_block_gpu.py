@@ -37,8 +37,11 @@ CONV_CASES = [
     (1, 32, 1000, 3, True, None, torch.float32, False),
     (3, 16, 37, 2, True, "silu", torch.float32, False),     # element path (seqlen % 4 != 0)
     (2, 8, 5, 1, False, "silu", torch.float32, False),
-    (2, 64, 2048, 4, True, "silu", torch.bfloat16, True),
-    (1, 48, 130, 4, False, "silu", torch.float16, False),
+    (2, 64, 2048, 4, True, "silu", torch.bfloat16, True),      # 8-element vectors
+    (1, 48, 130, 4, False, "silu", torch.float16, False),      # element path (seqlen % 4 != 0)
+    (2, 32, 1028, 4, True, "silu", torch.bfloat16, False),     # 16-bit 4-element vectors (seqlen % 8 == 4)
+    (1, 16, 4104, 4, True, "silu", torch.bfloat16, True),      # 3 workgroup segments, the last ragged
+    (1, 16, 3000, 3, True, None, torch.float32, False),        # fp32, 3 workgroup segments
 ]
 
 

@@ -40,6 +40,7 @@ CASES = [
     (1, 32, 16, 128, torch.float16, 2, True, True, True, True, True, True),     # fp16, 2 groups
     (2, 48, 16, 192, torch.float32, 1, True, True, False, True, True, True),    # no z, 3 workgroups
     (1, 16, 16, 64, torch.bfloat16, 1, True, True, True, False, False, True),   # one super-tile, no D / bias
+    (1, 16, 16, 320, torch.float32, 1, True, True, True, True, True, True),     # 5 super-tiles (odd count, z)
     # many channel blocks per group: dB / dC summed through workspace slices
     (2, 512, 16, 256, torch.float32, 1, True, True, True, True, True, True),    # 32 blocks: 3 slices
     (1, 768, 16, 128, torch.bfloat16, 2, True, True, True, True, True, True),   # 24 blocks per group: 2 slices

@@ -206,11 +206,12 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
 //  - the B / C tile of the super-chunk is staged through LDS (double
 //    buffered, loaded one super-chunk ahead);
 //  - y_t = sum_n C h is an in-row transposition through LDS: each lane
-//    writes its 16 products C_t h_t, and lane r sums the 16 states of step r
-//    one chunk later (after the next chunk's decay factors, so the LDS round
-//    trip is off the critical path); the 64 sums of a super-chunk are
-//    regrouped through LDS into the owners' float4 for the stores, one
-//    super-chunk late;
+//    writes its 16 states h_t, and lane r forms sum_n C h for step r one
+//    chunk later (after the next chunk's decay factors, so the LDS round
+//    trip is off the critical path), with C from a transposed copy of the
+//    C tile; the lanes of the recurrence never touch C.  The 64 sums of a
+//    super-chunk are regrouped through LDS into the owners' float4 for the
+//    stores, one super-chunk late;
 //  - the checkpoint of the state is one store per lane and chunk (a wave's
 //    4 channels x 16 states are 256 contiguous bytes).
 constexpr int kSC = 64;                      // steps per super-chunk
@@ -224,10 +225,14 @@ constexpr int kYoRow = kSC + 16;             // per-row regroup area, padded lik
 // states 0..15 reading group gi with ds_read_b128 cover all 64 banks once,
 // and a staging row writing its 16 groups does too.
 __device__ __forceinline__ int bc64_slot(int n, int gi) { return n * kSC + 4 * (gi ^ n); }
+// Transposed C tile, [64 steps][16 states]: float4 i of step t (states
+// 4i..4i+3) at t * 16 + 4 * (i ^ ((t >> 2) & 3)), so the 16 lanes of a row
+// reading steps 16q..16q+15 with ds_read_b128 cover all 64 banks once.
+__device__ __forceinline__ int ct_slot4(int t, int i) { return t * 16 + 4 * (i ^ ((t >> 2) & 3)); }
 
 template <typename IT, bool kZ>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
-    __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B, C][n][64 steps]
+    __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B [n][64 steps], C [64 steps][n]]
     __shared__ __attribute__((aligned(16))) float s_yp[kWaves * kRows * kYRow];    // [wave][row][n][16 steps]
     __shared__ __attribute__((aligned(16))) float s_yo[kWaves * kRows * kYoRow];   // [wave][row][64 steps]
 
@@ -292,7 +297,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     };
     auto stage = [&](const Super& S, int buf) {
         *reinterpret_cast<float4*>(s_bc + (buf * 2 + 0) * 16 * kSC + bc64_slot(row, r)) = S.B;
-        *reinterpret_cast<float4*>(s_bc + (buf * 2 + 1) * 16 * kSC + bc64_slot(row, r)) = S.C;
+        // C transposed: step 4r + i, state row
+        float* ct = s_bc + (buf * 2 + 1) * 16 * kSC;
+        const int ci = 4 * ((row >> 2) ^ (r & 3)) + (row & 3);
+        ct[(4 * r + 0) * 16 + ci] = S.C.x;
+        ct[(4 * r + 1) * 16 + ci] = S.C.y;
+        ct[(4 * r + 2) * 16 + ci] = S.C.z;
+        ct[(4 * r + 3) * 16 + ci] = S.C.w;
     };
     // this row's product tile: lane n writes its steps 4m..4m+3 as a float4
     // at n * 16 + 4 * (m ^ ((n >> 1) & 3)); lane r reads step r of state n at
@@ -328,18 +339,25 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         }
         bstore4<IT>(make_rsrc(go + int64_t(sc) * kSC), oo, y);
     };
-    // sum over states of the chunk whose products are in the tile: step r
+    // y_t = sum over states of C h for the chunk whose states are in the
+    // tile: lane r reads step r's 16 states, and multiplies them by that
+    // step's C row (read from the transposed tile while the chunk ran)
     auto read_tile = [&](float (&ys)[kT]) {
 #pragma unroll
         for (int n = 0; n < kT; ++n) ys[n] = yrow[n * 16 + yoff[(n >> 1) & 3]];
     };
-    auto sum16 = [&](const float (&ys)[kT]) {
-        const float s0 = (ys[0] + ys[1]) + (ys[2] + ys[3]);
-        const float s1 = (ys[4] + ys[5]) + (ys[6] + ys[7]);
-        const float s2 = (ys[8] + ys[9]) + (ys[10] + ys[11]);
-        const float s3 = (ys[12] + ys[13]) + (ys[14] + ys[15]);
-        return (s0 + s1) + (s2 + s3);
+    auto dot16 = [&](const float (&ys)[kT], const float (&cv)[kT]) {
+        float s0 = ys[0] * cv[0], s1 = ys[1] * cv[1];
+#pragma unroll
+        for (int n = 2; n < kT; n += 2) {
+            s0 = __builtin_fmaf(ys[n], cv[n], s0);
+            s1 = __builtin_fmaf(ys[n + 1], cv[n + 1], s1);
+        }
+        return s0 + s1;
     };
+    float cT[kT];     // C of step r of the chunk last run, states 0..15
+#pragma unroll
+    for (int n = 0; n < kT; ++n) cT[n] = 0.f;
 
     Super S;
     fetch(sc0, S);
@@ -363,15 +381,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 
         static_for<kQ>([&](auto Q) {
             constexpr int q = decltype(Q)::value;
-            float Bq[kT], Cq[kT];
+            float Bq[kT];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
-                const float4 vc = *reinterpret_cast<const float4*>(sC + bc64_slot(r, 4 * q + i));
                 Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
-                Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
             }
-            // products of the previous chunk, written by this row last chunk
+            // states of the previous chunk, written by this row last chunk
             float ys[kT];
             read_tile(ys);
             // decay factors of all 16 steps first: they do not depend on h, so
@@ -384,7 +400,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             // the LDS reads issued above have had the decay factors to land
             __builtin_amdgcn_sched_barrier(0);
             // the previous chunk's sums (chunk 4 sc + q - 1) into the regroup area
-            yo[((q + kQ - 1) % kQ) * kT + r] = sum16(ys);
+            yo[((q + kQ - 1) % kQ) * kT + r] = dot16(ys, cT);
             if constexpr (q == 0) {
                 finish_super(sc > sc0 ? sc - 1 : sc0);   // (at sc0 a placeholder, rewritten later)
                 pu = cu;     // this super-chunk's u, z wait for its outputs
@@ -394,13 +410,20 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             static_for<kT>([&](auto K) {
                 constexpr int k = decltype(K)::value;
                 h = __builtin_fmaf(a[k], h, bmul<4 * q + k / 4>(f4get(dtu, k % 4), Bq[k]));
-                yp[k] = Cq[k] * h;
+                yp[k] = h;
             });
             bstore<float>(Rx, ox, uint32_t(kQ * sc + q) * x_chunk_bytes, h);
 #pragma unroll
             for (int m = 0; m < 4; ++m)
                 *reinterpret_cast<float4*>(yrow + r * 16 + 4 * (m ^ ((r >> 1) & 3))) =
                     make_float4(yp[4 * m], yp[4 * m + 1], yp[4 * m + 2], yp[4 * m + 3]);
+            // C of step r of this chunk, for its sum one chunk later (read
+            // now: this buffer is not restaged before the next barrier)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 vc = *reinterpret_cast<const float4*>(sC + ct_slot4(16 * q + r, i));
+                cT[4 * i] = vc.x; cT[4 * i + 1] = vc.y; cT[4 * i + 2] = vc.z; cT[4 * i + 3] = vc.w;
+            }
         });
         // B / C tile of the next super-chunk into the other buffer
         stage(S, buf ^ 1);
@@ -409,7 +432,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     {
         float ys[kT];
         read_tile(ys);
-        yo[(kQ - 1) * kT + r] = sum16(ys);
+        yo[(kQ - 1) * kT + r] = dot16(ys, cT);
         finish_super(sc1 - 1);
     }
     if (p.last_state && seg == nseg - 1) p.last_state[(b * p.dim + c) * kT + r] = h;

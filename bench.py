@@ -537,8 +537,9 @@ def main():
         ws = ss.workspace_bytes(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
                                 z=z, y=y, dz=dz)
         fname, bname = f"{fname}<{tname}, z>", f"{bname}<{tname}, z>"
-        if ws > 0:   # the backward is three launches: clear slices and accumulators, scan, sum slices
-            bname = f"ss_zero_segs + {bname} + ss_ws_reduce"
+        # zero_grads: a fill launch clears the accumulators (and any dB / dC
+        # slices) before the scan; with slices, a last launch sums them
+        bname = f"ss_zero_segs + {bname}" + (" + ss_ws_reduce" if ws > 0 else "")
         kernel_ms = {}
         for name, fn in ((fname, fwd), (bname, bwd)):
             fn()

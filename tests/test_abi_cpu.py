@@ -347,21 +347,29 @@ def test_kernel_name_query(nat, lib):
 def test_workspace_query(nat, lib):
     # 2 channel blocks per group: one slice, no workspace
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, seqlen=128))) == 0
-    # 1536 channels in one group = 96 blocks: 8 slices of dB and dC (batch * dstate * seqlen floats each)
-    b = valid_bwd(nat, batch=2, dim=1536, seqlen=128)
-    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 8 * (2 * 16 * 128) * 4
+    # at most 96 channel blocks per slice: 1536 channels in one group (96
+    # blocks) accumulate directly; 3072 (192 blocks) use 2 slices of dB and dC
+    # (batch * dstate * seqlen floats each)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, batch=2, dim=1536, seqlen=128))) == 0
+    b = valid_bwd(nat, batch=2, dim=3072, seqlen=128)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 2 * (2 * 16 * 128) * 4
     # the general kernel (ragged length) uses none; invalid arguments give -1
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, dim=1536, seqlen=100))) == 0
     bad = valid_bwd(nat)
     bad.dout = None
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(bad)) == -1
     assert "dout is NULL" in lib.ss_last_error().decode()
-    # 5120 channels: 320 blocks, capped at 16 slices
+    # 5120 channels: 320 blocks, 4 slices; 26112 channels: 1632 blocks, capped at 16 slices
     b = valid_bwd(nat, batch=1, dim=5120, seqlen=64)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 4 * (16 * 64) * 4
+    b = valid_bwd(nat, batch=1, dim=26112, seqlen=64)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 16 * (16 * 64) * 4
-    # one long sequence: 8 dB / dC slices, then 8 sequence segments (96 blocks -> 768 workgroups)
+    # one long sequence: no dB / dC slices (96 blocks), 8 sequence segments (-> 768 workgroups)
     b = valid_bwd(nat, batch=1, dim=1536, seqlen=32768)
-    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 8 * (16 * 32768) * 4 + 1 * 8 * 1536 * 17 * 4
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 1 * 8 * 1536 * 17 * 4
+    # 3072 channels: 2 slices, then 4 segments (192 blocks -> 768 workgroups)
+    b = valid_bwd(nat, batch=1, dim=3072, seqlen=32768)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 2 * (16 * 32768) * 4 + 1 * 4 * 3072 * 17 * 4
 
 
 # --------------------------------------------------------------------- RMSNorm --

@@ -23,7 +23,7 @@ from tests._util import assert_close
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
-CASES = [(2, 1536, 16, 256, torch.float32), (2, 64, 4, 100, torch.float32), (1, 64, 16, 4096, torch.bfloat16)]
+CASES = [(1, 3072, 16, 256, torch.float32), (2, 64, 4, 100, torch.float32), (1, 64, 16, 4096, torch.bfloat16)]
 
 
 @pytest.mark.parametrize("case", CASES, ids=["fast-slices", "general", "segments"])
@@ -46,8 +46,10 @@ def test_scan_step_graph_replays(case):
     fwork = torch.empty(max(fws, 16), dtype=torch.uint8, device=DEV) if fws else None
     bws = ss.workspace_bytes(*bargs, z=t["z"], y=y, dz=dz)
     bwork = torch.empty(max(bws, 16), dtype=torch.uint8, device=DEV) if bws else None
-    if case[0] == 1:
+    if L == 4096:
         assert fws > 0 and bws > 0, "the long single sequence should use sequence segments"
+    if dim == 3072:
+        assert fws == 0 and bws == 2 * 2 * 16 * L * 4, "192 channel blocks should use 2 dB / dC slices"
 
     def step():
         ss.forward_into(*fargs, out, xck, z=t["z"], y=y, workspace=fwork)

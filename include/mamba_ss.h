@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 9
+#define SS_ABI_VERSION 10
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -308,6 +308,16 @@ typedef struct ss_state_update_args {
     const void* z;                       /* may be NULL iff !has_z */
     const float* delta_bias;             /* may be NULL iff !has_delta_bias */
     void* out;
+    /* ABI v10: when delta_low is not NULL, delta is the low-rank product
+     *   delta[b, d] = sum_r delta_low[b, r] * delta_weight[d, r]
+     * (the block's delta projection, summed in fp32 inside the kernel) and
+     * the delta pointer and strides are ignored; delta_low (batch,
+     * delta_rank) and delta_weight (dim, delta_rank) in itype. */
+    int64_t delta_rank;
+    int64_t delta_low_batch_stride, delta_low_rank_stride;
+    int64_t delta_weight_dim_stride, delta_weight_rank_stride;
+    const void* delta_low;
+    const void* delta_weight;
 } ss_state_update_args;
 
 /* ss_conv1d_update, per (batch b, channel d), state = the last width inputs:

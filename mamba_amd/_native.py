@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
@@ -117,6 +117,9 @@ class StateUpdateArgs(ctypes.Structure):
         ("C_batch_stride", _i64), ("C_group_stride", _i64), ("C_dstate_stride", _i64),
         ("state", _p), ("x", _p), ("delta", _p), ("A", _p), ("B", _p), ("C", _p),
         ("D", _p), ("z", _p), ("delta_bias", _p), ("out", _p),
+        ("delta_rank", _i64), ("delta_low_batch_stride", _i64), ("delta_low_rank_stride", _i64),
+        ("delta_weight_dim_stride", _i64), ("delta_weight_rank_stride", _i64),
+        ("delta_low", _p), ("delta_weight", _p),
     ]
 
 

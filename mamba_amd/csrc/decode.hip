@@ -30,8 +30,26 @@ namespace {
 
 constexpr int kDT = 256;              // threads per workgroup
 
+// The 16 bytes of v as 16 / sizeof(IT) floats.
 template <typename IT>
-__global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update_args a, bool vec) {
+__device__ __forceinline__ void unpack16(const uint4 v, float (&o)[16 / sizeof(IT)]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(IT) == 4) {
+            o[i] = __uint_as_float(w[i]);
+        } else if constexpr (__is_same(IT, bf16_t)) {
+            o[2 * i] = __uint_as_float(w[i] << 16);
+            o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        } else {
+            o[2 * i] = float(__builtin_bit_cast(_Float16, uint16_t(w[i] & 0xffffu)));
+            o[2 * i + 1] = float(__builtin_bit_cast(_Float16, uint16_t(w[i] >> 16)));
+        }
+    }
+}
+
+template <typename IT>
+__global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update_args a, bool vec, bool lowvec) {
     const int64_t i = int64_t(blockIdx.x) * kDT + threadIdx.x;
     if (i >= a.batch * a.dim) return;                   // no barrier in this kernel
     const int64_t b = i / a.dim, d = i % a.dim;
@@ -39,7 +57,41 @@ __global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update
     const IT* xs = static_cast<const IT*>(a.x);
     const IT* dts = static_cast<const IT*>(a.delta);
     const float x = io<IT>::load(xs + b * a.x_batch_stride + d * a.x_dim_stride);
-    float dt = io<IT>::load(dts + b * a.delta_batch_stride + d * a.delta_dim_stride);
+    float dt;
+    if (a.delta_low) {                                  // delta = delta_low[b, :] . delta_weight[d, :]
+        const IT* lo = static_cast<const IT*>(a.delta_low) + b * a.delta_low_batch_stride;
+        const IT* wr = static_cast<const IT*>(a.delta_weight) + d * a.delta_weight_dim_stride;
+        float s0 = 0.f, s1 = 0.f;
+        int64_t r = 0;
+        if (lowvec) {                                   // both rows contiguous, 16-byte aligned, whole vectors
+            constexpr int E = 16 / int(sizeof(IT));
+            const uint4* lo4 = reinterpret_cast<const uint4*>(lo);
+            const uint4* wr4 = reinterpret_cast<const uint4*>(wr);
+            for (int64_t q = 0; q < a.delta_rank / E; ++q) {
+                float lv[E], wv[E];
+                unpack16<IT>(lo4[q], lv);
+                unpack16<IT>(wr4[q], wv);
+#pragma unroll
+                for (int e = 0; e < E; e += 2) {
+                    s0 = __builtin_fmaf(lv[e], wv[e], s0);
+                    s1 = __builtin_fmaf(lv[e + 1], wv[e + 1], s1);
+                }
+            }
+            r = a.delta_rank;
+        }
+        for (; r + 1 < a.delta_rank; r += 2) {
+            s0 = __builtin_fmaf(io<IT>::load(lo + r * a.delta_low_rank_stride),
+                                io<IT>::load(wr + r * a.delta_weight_rank_stride), s0);
+            s1 = __builtin_fmaf(io<IT>::load(lo + (r + 1) * a.delta_low_rank_stride),
+                                io<IT>::load(wr + (r + 1) * a.delta_weight_rank_stride), s1);
+        }
+        if (r < a.delta_rank)
+            s0 = __builtin_fmaf(io<IT>::load(lo + r * a.delta_low_rank_stride),
+                                io<IT>::load(wr + r * a.delta_weight_rank_stride), s0);
+        dt = s0 + s1;
+    } else {
+        dt = io<IT>::load(dts + b * a.delta_batch_stride + d * a.delta_dim_stride);
+    }
     if (a.has_delta_bias) dt += a.delta_bias[d];
     if (a.delta_softplus) dt = softplus20(dt);
     const float dtx = dt * x;
@@ -108,11 +160,15 @@ hipError_t state_update_launch(const ss_state_update_args* a, hipStream_t stream
     const bool vec = a->dstate % 4 == 0 && a->state_dstate_stride == 1 && a->A_dstate_stride == 1 &&
                      al16(a->state) && al16(a->A) && a->state_batch_stride % 4 == 0 &&
                      a->state_dim_stride % 4 == 0 && a->A_dim_stride % 4 == 0;
+    const int64_t es = a->itype == SS_F32 ? 4 : 2;
+    const bool lowvec = a->delta_low && a->delta_low_rank_stride == 1 && a->delta_weight_rank_stride == 1 &&
+                        al16(a->delta_low) && al16(a->delta_weight) && (a->delta_low_batch_stride * es) % 16 == 0 &&
+                        (a->delta_weight_dim_stride * es) % 16 == 0 && (a->delta_rank * es) % 16 == 0;
     const dim3 grid{unsigned((a->batch * a->dim + kDT - 1) / kDT)};
     switch (a->itype) {
-        case SS_F32: hipLaunchKernelGGL((state_update_kernel<float>), grid, dim3(kDT), 0, stream, *a, vec); break;
-        case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t>), grid, dim3(kDT), 0, stream, *a, vec); break;
-        case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16>), grid, dim3(kDT), 0, stream, *a, vec); break;
+        case SS_F32: hipLaunchKernelGGL((state_update_kernel<float>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+        case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+        case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -444,11 +444,20 @@ int ss_state_update(const ss_state_update_args* a, void* stream) {
     if (a->batch > int64_t(UINT32_MAX) / 2 / (a->dim > 0 ? a->dim : 1))
         return fail(SS_ERR_UNSUPPORTED, "batch * dim is too large");
     const size_t es = elem_size(a->itype);
-    if (!a->state || !a->x || !a->delta || !a->out || (a->dstate > 0 && (!a->A || !a->B || !a->C)))
+    const bool low = a->delta_low != nullptr;
+    if (!a->state || !a->x || (!low && !a->delta) || !a->out || (a->dstate > 0 && (!a->A || !a->B || !a->C)))
         return fail(SS_ERR_INVALID, "state / x / delta / A / B / C / out is NULL");
+    if (low && (!a->delta_weight || a->delta_rank < 1))
+        return fail(SS_ERR_INVALID, "delta_low given without delta_weight or with delta_rank=%lld",
+                    (long long)a->delta_rank);
+    if (low && (!aligned(a->delta_low, elem_size(a->itype)) || !aligned(a->delta_weight, elem_size(a->itype))))
+        return fail(SS_ERR_INVALID, "delta_low / delta_weight is misaligned");
+    if (low && (a->delta_low_batch_stride < 0 || a->delta_low_rank_stride < 0 || a->delta_weight_dim_stride < 0 ||
+                a->delta_weight_rank_stride < 0))
+        return fail(SS_ERR_INVALID, "negative stride");
     if ((a->has_D && !a->D) || (a->has_z && !a->z) || (a->has_delta_bias && !a->delta_bias))
         return fail(SS_ERR_INVALID, "D / z / delta_bias is NULL but flagged present");
-    const void* p2[] = {a->x, a->delta, a->B, a->C, a->has_z ? a->z : nullptr, a->out};
+    const void* p2[] = {a->x, low ? nullptr : a->delta, a->B, a->C, a->has_z ? a->z : nullptr, a->out};
     for (const void* q : p2)
         if (q && !aligned(q, es)) return fail(SS_ERR_INVALID, "x / delta / B / C / z / out is misaligned");
     const void* p4[] = {a->state, a->A, a->has_D ? a->D : nullptr, a->has_delta_bias ? a->delta_bias : nullptr};

@@ -136,9 +136,10 @@ class MambaSimple(nn.Module):
         x = causal_conv1d_update(x, conv_state, conv_w, conv_b, "silu")
         x_db = decode_linear(x, self.ssm_param_proj.weight)                          # (batch, R + 2N)
         R, N = self.delta_rank, self.state_dim
-        dt = decode_linear(x_db[:, :R], self.delta_proj.weight)                     # bias goes in the update
-        y = selective_state_update(ssm_state, x, dt, A, x_db[:, R:R + N], x_db[:, R + N:], D, z=z,
-                                   dt_bias=dt_bias, dt_softplus=True)
+        # the delta projection (x_db[:, :R] @ W.T) is summed inside the state
+        # update; its bias goes in there too
+        y = selective_state_update(ssm_state, x, (x_db[:, :R], self.delta_proj.weight), A, x_db[:, R:R + N],
+                                   x_db[:, R + N:], D, z=z, dt_bias=dt_bias, dt_softplus=True)
         out = decode_linear(y, self.output_proj.weight, self.output_proj.bias)
         return out.unsqueeze(1) if squeeze else out
 

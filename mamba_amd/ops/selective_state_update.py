@@ -12,6 +12,11 @@ CausalLM.generate is a stub, models/causal_lm.py:61-62):
 state: fp32 (batch, dim, dstate); x, dt, z: (batch, dim); A: (dim, dstate);
 B, C: (batch, dstate) or (batch, n_groups, dstate), in x's dtype (any
 strides); D, dt_bias: (dim,).  Returns out (batch, dim) in x's dtype.
+
+dt may also be a pair (dt_low, dt_weight): the block's delta projection
+dt = dt_low @ dt_weight.T (modules/mamba_simple.py:118-119), with dt_low
+(batch, rank) and dt_weight (dim, rank) in x's dtype, summed in fp32 inside
+the kernel, so a decode step needs no launch for that product.
 """
 import ctypes
 
@@ -35,7 +40,15 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, 
     _require(state.dim() == 3 and state.shape[:2] == (batch, dim) and state.dtype == torch.float32
              and state.device == dev, f"state must be fp32 ({batch}, {dim}, dstate)")
     dstate = state.shape[2]
-    _require(dt.shape == x.shape and dt.dtype == x.dtype, "dt must match x in shape and dtype")
+    low = isinstance(dt, (tuple, list))
+    if low:
+        dt_low, dt_w = dt
+        _require(dt_low.dim() == 2 and dt_low.shape[0] == batch and dt_low.dtype == x.dtype
+                 and dt_low.device == dev, "dt_low must be (batch, rank) in x's dtype")
+        _require(dt_w.shape == (dim, dt_low.shape[1]) and dt_w.dtype == x.dtype and dt_w.device == dev,
+                 "dt_weight must be (dim, rank) in x's dtype")
+    else:
+        _require(dt.shape == x.shape and dt.dtype == x.dtype, "dt must match x in shape and dtype")
     _require(A.shape == (dim, dstate), f"A must be ({dim}, {dstate})")
     A32 = A.to(device=dev, dtype=torch.float32)
     if B.dim() == 2:
@@ -61,14 +74,21 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None, 
                                                             int(db32 is not None), int(bool(dt_softplus)))
     a.state_batch_stride, a.state_dim_stride, a.state_dstate_stride = state.stride()
     a.x_batch_stride, a.x_dim_stride = x.stride()
-    a.delta_batch_stride, a.delta_dim_stride = dt.stride()
+    if low:
+        a.delta_rank = dt_low.shape[1]
+        a.delta_low_batch_stride, a.delta_low_rank_stride = dt_low.stride()
+        a.delta_weight_dim_stride, a.delta_weight_rank_stride = dt_w.stride()
+        a.delta_low, a.delta_weight = _ptr(dt_low), _ptr(dt_w)
+    else:
+        a.delta_batch_stride, a.delta_dim_stride = dt.stride()
     if z is not None:
         a.z_batch_stride, a.z_dim_stride = z.stride()
     a.out_batch_stride, a.out_dim_stride = out.stride()
     a.A_dim_stride, a.A_dstate_stride = A32.stride()
     a.B_batch_stride, a.B_group_stride, a.B_dstate_stride = B.stride()
     a.C_batch_stride, a.C_group_stride, a.C_dstate_stride = C.stride()
-    a.state, a.x, a.delta, a.A, a.B, a.C = _ptr(state), _ptr(x), _ptr(dt), _ptr(A32), _ptr(B), _ptr(C)
+    a.state, a.x, a.A, a.B, a.C = _ptr(state), _ptr(x), _ptr(A32), _ptr(B), _ptr(C)
+    a.delta = None if low else _ptr(dt)
     a.D, a.z, a.delta_bias, a.out = _ptr(D32), _ptr(z), _ptr(db32), _ptr(out)
     with torch.cuda.device(dev):
         nat.check(lib.ss_state_update(ctypes.byref(a), _stream(dev)), "selective_state_update")

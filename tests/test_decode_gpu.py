@@ -79,6 +79,37 @@ def test_state_update_matches_oracle(case):
     assert_close(out.cpu(), want_out.double(), tol, tol, "out")
 
 
+@pytest.mark.parametrize("dt_,rank", [(torch.float32, 48), (torch.bfloat16, 48), (torch.float16, 7)])
+def test_state_update_low_rank_delta(dt_, rank):
+    """dt given as (dt_low, dt_weight): the delta projection summed inside the
+    kernel equals the oracle fed dt = dt_low @ dt_weight.T in float64; dt_low
+    is a column slice of a wider row.  Rank 48 takes the 16-byte vector loads,
+    rank 7 the element loads with an unpaired last term."""
+    from mamba_amd.ops.selective_state_update import selective_state_update
+    _say(f"state update, low-rank delta, rank {rank} {dt_}")
+    gen = torch.Generator().manual_seed(500 + rank)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    batch, dim, N = 5, 96, 16
+    x, z = r(batch, dim).to(dt_), r(batch, dim).to(dt_)
+    xdb = (0.3 * r(batch, rank + 2 * N)).to(dt_)          # x_proj output: [dt_low | B | C]
+    w = (r(dim, rank) / rank ** 0.5).to(dt_)
+    A = -torch.rand(dim, N, generator=gen) * 3
+    B, C = r(batch, 1, N).to(dt_), r(batch, 1, N).to(dt_)
+    D, bias = r(dim), r(dim) * 0.5
+    state0 = r(batch, dim, N)
+    st = state0.to(DEV).clone()
+    xdb_d = xdb.to(DEV)
+    out = selective_state_update(st, x.to(DEV), (xdb_d[:, :rank], w.to(DEV)), A.to(DEV), B.to(DEV), C.to(DEV),
+                                 D.to(DEV), z=z.to(DEV), dt_bias=bias.to(DEV), dt_softplus=True)
+    dt64 = xdb[:, :rank].double() @ w.double().t()
+    want_out, want_st = selective_state_update_ref(state0.double(), x.double(), dt64, A.double(), B.double(),
+                                                   C.double(), D.double(), z=z.double(), dt_bias=bias.double(),
+                                                   dt_softplus=True)
+    tol = TOL[dt_]
+    assert_close(st.cpu().double(), want_st, 1e-4, 1e-4, "state")
+    assert_close(out.cpu().double(), want_out.double(), tol, tol, "out")
+
+
 @pytest.mark.parametrize("width,bias,act,dt_", [(4, True, "silu", torch.float32), (3, False, None, torch.float32),
                                                 (1, True, "silu", torch.bfloat16), (2, True, "silu", torch.float16),
                                                 (4, False, "silu", torch.bfloat16)])

@@ -2,7 +2,8 @@
 
 * ss_state_update against the float64 step oracle: dstate 16 (16-byte state
   path) and 5 (element path), a strided state, 1 and 2 groups, with and
-  without D / z / bias, fp32 / bf16 / fp16 I/O;
+  without D / z / bias, fp32 / bf16 / fp16 I/O; delta as the low-rank pair
+  (dt_low, dt_weight) summed in the kernel (vector and element loads);
 * ss_conv1d_update against the step oracle: widths 1-4, with and without
   bias and SiLU; the shifted state is bit-exact;
 * token-by-token state updates from a zero state reproduce

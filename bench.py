@@ -444,18 +444,27 @@ def calibrate_copy(mib, reps=5):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # scan workloads: 100 + 100 steps by default.  The GPU's clocks ramp under
+    # sustained load: after idle the first ~60 steps of the fp32 workload run
+    # up to 20 % slower than the settled rate, so a short warm-up would time
+    # the ramp rather than the kernels (about 50 ms for each phase here).
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (scan 100, other workloads 20)")
+    ap.add_argument("--warmup", type=int, default=None, help="warm-up steps (scan 100, other workloads 5)")
     ap.add_argument("--workload", default=DEFAULT,
                     choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS) + sorted(NORM_WORKLOADS)
                     + sorted(DECODE_WORKLOADS))
-    ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-ref-order", action="store_true",
                     help="block / LM workloads: skip timing the reference's op order")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only time a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
+    scan = args.workload in WORKLOADS
+    if args.steps is None:
+        args.steps = 100 if scan else 20
+    if args.warmup is None:
+        args.warmup = 100 if scan else 5
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
@@ -541,6 +550,11 @@ def main():
         # slices) before the scan; with slices, a last launch sums them
         bname = f"ss_zero_segs + {bname}" + (" + ss_ws_reduce" if ws > 0 else "")
         kernel_ms = {}
+        # the set-up above leaves the GPU idle and its clocks drop: warm the
+        # prepared launches up as long as the steps, then time each kernel
+        for _ in range(args.warmup):
+            fwd()
+            bwd()
         for name, fn in ((fname, fwd), (bname, bwd)):
             fn()
             torch.cuda.synchronize()

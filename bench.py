@@ -125,11 +125,12 @@ def bench_norm(args):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / n
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_up(step, args.warmup)
     ms_per_step = timed(step, args.steps)
-    kernel_ms = {fname: timed(fwd, args.kernel_reps), bname: timed(bwd, args.kernel_reps)}
+    warm_up(fwd, args.warmup)
+    f_ms = timed(fwd, args.kernel_reps)
+    warm_up(bwd, args.warmup)
+    kernel_ms = {fname: f_ms, bname: timed(bwd, args.kernel_reps)}
     print(f"[bench] kernels: " + ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in kernel_ms.items()),
           file=sys.stderr, flush=True)
     fwd_bytes, bwd_bytes = norm_bytes(rows, dim, s)
@@ -168,7 +169,7 @@ def norm_cpu_baseline(rows, dim, dtype_name, sample_rows=None, reps=3):
 
     sample_rows = rows if sample_rows is None else sample_rows
 
-    threads = len(os.sched_getaffinity(0))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     dtype = getattr(torch, dtype_name)
     gen = torch.Generator().manual_seed(1005)
@@ -190,6 +191,7 @@ def norm_cpu_baseline(rows, dim, dtype_name, sample_rows=None, reps=3):
     s = 2 if dtype != torch.float32 else 4
     fb, bb = norm_bytes(sample_rows, dim, s)
     return {"value": round((fb + bb) / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{sample_rows} of {rows} rows, dim {dim}, {dtype_name}; median of {reps}",
             "seconds_per_sample": round(t, 4)}
 
@@ -219,9 +221,7 @@ def bench_decode(args):
     tok = ids[:, -1].clone()
 
     def timed(fn, n):
-        for _ in range(args.warmup):
-            fn()
-        torch.cuda.synchronize()
+        warm_up(fn, args.warmup)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(n):
@@ -258,9 +258,7 @@ def bench_model(args):
     torch.manual_seed(1003)
 
     def timed(fn):
-        for _ in range(args.warmup):
-            fn()
-        torch.cuda.synchronize()
+        warm_up(fn, args.warmup)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(args.steps):
@@ -343,6 +341,96 @@ def bench_model(args):
     print(json.dumps(line), flush=True)
 
 
+def synthetic_inputs(batch, dim, dstate, seqlen, *, seed, dtype):
+    """Seeded synthetic scan inputs of the benchmark distributions.
+
+    A CPU generator seeded with ``seed`` draws, in this order, u, delta, z,
+    B, C (variable, one group), dt and dout, each N(0, 1) fp32 (dt uniform
+    on [1e-3, 1e-1]); delta_bias = dt + log(-expm1(-dt)) is the inverse
+    softplus of dt (the form of modules/mamba_simple.py:76); A = -(1..N) per
+    channel (modules/mamba_simple.py:80-82,128); D = ones.  The sequence
+    tensors are cast to ``dtype``; A, D and delta_bias stay fp32."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(batch, dim, seqlen, generator=g)
+    delta = torch.randn(batch, dim, seqlen, generator=g)
+    z = torch.randn(batch, dim, seqlen, generator=g)
+    B = torch.randn(batch, 1, dstate, seqlen, generator=g)
+    C = torch.randn(batch, 1, dstate, seqlen, generator=g)
+    dt = torch.rand(dim, generator=g) * (1e-1 - 1e-3) + 1e-3
+    dout = torch.randn(batch, dim, seqlen, generator=g)
+    return dict(u=u.to(dtype), delta=delta.to(dtype), z=z.to(dtype), B=B.to(dtype), C=C.to(dtype),
+                dout=dout.to(dtype), delta_bias=dt + torch.log(-torch.expm1(-dt)),
+                A=-torch.arange(1, dstate + 1, dtype=torch.float32).repeat(dim, 1), D=torch.ones(dim))
+
+
+def kernel_sources_digest():
+    """sha256 of the sources the scan kernels are built from: a stored
+    traffic figure is only reported while it matches."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in ("ss_fwd.hip", "ss_bwd.hip", "ss_device.hpp", "ss_kernels.hpp", "ss_api.hip"):
+        with open(os.path.join(_HERE, "mamba_amd", "csrc", name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
+def stored_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from profiles/traffic_<workload>.json
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by a copy calibration), with
+    where it came from; (None, reason) when there is none or it was taken
+    with other kernel sources than the ones built now."""
+    path = os.path.join("profiles", f"traffic_{workload}.json")
+    full = os.path.join(_HERE, path)
+    if not os.path.exists(full):
+        return None, f"no {path}"
+    with open(full) as f:
+        rec = json.load(f)
+    if rec.get("sources_sha256") != kernel_sources_digest():
+        return None, f"{path} was measured with other kernel sources (stale)"
+    if kernel not in rec:
+        return None, f"{path} has no entry for {kernel}"
+    return rec[kernel], (f"{path}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel build "
+                         f"(sources sha256 {rec['sources_sha256'][:12]}), scaled by a 1 GiB copy calibration")
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
+def cpu_threads():
+    """Host threads for the CPU baselines: every core this process may run
+    on, capped by OMP_NUM_THREADS when that is set (a GPU box allots each GPU
+    a share of its cores and sets it to that share)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return n
+
+
+def warm_up(fn, steps, min_ms=100.0):
+    """Runs fn at least `steps` times and for at least `min_ms` of GPU time:
+    the clocks ramp up under sustained load (about 50 ms from idle)."""
+    import torch
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < min_ms:
+        fn()
+        torch.cuda.synchronize()
+
+
 def algorithmic_bytes(batch, dim, dstate, seqlen, s, groups=1):
     """HBM bytes that one forward / backward must move at minimum.
 
@@ -363,19 +451,18 @@ def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
     """Times the C restatement of the reference's algorithm (oracle/ss_oracle.c:
     the reference kernels' arithmetic in float64, plain loops) forward +
     backward on this host's cores: one task per (batch row, 96-channel slice),
-    run by a pool of up to 16 threads (the C calls release the GIL).  A
+    run by a pool of cpu_threads() threads (the C calls release the GIL).  A
     one-slice calibration run estimates the time; the sample is the whole
     workload when that takes at most `max_seconds`, else its first batch
     rows.  GB/s uses the same byte formula (and I/O dtype) as ``value``."""
     import torch
     from concurrent.futures import ThreadPoolExecutor
     from oracle import c_oracle
-    from oracle.selective_scan_ref import make_inputs
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads = cpu_threads()
     slice_ch = 96 if dim % 96 == 0 else dim
     x = {k: (v.double() if v is not None else None)
-         for k, v in make_inputs(batch, dim, dstate, seqlen, seed=1001, dtype=torch.float32).items()}
+         for k, v in synthetic_inputs(batch, dim, dstate, seqlen, seed=1001, dtype=torch.float32).items()}
 
     def task(bi, lo):
         hi = lo + slice_ch
@@ -406,6 +493,7 @@ def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
         "value": round((fwd_b + bwd_b) / dt / 1e9, 4),
         "unit": "GB/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"oracle/ss_oracle.c (float64 C restatement of the reference kernels) fwd+bwd on batch {rows} "
                   f"x dim {dim} x seqlen {seqlen} x dstate {dstate}, {len(tasks)} tasks of {slice_ch} channels "
@@ -488,13 +576,12 @@ def main():
     import torch
     from mamba_amd import selective_scan as ss
     from mamba_amd.ops.selective_scan_interface import selective_scan_fn
-    from oracle.selective_scan_ref import make_inputs  # seeded synthetic inputs only
 
     batch, dim, dstate, seqlen, dtype_name, seed = WORKLOADS[args.workload]
     dtype = getattr(torch, dtype_name)
     s = 2 if dtype != torch.float32 else 4
     dev = torch.device("cuda:0")
-    x = make_inputs(batch, dim, dstate, seqlen, seed=seed, dtype=dtype)
+    x = synthetic_inputs(batch, dim, dstate, seqlen, seed=seed, dtype=dtype)
     names = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
     g = {k: x[k].to(dev).requires_grad_(True) for k in names}
     dout = x["dout"].to(dev)
@@ -505,9 +592,7 @@ def main():
                                 delta_bias=g["delta_bias"], delta_softplus=True)
         return torch.autograd.grad(out, params, dout)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_up(step, args.warmup)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
@@ -552,9 +637,7 @@ def main():
         kernel_ms = {}
         # the set-up above leaves the GPU idle and its clocks drop: warm the
         # prepared launches up as long as the steps, then time each kernel
-        for _ in range(args.warmup):
-            fwd()
-            bwd()
+        warm_up(lambda: (fwd(), bwd()), args.warmup)
         for name, fn in ((fname, fwd), (bname, bwd)):
             fn()
             torch.cuda.synchronize()
@@ -575,14 +658,10 @@ def main():
     dom_bytes = fwd_bytes if dom == fname else bwd_bytes
     achieved = dom_bytes / (kernel_ms[dom] * 1e-3) / 1e9
 
-    traffic = None
-    tpath = os.path.join(_HERE, "profiles", f"traffic_{args.workload}.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get(dom)
+    traffic, traffic_source = stored_traffic(args.workload, dom)
 
     line = {
-        "metric": "selective-scan fwd+bwd GB/s (% HBM peak) + elems/s, D=1536 N=16 L=2048",
+        "metric": f"selective-scan fwd+bwd GB/s (% HBM peak) + elems/s, D={dim} N={dstate} L={seqlen}",
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -610,6 +689,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "bytes_per_launch": dom_bytes,
         },
         "cpu_baseline": None,

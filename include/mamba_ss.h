@@ -310,8 +310,9 @@ typedef struct ss_state_update_args {
     void* out;
     /* ABI v10: when delta_low is not NULL, delta is the low-rank product
      *   delta[b, d] = sum_r delta_low[b, r] * delta_weight[d, r]
-     * (the block's delta projection, summed in fp32 inside the kernel) and
-     * the delta pointer and strides are ignored; delta_low (batch,
+     * (the block's delta projection, summed in fp32 inside the kernel and
+     * rounded once to itype, as that projection's output is in the forward)
+     * and the delta pointer and strides are ignored; delta_low (batch,
      * delta_rank) and delta_weight (dim, delta_rank) in itype. */
     int64_t delta_rank;
     int64_t delta_low_batch_stride, delta_low_rank_stride;

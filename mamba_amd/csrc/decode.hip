@@ -26,6 +26,14 @@
 
 namespace ss {
 
+// v rounded to IT and back to float (round to nearest even)
+template <typename IT>
+__device__ __forceinline__ float round_to(float v) {
+    if constexpr (sizeof(IT) == 4) return v;
+    else if constexpr (__is_same(IT, bf16_t)) return __uint_as_float(uint32_t(io<bf16_t>::round(v)) << 16);
+    else return float(_Float16(v));
+}
+
 namespace {
 
 constexpr int kDT = 256;              // threads per workgroup
@@ -88,7 +96,9 @@ __global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update
         if (r < a.delta_rank)
             s0 = __builtin_fmaf(io<IT>::load(lo + r * a.delta_low_rank_stride),
                                 io<IT>::load(wr + r * a.delta_weight_rank_stride), s0);
-        dt = s0 + s1;
+        // rounded to the element type, as the forward's delta is: there it is
+        // the output of the block's delta projection, a GEMM in that type
+        dt = round_to<IT>(s0 + s1);
     } else {
         dt = io<IT>::load(dts + b * a.delta_batch_stride + d * a.delta_dim_stride);
     }

@@ -2,7 +2,9 @@
 
 Test infrastructure only.  ``build()`` compiles the library with the
 Makefile beside this file; the wrappers take and return torch tensors and
-do all arithmetic in float64.
+do all arithmetic in float64.  ``scan`` is the same forward / backward as an
+autograd function, so the block and model oracles can differentiate through
+long sequences without selective_scan_ref's per-step autograd graph.
 """
 import ctypes
 import os
@@ -82,3 +84,32 @@ def bwd(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False
     if rc != 0:
         raise ValueError("ss_oracle_bwd rejected the shapes")
     return dict(du=du, ddelta=dd, dA=dA, dB=dB, dC=dC, dD=dD, ddelta_bias=db, dz=dz)
+
+
+class CScanFn(torch.autograd.Function):
+    """selective_scan (forward_kernel.cu:174-310, backward_kernel.cu:276-585,
+    z gate of modules/mamba_simple.py:143-146) with both directions in the
+    float64 C restatement; the output comes back in u's dtype."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B, C, D, z, delta_bias, delta_softplus):
+        out, _ = fwd(u, delta, A, B, C, D, z=z, delta_bias=delta_bias, delta_softplus=delta_softplus)
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias)
+        ctx.delta_softplus = delta_softplus
+        return out.to(u.dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        u, delta, A, B, C, D, z, bias = ctx.saved_tensors
+        g = bwd(u, delta, A, B, C, D, z=z, delta_bias=bias, delta_softplus=ctx.delta_softplus, dout=dout)
+
+        def cast(x, ref):
+            return None if x is None or ref is None else x.to(ref.dtype)
+        return (cast(g["du"], u), cast(g["ddelta"], delta), cast(g["dA"], A), cast(g["dB"], B),
+                cast(g["dC"], C), cast(g["dD"], D), cast(g["dz"], z), cast(g["ddelta_bias"], bias), None)
+
+
+def scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False, compute_dtype=None):
+    """selective_scan_ref's signature on the C restatement (compute_dtype is
+    ignored: the arithmetic is float64); differentiable."""
+    return CScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus)

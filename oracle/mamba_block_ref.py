@@ -44,8 +44,10 @@ def causal_conv1d_ref(x, weight, bias=None, activation=None):
 
 def mamba_inner_ref(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight,
                     out_proj_weight, out_proj_bias, A, B=None, C=None, D=None, delta_bias=None,
-                    B_proj_bias=None, C_proj_bias=None, delta_softplus=True):
-    """xz: (batch, 2 * dim, seqlen) -> (batch, seqlen, out_features)."""
+                    B_proj_bias=None, C_proj_bias=None, delta_softplus=True, scan=None):
+    """xz: (batch, 2 * dim, seqlen) -> (batch, seqlen, out_features).  ``scan``
+    replaces selective_scan_ref (same signature), e.g. c_oracle.scan for
+    long sequences."""
     L = xz.shape[-1]
     R = delta_proj_weight.shape[1]
     N = A.shape[-1]
@@ -65,12 +67,12 @@ def mamba_inner_ref(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_we
             C = C + C_proj_bias.to(C.dtype)
         C = C.reshape(batch, L, N).transpose(1, 2).unsqueeze(1)
     ct = torch.float64 if x.dtype == torch.float64 else torch.float32
-    y = selective_scan_ref(x, delta, A, B, C, D, z=z, delta_bias=delta_bias,
-                           delta_softplus=delta_softplus, compute_dtype=ct)
+    y = (scan or selective_scan_ref)(x, delta, A, B, C, D, z=z, delta_bias=delta_bias,
+                                     delta_softplus=delta_softplus, compute_dtype=ct)
     return F.linear(y.transpose(1, 2), out_proj_weight, out_proj_bias)
 
 
-def mamba_simple_ref(p, hidden, state_dim=16):
+def mamba_simple_ref(p, hidden, state_dim=16, scan=None):
     """MambaSimple.forward (modules/mamba_simple.py:95-149) from its parameters.
 
     p: dict with the reference module's parameter names: input_proj.weight
@@ -83,7 +85,8 @@ def mamba_simple_ref(p, hidden, state_dim=16):
     A = -torch.exp(p["log_A"].to(ft))
     return mamba_inner_ref(xz, p["short_conv.weight"], p.get("short_conv.bias"), p["ssm_param_proj.weight"],
                            p["delta_proj.weight"], p["output_proj.weight"], p.get("output_proj.bias"), A,
-                           D=p["D"].to(ft), delta_bias=p["delta_proj.bias"].to(ft), delta_softplus=True)
+                           D=p["D"].to(ft), delta_bias=p["delta_proj.bias"].to(ft), delta_softplus=True,
+                           scan=scan)
 
 
 def rms_norm_ref(x, weight, eps=1e-6):
@@ -100,7 +103,7 @@ def add_rms_norm_ref(x, residual, weight, eps=1e-6):
     return rms_norm_ref(s, weight, eps), s
 
 
-def causal_lm_ref(p, input_ids, num_layers, state_dim=16, eps=1e-6):
+def causal_lm_ref(p, input_ids, num_layers, state_dim=16, eps=1e-6, scan=None):
     """CausalLM.forward in eval mode (dropout off): models/causal_lm.py:30-59.
 
     p holds the reference model's state_dict names: embedding.weight,
@@ -109,6 +112,6 @@ def causal_lm_ref(p, input_ids, num_layers, state_dim=16, eps=1e-6):
     h = F.embedding(input_ids, p["embedding.weight"])
     for i in range(num_layers):
         sub = {k[len(f"layers.{i}.mamba."):]: v for k, v in p.items() if k.startswith(f"layers.{i}.mamba.")}
-        h = h + mamba_simple_ref(sub, rms_norm_ref(h, p[f"layers.{i}.norm.weight"], eps), state_dim)
+        h = h + mamba_simple_ref(sub, rms_norm_ref(h, p[f"layers.{i}.norm.weight"], eps), state_dim, scan=scan)
     h = rms_norm_ref(h, p["norm.weight"], eps)
     return F.linear(h, p.get("lm_head.weight", p["embedding.weight"]))

@@ -14,6 +14,7 @@
   refuses more than one GPU.
 """
 import ctypes
+import json
 import os
 import re
 import subprocess
@@ -314,6 +315,36 @@ def test_bench_byte_model():
     fwd, bwd = bench.algorithmic_bytes(8, 1536, 16, 2048, 4)
     assert (fwd, bwd) == (404_860_928, 709_058_560)
     assert sum(bench.algorithmic_bytes(4, 5120, 16, 8192, 2)) == 3_700_482_048
+
+
+def test_bench_inputs_and_provenance(tmp_path, monkeypatch):
+    """The bench draws its own inputs (its GPU leg imports nothing from
+    oracle/), with the oracle's distributions and draw order; a stored
+    traffic figure is reported only for the kernel sources it was taken with."""
+    sys.path.insert(0, ROOT)
+    import bench
+    import torch
+    from oracle.selective_scan_ref import make_inputs
+    got = bench.synthetic_inputs(2, 32, 16, 64, seed=7, dtype=torch.bfloat16)
+    want = make_inputs(2, 32, 16, 64, seed=7, dtype=torch.bfloat16)
+    for k in ("u", "delta", "z", "B", "C", "dout", "delta_bias", "A", "D"):
+        assert torch.equal(got[k], want[k]), k
+    # the scan leg of main() and the helpers it calls do not name the oracle
+    import inspect
+    src = inspect.getsource(bench.main)
+    assert "import" not in src.split("cpu_baseline(")[0] or "oracle" not in "".join(
+        l for l in src.split("cpu_baseline(")[0].splitlines() if "import" in l)
+    rec = {"sources_sha256": bench.kernel_sources_digest(), "k": 123}
+    (tmp_path / "profiles").mkdir()
+    (tmp_path / "profiles" / "traffic_w.json").write_text(json.dumps(rec))
+    (tmp_path / "mamba_amd").symlink_to(os.path.join(ROOT, "mamba_amd"))
+    monkeypatch.setattr(bench, "_HERE", str(tmp_path))
+    assert bench.stored_traffic("w", "k")[0] == 123
+    rec["sources_sha256"] = "0" * 64
+    (tmp_path / "profiles" / "traffic_w.json").write_text(json.dumps(rec))
+    val, why = bench.stored_traffic("w", "k")
+    assert val is None and "stale" in why
+    assert bench.cpu_threads() >= 1 and bench.cpu_model()
 
 
 def test_bench_refuses_more_than_one_gpu():

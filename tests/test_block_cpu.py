@@ -17,7 +17,7 @@ import torch.nn.functional as F
 
 from mamba_amd.models import CausalLM, CausalLMConfig
 from mamba_amd.modules import MambaSimple, RMSNorm
-from oracle.mamba_block_ref import causal_conv1d_ref, causal_lm_ref, mamba_simple_ref, rms_norm_ref
+from oracle.mamba_block_ref import causal_conv1d_ref, causal_lm_ref, mamba_inner_ref, mamba_simple_ref, rms_norm_ref
 from oracle.selective_scan_ref import selective_scan_ref
 
 F64 = torch.float64
@@ -208,3 +208,43 @@ def test_initialisation_matches_reference_rules():
     assert float(dt.min()) >= 1e-3 * 0.999 and float(dt.max()) <= 1e-1 * 1.001
     bound = m.delta_rank ** -0.5
     assert float(m.delta_proj.weight.detach().abs().max()) <= bound
+
+
+def test_c_scan_autograd_matches_scan_oracle():
+    """c_oracle.scan (the float64 C restatement as an autograd function, used by
+    the block and model oracles on long sequences) gives selective_scan_ref's
+    output and, through autograd, its gradients; a Mamba block differentiated
+    through either scan agrees too."""
+    from oracle import c_oracle
+    from oracle.selective_scan_ref import make_inputs, selective_scan_ref
+    x = make_inputs(2, 24, 8, 40, seed=31)
+    names = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
+    a = {k: x[k].double().requires_grad_(True) for k in names}
+    b = {k: x[k].double().requires_grad_(True) for k in names}
+    oa = selective_scan_ref(*(a[k] for k in names[:6]), z=a["z"], delta_bias=a["delta_bias"],
+                            delta_softplus=True, compute_dtype=torch.float64)
+    ob = c_oracle.scan(*(b[k] for k in names[:6]), z=b["z"], delta_bias=b["delta_bias"], delta_softplus=True)
+    assert torch.allclose(oa, ob, rtol=1e-10, atol=1e-10)
+    dout = x["dout"].double()
+    oa.backward(dout)
+    ob.backward(dout)
+    for k in names:
+        assert torch.allclose(a[k].grad, b[k].grad, rtol=1e-9, atol=1e-9), k
+
+    torch.manual_seed(3)
+    batch, d_model, dim, L, R, N = 2, 16, 32, 24, 4, 8
+    xz = torch.randn(batch, 2 * dim, L, dtype=torch.float64)
+    w = [torch.randn(dim, 1, 4, dtype=torch.float64) * 0.3, torch.randn(dim, dtype=torch.float64) * 0.1,
+         torch.randn(R + 2 * N, dim, dtype=torch.float64) * dim ** -0.5,
+         torch.rand(dim, R, dtype=torch.float64) * R ** -0.5, torch.randn(d_model, dim, dtype=torch.float64) * 0.2,
+         None, -torch.arange(1, N + 1, dtype=torch.float64).repeat(dim, 1)]
+    grads = []
+    for scan in (None, c_oracle.scan):
+        xg = xz.clone().requires_grad_(True)
+        ws = [t.clone().requires_grad_(True) if t is not None else None for t in w]
+        out = mamba_inner_ref(xg, *ws, D=torch.ones(dim, dtype=torch.float64),
+                              delta_bias=torch.full((dim,), -2.0, dtype=torch.float64), scan=scan)
+        out.pow(2).sum().backward()
+        grads.append([xg.grad] + [t.grad for t in ws if t is not None])
+    for ga, gb in zip(*grads):
+        assert torch.allclose(ga, gb, rtol=1e-9, atol=1e-9)

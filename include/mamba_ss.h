@@ -30,7 +30,8 @@
  *
  * All calls are asynchronous on `stream` (a hipStream_t, NULL = default
  * stream) and re-entrant: no global mutable state besides the thread-local
- * error message.
+ * error message, except ss_bwd_noalloc, whose calls share one fixed scratch
+ * buffer per GPU (see there).
  */
 #ifndef MAMBA_SS_H
 #define MAMBA_SS_H
@@ -41,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 10
+#define SS_ABI_VERSION 11
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -184,6 +185,22 @@ int ss_fwd(const ss_fwd_args* a, void* stream);
    ddelta_bias (after clearing them when zero_grads is set).  Replaces selective_scan.backward / backward_kernel_launch
    (selective_scan.cpp:246-329, backward_kernel.cu:588-618). */
 int ss_bwd(const ss_bwd_args* a, void* stream);
+
+/* ss_bwd that allocates nothing and needs no workspace from the caller.  No
+   counterpart in the reference: it is for callers that cannot allocate
+   device memory (code under HIP graph capture, tight serving or training
+   loops, harnesses that forbid hipMalloc).  Same arguments, kernels and
+   results as ss_bwd; a->workspace and a->workspace_bytes are ignored.  The
+   scratch that ss_bwd would take from a workspace (dB / dC slices, sequence
+   segment carries) comes from a fixed device buffer of
+   SS_NOALLOC_SCRATCH_BYTES bytes inside the library, one per GPU, held until
+   the process ends; arguments that need more (ss_bwd_workspace_bytes) are
+   rejected with SS_ERR_UNSUPPORTED.  Every call on a GPU shares that GPU's
+   buffer, and each call clears what it uses: calls that overlap in time on
+   one GPU (several streams or threads) race and must be serialised by the
+   caller. */
+#define SS_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int ss_bwd_noalloc(const ss_bwd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------
  * Causal depthwise conv1d (+ SiLU), the step before the scan in the Mamba

@@ -13,13 +13,15 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 10
+ABI_VERSION = 11
+# bytes of the fixed device scratch of ss_bwd_noalloc (SS_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 EXPORTED = (
     "ss_abi_version", "ss_chunk_size", "ss_max_dstate", "ss_struct_sizes",
     "ss_last_error", "ss_fwd_check", "ss_bwd_check", "ss_bwd_workspace_bytes", "ss_fwd_workspace_bytes",
     "ss_fwd_kernel_name", "ss_bwd_kernel_name",
-    "ss_fwd", "ss_bwd", "ss_conv1d_fwd", "ss_conv1d_bwd",
+    "ss_fwd", "ss_bwd", "ss_bwd_noalloc", "ss_conv1d_fwd", "ss_conv1d_bwd",
     "ss_rmsnorm_fwd", "ss_rmsnorm_bwd", "ss_rmsnorm_bwd_workspace_bytes",
     "ss_state_update", "ss_conv1d_update", "ss_decode_linear",
 )
@@ -199,6 +201,8 @@ def load():
         lib.ss_fwd.restype = ctypes.c_int
         lib.ss_bwd.argtypes = [ctypes.POINTER(BwdArgs), _p]
         lib.ss_bwd.restype = ctypes.c_int
+        lib.ss_bwd_noalloc.argtypes = [ctypes.POINTER(BwdArgs), _p]
+        lib.ss_bwd_noalloc.restype = ctypes.c_int
         if lib.ss_abi_version() != ABI_VERSION:
             raise RuntimeError(f"mamba_amd: library ABI {lib.ss_abi_version()} != binding ABI {ABI_VERSION}")
         fs, bs = _i64(), _i64()

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/mamba_ss.h"
@@ -269,6 +270,85 @@ int check_norm_common(int64_t rows, int64_t dim, int dtype, int w_dtype, const v
     return SS_OK;
 }
 
+
+// The backward of a call with no scan work (batch, dim or seqlen 0): only
+// zero_grads has something to do, clearing the accumulators.
+int bwd_empty(const ss_bwd_args* a, void* stream) {
+    if (!a->zero_grads) return ok();
+    ss::BwdParams p = make_bwd_params(a);
+    struct G { const float* ptr; int64_t n; const char* name; };
+    const G gs[] = {{a->dA, p.dA_n, "dA"}, {a->dB, p.dB_n, "dB"}, {a->dC, p.dC_n, "dC"},
+                    {a->f.has_D ? a->dD : nullptr, a->f.has_D ? p.dD_n : 0, "dD"},
+                    {a->f.has_delta_bias ? a->ddelta_bias : nullptr, a->f.has_delta_bias ? p.dD_n : 0,
+                     "ddelta_bias"}};
+    for (const G& g : gs) {
+        if (g.n > 0 && !g.ptr) return fail(SS_ERR_INVALID, "%s is NULL", g.name);
+        if (g.ptr && !aligned(g.ptr, 4)) return fail(SS_ERR_INVALID, "%s is misaligned", g.name);
+    }
+    hipError_t e = ss::launch_bwd_zero_only(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+// The backward of checked arguments with scratch ws of ws_bytes bytes (NULL:
+// none; the kernels then run without dB / dC slices and sequence segments).
+int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
+    ss::BwdParams p = make_bwd_params(a);
+    int slices = 1, nseg = 1;
+    int64_t slice_bytes = 0;
+    const int64_t need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
+    if (need > 0 && ws) {
+        if (ws_bytes < need)
+            return fail(SS_ERR_INVALID, "workspace of %lld bytes, %lld needed", (long long)ws_bytes,
+                        (long long)need);
+        if (!aligned(ws, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
+        if (slice_bytes > 0) {
+            p.ws = static_cast<float*>(ws);
+            p.ws_slices = slices;
+            p.ws_stride = slice_bytes / int64_t(sizeof(float)) / (2 * slices);
+        }
+        if (nseg > 1) {
+            p.f.nseg = nseg;
+            p.f.seg_h = reinterpret_cast<float*>(static_cast<char*>(ws) + slice_bytes);
+            p.f.seg_s = p.f.seg_h + p.f.batch * nseg * p.f.dim * 16;
+        }
+    }
+    hipError_t e = ss::launch_bwd(p, a->f.itype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+// Fixed device scratch of ss_bwd_noalloc, for callers that cannot allocate.
+// Each GPU the library runs on holds its own copy until the process ends.
+// Host code never passes `scratch` itself to a kernel or a copy (on the host
+// it names a stand-in, not device memory): it looks up the array's device
+// address once per device with hipGetSymbolAddress and uses that.
+constexpr int64_t kScratchBytes = SS_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device, with that device current).
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(SS_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(SS_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(SS_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return SS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -355,46 +435,29 @@ int ss_bwd(const ss_bwd_args* a, void* stream) {
     bool empty = false;
     int rc = check_bwd(a, &empty);
     if (rc != SS_OK) return rc;
-    if (empty) {
-        // no scan work, but zero_grads still owes zeroed accumulators
-        if (!a->zero_grads) return ok();
-        ss::BwdParams p = make_bwd_params(a);
-        struct G { const float* ptr; int64_t n; const char* name; };
-        const G gs[] = {{a->dA, p.dA_n, "dA"}, {a->dB, p.dB_n, "dB"}, {a->dC, p.dC_n, "dC"},
-                        {a->f.has_D ? a->dD : nullptr, a->f.has_D ? p.dD_n : 0, "dD"},
-                        {a->f.has_delta_bias ? a->ddelta_bias : nullptr, a->f.has_delta_bias ? p.dD_n : 0,
-                         "ddelta_bias"}};
-        for (const G& g : gs) {
-            if (g.n > 0 && !g.ptr) return fail(SS_ERR_INVALID, "%s is NULL", g.name);
-            if (g.ptr && !aligned(g.ptr, 4)) return fail(SS_ERR_INVALID, "%s is misaligned", g.name);
-        }
-        hipError_t e = ss::launch_bwd_zero_only(p, static_cast<hipStream_t>(stream));
-        if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
-        return ok();
-    }
-    ss::BwdParams p = make_bwd_params(a);
+    if (empty) return bwd_empty(a, stream);
+    return bwd_run(a, a->workspace, a->workspace ? a->workspace_bytes : 0, stream);
+}
+
+int ss_bwd_noalloc(const ss_bwd_args* a, void* stream) {
+    bool empty = false;
+    int rc = check_bwd(a, &empty);
+    if (rc != SS_OK) return rc;
+    if (empty) return bwd_empty(a, stream);
     int slices = 1, nseg = 1;
     int64_t slice_bytes = 0;
-    const int64_t need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
-    if (need > 0 && a->workspace) {
-        if (a->workspace_bytes < need)
-            return fail(SS_ERR_INVALID, "workspace of %lld bytes, %lld needed", (long long)a->workspace_bytes,
-                        (long long)need);
-        if (!aligned(a->workspace, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
-        if (slice_bytes > 0) {
-            p.ws = static_cast<float*>(a->workspace);
-            p.ws_slices = slices;
-            p.ws_stride = slice_bytes / int64_t(sizeof(float)) / (2 * slices);
-        }
-        if (nseg > 1) {
-            p.f.nseg = nseg;
-            p.f.seg_h = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + slice_bytes);
-            p.f.seg_s = p.f.seg_h + p.f.batch * nseg * p.f.dim * 16;
-        }
+    const int64_t need = ws_bytes_for(make_bwd_params(a), &slices, &nseg, &slice_bytes);
+    if (need > kScratchBytes)
+        return fail(SS_ERR_UNSUPPORTED,
+                    "ss_bwd_noalloc: these arguments need %lld bytes of scratch, more than the %lld bytes "
+                    "of its fixed device buffer; use ss_bwd with a workspace",
+                    (long long)need, (long long)kScratchBytes);
+    void* ws = nullptr;
+    if (need > 0) {
+        rc = scratch_on_current_device(&ws);
+        if (rc != SS_OK) return rc;
     }
-    hipError_t e = ss::launch_bwd(p, a->f.itype, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
-    return ok();
+    return bwd_run(a, ws, need, stream);
 }
 
 int ss_conv1d_fwd(const ss_conv1d_args* a, void* stream) {

@@ -60,7 +60,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 10
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 11
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -500,3 +500,24 @@ def test_forward_workspace_query(nat, lib):
     assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 0                           # general kernel: serial
     a.u = None
     assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == -1
+
+
+def test_noalloc_entry_checks_before_device_work(nat, lib):
+    """ss_bwd_noalloc: the scratch limit of the header is the binding's; bad
+    arguments and arguments needing more scratch than the fixed buffer are
+    rejected before any device work (no GPU is touched here)."""
+    text = open(HEADER).read()
+    m = re.search(r"#define\s+SS_NOALLOC_SCRATCH_BYTES\s+\((\d+)ll\s*<<\s*(\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == nat.NOALLOC_SCRATCH_BYTES
+    bad = valid_bwd(nat)
+    bad.dout = None
+    assert lib.ss_bwd_noalloc(ctypes.byref(bad), None) == nat.SS_ERR_INVALID
+    assert "dout is NULL" in lib.ss_last_error().decode()
+    # 1632 channel blocks in one group: 16 dB / dC slices of 16 x 32768 floats
+    # each, 64 MiB, twice the fixed buffer
+    big = valid_bwd(nat, batch=1, dim=26112, seqlen=32768)
+    need = lib.ss_bwd_workspace_bytes(ctypes.byref(big))
+    assert need == 2 * 16 * (16 * 32768) * 4 > nat.NOALLOC_SCRATCH_BYTES
+    assert lib.ss_bwd_noalloc(ctypes.byref(big), None) == nat.SS_ERR_UNSUPPORTED
+    msg = lib.ss_last_error().decode()
+    assert str(need) in msg and str(nat.NOALLOC_SCRATCH_BYTES) in msg

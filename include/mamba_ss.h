@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 11
+#define SS_ABI_VERSION 12
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -131,7 +131,17 @@ typedef struct ss_bwd_args {
        the clearing shares a launch with the workspace's.  0: accumulate into
        what the caller passes. */
     int32_t zero_grads;
-    int32_t pad_;
+    /* nonzero: deterministic sums (ABI v12).  dB and dC are summed over the
+       channels, and dA, dD and ddelta_bias over batch rows and sequence
+       segments, in a fixed order instead of by atomic adds, so repeated calls
+       on the same inputs give the same bits.  Needs the fast kernels (dstate
+       16, variable B and C, seqlen a multiple of 32, dim and channels per
+       group multiples of 16; SS_ERR_UNSUPPORTED otherwise), 16-byte aligned
+       dB / dC, and a workspace of ss_bwd_workspace_bytes() bytes (one dB /
+       dC partial per 16-channel block: batch * dim / 8 * dstate * seqlen
+       floats).  No counterpart in the reference, whose sums are atomic
+       (backward_kernel.cu:472-475,553-578). */
+    int32_t deterministic;
 } ss_bwd_args;
 
 /* ABI version (SS_ABI_VERSION of the built library). */

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 11
+ABI_VERSION = 12
 # bytes of the fixed device scratch of ss_bwd_noalloc (SS_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -59,7 +59,7 @@ class BwdArgs(ctypes.Structure):
         ("dout", _p), ("du", _p), ("ddelta", _p), ("dz", _p),
         ("dA", _p), ("dB", _p), ("dC", _p), ("dD", _p), ("ddelta_bias", _p),
         ("workspace", _p), ("workspace_bytes", _i64),
-        ("zero_grads", _i32), ("pad_", _i32),
+        ("zero_grads", _i32), ("deterministic", _i32),
     ]
 
 

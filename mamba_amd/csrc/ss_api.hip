@@ -206,6 +206,8 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     p.ws_slices = 1;
     p.ws_stride = 0;
     p.zero_grads = a->zero_grads != 0;
+    p.det = a->deterministic != 0;
+    p.det_par = nullptr;
     const ss_fwd_args& f = a->f;
     const int64_t G = (f.is_var_B || f.is_var_C) ? f.n_groups : 1;
     p.dA_n = f.dim * f.dstate;
@@ -219,17 +221,36 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
 // not use one: other kernel, one slice, or dB / dC not 16-byte aligned).
 // Backward workspace: the dB / dC slices (when they apply), then the
 // sequence-segment carries (when they apply).  *slice_bytes: the first part.
+// With deterministic sums (p.det, fast kernels only) every channel block of
+// a group has a slice of its own, even a lone one, and the dA / dD /
+// ddelta_bias partials follow the carries: (batch * nseg) rows of dim * 18
+// floats.
 int64_t ws_bytes_for(const ss::BwdParams& p, int* slices, int* nseg, int64_t* slice_bytes) {
     *slices = ss::bwd_ws_slices(p);
     *slice_bytes = 0;
-    if (*slices <= 1 || !aligned(p.dB, 16) || !aligned(p.dC, 16)) {
+    const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * p.f.seqlen;
+    if (p.det) {
+        *slice_bytes = int64_t(2) * *slices * stride * int64_t(sizeof(float));
+    } else if (*slices <= 1 || !aligned(p.dB, 16) || !aligned(p.dC, 16)) {
         *slices = 1;
     } else {
-        const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * p.f.seqlen;
         *slice_bytes = int64_t(2) * *slices * stride * int64_t(sizeof(float));
     }
     *nseg = ss::bwd_segments(p);
-    return *slice_bytes + ss::fwd_seg_bytes(p.f, *nseg);
+    const int64_t par = p.det ? p.f.batch * *nseg * p.f.dim * (p.f.dstate + 2) * int64_t(sizeof(float)) : 0;
+    return *slice_bytes + ss::fwd_seg_bytes(p.f, *nseg) + par;
+}
+
+// Deterministic sums need the fast kernels and 16-byte aligned dB / dC.
+int check_det(const ss::BwdParams& p) {
+    if (!p.det) return SS_OK;
+    if (!ss::bwd_fast_ok(p))
+        return fail(SS_ERR_UNSUPPORTED,
+                    "deterministic sums need the fast backward (dstate 16, variable B and C, seqlen a multiple "
+                    "of 32, dim and channels per group multiples of 16)");
+    if (!aligned(p.dB, 16) || !aligned(p.dC, 16))
+        return fail(SS_ERR_UNSUPPORTED, "deterministic sums need 16-byte aligned dB and dC");
+    return SS_OK;
 }
 
 int check_conv(const ss_conv1d_args* a, bool* empty) {
@@ -294,9 +315,13 @@ int bwd_empty(const ss_bwd_args* a, void* stream) {
 // none; the kernels then run without dB / dC slices and sequence segments).
 int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
     ss::BwdParams p = make_bwd_params(a);
+    int rc = check_det(p);
+    if (rc != SS_OK) return rc;
     int slices = 1, nseg = 1;
     int64_t slice_bytes = 0;
     const int64_t need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
+    if (p.det && need > 0 && !ws)
+        return fail(SS_ERR_INVALID, "deterministic sums need a workspace of %lld bytes", (long long)need);
     if (need > 0 && ws) {
         if (ws_bytes < need)
             return fail(SS_ERR_INVALID, "workspace of %lld bytes, %lld needed", (long long)ws_bytes,
@@ -307,11 +332,13 @@ int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
             p.ws_slices = slices;
             p.ws_stride = slice_bytes / int64_t(sizeof(float)) / (2 * slices);
         }
+        const int64_t seg_bytes = ss::fwd_seg_bytes(p.f, nseg);
         if (nseg > 1) {
             p.f.nseg = nseg;
             p.f.seg_h = reinterpret_cast<float*>(static_cast<char*>(ws) + slice_bytes);
             p.f.seg_s = p.f.seg_h + p.f.batch * nseg * p.f.dim * 16;
         }
+        if (p.det) p.det_par = reinterpret_cast<float*>(static_cast<char*>(ws) + slice_bytes + seg_bytes);
     }
     hipError_t e = ss::launch_bwd(p, a->f.itype, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
@@ -410,11 +437,13 @@ int64_t ss_fwd_workspace_bytes(const ss_fwd_args* a) {
 int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a) {
     bool empty = false;
     if (check_bwd(a, &empty) != SS_OK) return -1;
+    if (empty) return ok(), 0;
+    const ss::BwdParams p = make_bwd_params(a);
+    if (check_det(p) != SS_OK) return -1;
     ok();
-    if (empty) return 0;
     int slices = 1, nseg = 1;
     int64_t slice_bytes = 0;
-    return ws_bytes_for(make_bwd_params(a), &slices, &nseg, &slice_bytes);
+    return ws_bytes_for(p, &slices, &nseg, &slice_bytes);
 }
 
 const char* ss_fwd_kernel_name(const ss_fwd_args* a) {
@@ -444,9 +473,12 @@ int ss_bwd_noalloc(const ss_bwd_args* a, void* stream) {
     int rc = check_bwd(a, &empty);
     if (rc != SS_OK) return rc;
     if (empty) return bwd_empty(a, stream);
+    const ss::BwdParams p = make_bwd_params(a);
+    rc = check_det(p);
+    if (rc != SS_OK) return rc;
     int slices = 1, nseg = 1;
     int64_t slice_bytes = 0;
-    const int64_t need = ws_bytes_for(make_bwd_params(a), &slices, &nseg, &slice_bytes);
+    const int64_t need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
     if (need > kScratchBytes)
         return fail(SS_ERR_UNSUPPORTED,
                     "ss_bwd_noalloc: these arguments need %lld bytes of scratch, more than the %lld bytes "

@@ -396,7 +396,9 @@ __device__ __forceinline__ float rows4_sum(float v0, float v1, float v2, float v
 // flush reading (16 steps x 2 states).
 __device__ __forceinline__ int wg_slot(int t, int n) { return t * 16 + (n ^ t); }
 
-template <typename IT, bool kZ>
+// kDet: deterministic sums (plain stores of the partials, summed in a fixed
+// order afterwards) instead of atomic adds.
+template <typename IT, bool kZ, bool kDet>
 // 3 workgroups per CU (12 waves): at most 168 VGPRs and 54,613 B of LDS.
 __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kT];              // [buf][B, C][n][t]
@@ -422,7 +424,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const int64_t g = c0 / p.dpg;
     const int64_t L = p.seqlen;
     const int64_t G = p.dim / p.dpg;
-    const int nck = int(L / kT);     // even; below 2^22 (seqlen < 2^26)
+    // chunks of 16 steps, padded to an even count: a ragged seqlen ends in a
+    // partial chunk and, for an odd count, one wholly past the sequence; both
+    // are the first two this kernel runs (the tail), made of identity steps
+    const int nck = int((L + 2 * kT - 1) / (2 * kT)) * 2;   // below 2^22 (seqlen < 2^26)
     // this workgroup's chunks [k0, k1), an even number starting at an even index
     const int k0 = seg * (nck / nseg), k1 = k0 + nck / nseg;
 
@@ -441,7 +446,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const rsrc_t Rdd = make_rsrc(static_cast<IT*>(q.ddelta) + b * q.dd_bs + c0 * q.dd_ds);
     const rsrc_t Rdz = make_rsrc(kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + c0 * q.dz_ds : nullptr);
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
-    const rsrc_t Rx = make_rsrc(p.x + (b * nck * p.dim + c0) * kT);
+    const rsrc_t Rx = make_rsrc(p.x + (b * p.n_chunks * p.dim + c0) * kT);
     // dB / dC of this batch row and group, or of its slice of the workspace
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
     const rsrc_t RdB = make_rsrc((q.ws ? q.ws + 2 * slice * q.ws_stride : q.dB) + (b * G + g) * int64_t(kT) * L);
@@ -494,6 +499,29 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         const float v = bload<float>(Rx, ox, uint32_t(ck > 0 ? ck - 1 : 0) * x_chunk_bytes);
         P.x = ck > 0 ? v : 0.f;
     };
+    // A chunk of the tail: loads at steps clamped to the sequence, and past
+    // its end the inputs of an identity step (delta' = 0, so decay 1 and no
+    // input; dout, u, B, C zero), as the reference pads its last chunk
+    // (backward_kernel.cu:291-315 with forward_kernel.cu:267-271).
+    auto fetch_tail = [&](int ck, Chunk& P) {
+        const int t = ck * kT + r;
+        const bool in = t < L;
+        const int te = in ? t : int(L) - 1;
+        P.u = in ? bload<IT>(Ru, uint32_t(row * p.u_ds + te) * es, 0) : 0.f;
+        P.d = in ? bload<IT>(Rd, uint32_t(row * p.dl_ds + te) * es, 0) : (softplus ? -INFINITY : -bias);
+        P.o = in ? bload<IT>(Ro, uint32_t(row * q.do_ds + te) * es, 0) : 0.f;
+        if constexpr (kZ) {
+            P.z = in ? bload<IT>(Rz, uint32_t(row * p.z_ds + te) * es, 0) : 0.f;
+            P.y = in ? bload<IT>(Ry, uint32_t(row * p.y_ds + te) * es, 0) : 0.f;
+        } else {
+            P.z = 0.f;
+            P.y = 0.f;
+        }
+        P.B = in ? bload<IT>(RB, uint32_t(row * p.B_ns + te) * es, 0) : 0.f;
+        P.C = in ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
+        const float v = bload<float>(Rx, ox, uint32_t(ck > 0 ? ck - 1 : 0) * x_chunk_bytes);
+        P.x = ck > 0 ? v : 0.f;
+    };
     // this lane's element of the B / C tile (state row, step r) into buffer buf
     auto stage = [&](const Chunk& P, int buf) {
         s_bc[(buf * 2 + 0) * 16 * kT + bc_slot(row, r)] = P.B;
@@ -502,7 +530,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // dB / dC of chunk ck from wave-partial buffer buf: thread (n, t) sums the
     // 4 waves and adds once into global memory (16 consecutive steps per state)
     const int fn = tid >> 4, ft = tid & 15;
-    const uint32_t ofl = uint32_t(fn * L + ft) * 4u;
+    const uint32_t ofl0 = uint32_t(fn * L + ft) * 4u;
     // split in the LDS reads and the sums + global adds, so that other work
     // can sit between them
     auto flush_read = [&](int buf, float (&v)[2 * kWaves]) {
@@ -512,17 +540,29 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             v[kWaves + ww] = s_wg[((buf * 2 + 1) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
         }
     };
-    auto flush_commit = [&](int ck, const float (&v)[2 * kWaves]) {
+    // (TAIL: steps past the sequence, whose sums are zero, are added to its
+    // last step instead, so no address leaves the row)
+    auto flush_commit = [&](int ck, const float (&v)[2 * kWaves], auto TAIL) {
         const float sB = (v[0] + v[1]) + (v[2] + v[3]);
         const float sC = (v[4] + v[5]) + (v[6] + v[7]);
-        const uint32_t so = uint32_t(ck * kT) * 4u;
-        batomic_add(RdB, ofl, so, sB);
-        batomic_add(RdC, ofl, so, sC);
+        uint32_t so = uint32_t(ck * kT) * 4u;
+        uint32_t ofl = ofl0;
+        if constexpr (decltype(TAIL)::value) {
+            const int t = ck * kT + ft;
+            if (t >= L) ofl = uint32_t(fn * L + int(L) - 1 - ck * kT) * 4u;
+        }
+        if constexpr (kDet) {
+            bstore<float>(RdB, ofl, so, sB);
+            bstore<float>(RdC, ofl, so, sC);
+        } else {
+            batomic_add(RdB, ofl, so, sB);
+            batomic_add(RdC, ofl, so, sC);
+        }
     };
     auto flush = [&](int ck, int buf) {
         float v[2 * kWaves];
         flush_read(buf, v);
-        flush_commit(ck, v);
+        flush_commit(ck, v, std::false_type{});
     };
 
     // the adjoint carry entering this segment from the right: the later
@@ -538,8 +578,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // refilled with chunk ck - 2; `nxt` holds chunk ck - 1, staged at the end.
     // BUF = ck & 1 is a compile-time constant of each unrolled half, so every
     // LDS address is an immediate offset.
-    auto chunk = [&](int ck, Chunk& cur_in, const Chunk& nxt, auto BUF) {
+    // TAIL: the chunks that may hold steps past the sequence (the first four
+    // run), whose outputs there are dropped.
+    auto chunk = [&](int ck_in, Chunk& cur_in, const Chunk& nxt, auto BUF, auto TAIL) {
         constexpr int buf = decltype(BUF)::value;
+        constexpr bool kTail = decltype(TAIL)::value;
+        // uniform: keeps the chunk's offsets in SGPRs (the tail's masked stores
+        // would otherwise turn them into waterfall loops)
+        const int ck = __builtin_amdgcn_readfirstlane(ck_in);
         lds_barrier();   // B / C tile of ck staged; dB / dC partials of ck + 1 complete
         const Chunk cur = cur_in;
         fetch(ck > k0 + 1 ? ck - 2 : k0, cur_in);
@@ -575,7 +621,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         });
         // the LDS reads issued above have had the decay factors to land
         __builtin_amdgcn_sched_barrier(0);
-        flush_commit(ck + 1 < k1 ? ck + 1 : k1 - 1, fv);
+        flush_commit(ck + 1 < k1 ? ck + 1 : k1 - 1, fv, TAIL);
         float hcur = h0;
         static_for<kT>([&](auto K) {
             constexpr int k = decltype(K)::value;
@@ -661,11 +707,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         const float ddt = uu * s1r + s2r;
         const float dd = softplus ? ddt * sigmoidf_(pre) : ddt;
         const uint32_t so = uint32_t(ck * kT) * es;
-        bstore<IT>(Rdu, odu, so, du);
-        bstore<IT>(Rdd, odd, so, dd);
-        if constexpr (kZ) bstore<IT>(Rdz, odz, so, dout * yv * sgz * (1.f + zz * (1.f - sgz)));
+        const bool in = !kTail || ck * kT + r < L;
+        if (in) {
+            bstore<IT>(Rdu, odu, so, du);
+            bstore<IT>(Rdd, odd, so, dd);
+            if constexpr (kZ) bstore<IT>(Rdz, odz, so, dout * yv * sgz * (1.f + zz * (1.f - sgz)));
+        }
         dD_acc += dy * uu;
-        db_acc += dd;
+        db_acc += in ? dd : 0.f;
 
         // B / C tile of the next chunk (ck - 1) into the other buffer
         stage(nxt, buf ^ 1);
@@ -673,15 +722,23 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
 
     // chunks k1 - 1, k1 - 2 first; two buffers of inputs alternate roles
     Chunk PA, PB;
-    fetch(k1 - 1, PA);
-    fetch(k1 - 2, PB);
+    fetch_tail(k1 - 1, PA);
+    fetch_tail(k1 - 2, PB);
     // the first flush (of the nonexistent chunk k1) adds these zeros to chunk k1 - 1
 #pragma unroll
     for (int i = 0; i < 8; ++i) s_wg[i * kThreads + tid] = 0.f;     // buffer k1 & 1 = 0
     stage(PA, 1);
-    for (int ck = k1 - 1; ck > k0; ck -= 2) {   // k0, k1 even: ck odd, then even
-        chunk(ck, PA, PB, std::integral_constant<int, 1>{});
-        chunk(ck - 1, PB, PA, std::integral_constant<int, 0>{});
+    // the first two pairs hold every output of the tail chunks (their dB / dC
+    // are flushed one chunk later); k0, k1 even: ck odd, then even
+    const int kt_end = k1 - 4 > k0 ? k1 - 4 : k0;
+    int ck = k1 - 1;
+    for (; ck > kt_end; ck -= 2) {
+        chunk(ck, PA, PB, std::integral_constant<int, 1>{}, std::true_type{});
+        chunk(ck - 1, PB, PA, std::integral_constant<int, 0>{}, std::true_type{});
+    }
+    for (; ck > k0; ck -= 2) {
+        chunk(ck, PA, PB, std::integral_constant<int, 1>{}, std::false_type{});
+        chunk(ck - 1, PB, PA, std::integral_constant<int, 0>{}, std::false_type{});
     }
     lds_barrier();
     flush(k0, 0);
@@ -689,11 +746,39 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // ---- per-channel and per-(channel, state) sums over time and batch
     dD_acc = row_allsum(dD_acc);
     db_acc = row_allsum(db_acc);
-    if (r == 0) {
-        if (q.dD) atomicAdd(q.dD + c, dD_acc);
-        if (q.ddelta_bias) atomicAdd(q.ddelta_bias + c, db_acc);
+    if constexpr (kDet) {
+        // this (batch row, segment)'s partials: row b * nseg + seg of det_par
+        float* pr = q.det_par + (b * nseg + seg) * p.dim * (kT + 2);
+        pr[c * kT + r] = dA_acc;
+        if (r == 0) {
+            pr[p.dim * kT + c] = dD_acc;
+            pr[p.dim * (kT + 1) + c] = db_acc;
+        }
+    } else {
+        if (r == 0) {
+            if (q.dD) atomicAdd(q.dD + c, dD_acc);
+            if (q.ddelta_bias) atomicAdd(q.ddelta_bias + c, db_acc);
+        }
+        atomicAdd(q.dA + c * kT + r, dA_acc);
     }
-    atomicAdd(q.dA + c * kT + r, dA_acc);
+}
+
+// Deterministic sums of the dA, dD, ddelta_bias partials: element i of
+// [dA (dim * 16), dD (dim), ddelta_bias (dim)] is the sum of the rows'
+// entries in row order, then added to the accumulator or, with overwrite,
+// stored in its place.
+__global__ __launch_bounds__(256) void ss_det_param_reduce(const float* __restrict__ par, int rows, int64_t dim,
+                                                           float* __restrict__ dA, float* __restrict__ dD,
+                                                           float* __restrict__ db, int overwrite) {
+    const int64_t n = dim * (kT + 2);
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        float* dst = i < dim * kT ? dA + i : (i < dim * (kT + 1) ? dD + (i - dim * kT) : db + (i - dim * (kT + 1)));
+        if (i >= dim * kT && i < dim * (kT + 1) && !dD) continue;
+        if (i >= dim * (kT + 1) && !db) continue;
+        float s = 0.f;
+        for (int k = 0; k < rows; ++k) s += par[int64_t(k) * n + i];
+        *dst = overwrite ? s : *dst + s;
+    }
 }
 
 // Pass A of the sequence-parallel backward: workgroup (b, seg, 16 channels)
@@ -723,7 +808,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
     const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
-    const int nck_seg = int(p.seqlen / kT) / p.nseg;
+    const int nck_seg = int((p.seqlen + 2 * kT - 1) / (2 * kT)) * 2 / p.nseg;   // padded as in ss_bwd_fast
     const int k0 = seg * nck_seg, k1 = k0 + nck_seg;
 
     const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
@@ -731,20 +816,23 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
     const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
     const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
     constexpr uint32_t es = sizeof(IT);
-    const uint32_t od = uint32_t(row * p.dl_ds + r) * es, oo = uint32_t(row * q.do_ds + r) * es;
-    const uint32_t oz = uint32_t(row * p.z_ds + r) * es, oC = uint32_t(row * p.C_ns + r) * es;
 
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
     const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
 
     struct Ck { float d, o, z, C; };
+    // steps past a ragged sequence's end (the last segment's last chunks) are
+    // identity steps: delta' = 0, dout = 0, C = 0, loads clamped to the end
+    const int64_t L = p.seqlen;
     auto fetch = [&](int ck, Ck& P) {
-        const uint32_t so = uint32_t(ck * kT) * es;
-        P.d = bload<IT>(Rd, od, so);
-        P.o = bload<IT>(Ro, oo, so);
-        P.z = kZ ? bload<IT>(Rz, oz, so) : 0.f;
-        P.C = bload<IT>(RC, oC, so);
+        const int t = ck * kT + r;
+        const bool in = t < L;
+        const int te = in ? t : int(L) - 1;
+        P.d = in ? bload<IT>(Rd, uint32_t(row * p.dl_ds + te) * es, 0) : (softplus ? -INFINITY : -bias);
+        P.o = in ? bload<IT>(Ro, uint32_t(row * q.do_ds + te) * es, 0) : 0.f;
+        P.z = kZ && in ? bload<IT>(Rz, uint32_t(row * p.z_ds + te) * es, 0) : 0.f;
+        P.C = in ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
     };
     auto stage = [&](const Ck& P, int buf) { s_c[buf * 16 * kT + bc_slot(row, r)] = P.C; };
 
@@ -796,7 +884,7 @@ int bwd_segments(const BwdParams& q) {
     if (!bwd_fast_ok(q)) return 1;
     const FwdParams& p = q.f;
     const int64_t wgs = p.batch * (p.dim / kChPerWG);
-    const int64_t nck = p.seqlen / kT;
+    const int64_t nck = (p.seqlen + 2 * kT - 1) / (2 * kT) * 2;   // padded to an even count
     int nseg = 1;
     while (wgs * nseg < 768 && 2 * nseg <= 64 && nck % (4 * nseg) == 0 && nck / (2 * nseg) >= 16) nseg *= 2;
     return nseg;
@@ -806,7 +894,8 @@ bool bwd_fast_ok(const BwdParams& q) {
     const FwdParams& p = q.f;
     // every byte offset the kernel forms stays below 2^32: rows and seqlen
     // below 2^26 elements, and the checkpoint offset (chunk x dim x 64 B)
-    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 2 * kT && p.seqlen % (2 * kT) == 0 &&
+    // (a seqlen that is not a multiple of 32 ends in identity-padded chunks)
+    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 1 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && (!p.has_z || p.y != nullptr) &&
            small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
                           q.do_ds, q.du_ds, q.dd_ds, q.dz_ds}) &&
@@ -842,18 +931,23 @@ __global__ __launch_bounds__(256) void ss_zero_segs(const ZeroSegs z) {
 }
 
 // dB (+)= sum of the dB slices, dC (+)= sum of the dC slices (n4 float4
-// each); `overwrite` ignores what dB / dC held.
+// each), the slices summed in order first; `overwrite` ignores what dB / dC
+// held.
 __global__ __launch_bounds__(256) void ss_ws_reduce(const float4* __restrict__ ws, int slices, int64_t n4,
                                                     float4* __restrict__ dB, float4* __restrict__ dC,
                                                     int overwrite) {
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        float4 sb = overwrite ? make_float4(0.f, 0.f, 0.f, 0.f) : dB[i];
-        float4 sc = overwrite ? make_float4(0.f, 0.f, 0.f, 0.f) : dC[i];
-        for (int k = 0; k < slices; ++k) {
+        float4 sb = ws[i], sc = ws[n4 + i];
+        for (int k = 1; k < slices; ++k) {
             const float4 vb = ws[(2 * k) * n4 + i], vc = ws[(2 * k + 1) * n4 + i];
             sb.x += vb.x; sb.y += vb.y; sb.z += vb.z; sb.w += vb.w;
             sc.x += vc.x; sc.y += vc.y; sc.z += vc.z; sc.w += vc.w;
+        }
+        if (!overwrite) {
+            const float4 ob = dB[i], oc = dC[i];
+            sb.x += ob.x; sb.y += ob.y; sb.z += ob.z; sb.w += ob.w;
+            sc.x += oc.x; sc.y += oc.y; sc.z += oc.z; sc.w += oc.w;
         }
         dB[i] = sb;
         dC[i] = sc;
@@ -872,8 +966,10 @@ static hipError_t launch_zero(const BwdParams& p, bool sliced, hipStream_t strea
         ++z.count;
         most = n > most ? n : most;
     };
-    if (sliced) add(p.ws, 2 * p.ws_slices * p.ws_stride);
-    if (p.zero_grads) {
+    // deterministic sums: every slice element is written, and the fixed-order
+    // passes overwrite (zero_grads) or add to the accumulators themselves
+    if (sliced && !p.det) add(p.ws, 2 * p.ws_slices * p.ws_stride);
+    if (p.zero_grads && !p.det) {
         add(p.dA, p.dA_n);
         add(p.dD, p.dD_n);
         add(p.ddelta_bias, p.dD_n);
@@ -893,6 +989,7 @@ hipError_t launch_bwd_zero_only(const BwdParams& p, hipStream_t stream) { return
 
 int bwd_ws_slices(const BwdParams& p) {
     if (!bwd_fast_ok(p)) return 1;
+    if (p.det) return int(p.f.dpg / kChPerWG);   // one slice per channel block of a group
     // at most 96 channel blocks per slice: each workgroup adds once per
     // (state, step) and chunk, so the contention of up to 96 adders per
     // address costs less than clearing and summing more slices (measured on
@@ -924,8 +1021,19 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
             else hipLaunchKernelGGL((ss_bwd_seg_carry<IT, false>), agrid, block, 0, stream, p);
         }
         const dim3 sgrid(unsigned(nblk * p.f.batch * nseg));
-        if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true>), sgrid, block, 0, stream, p);
-        else hipLaunchKernelGGL((ss_bwd_fast<IT, false>), sgrid, block, 0, stream, p);
+        if (p.det) {
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, true>), sgrid, block, 0, stream, p);
+        } else {
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false>), sgrid, block, 0, stream, p);
+        }
+        if (p.det) {
+            const int64_t n = p.f.dim * (kT + 2);
+            const unsigned pgrid = unsigned((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
+            hipLaunchKernelGGL(ss_det_param_reduce, dim3(pgrid), dim3(256), 0, stream, p.det_par,
+                               int(p.f.batch * nseg), p.f.dim, p.dA, p.dD, p.ddelta_bias, int(p.zero_grads));
+        }
         if (sliced) {
             hipLaunchKernelGGL(ss_ws_reduce, dim3(rgrid), dim3(256), 0, stream,
                                reinterpret_cast<const float4*>(p.ws), int(p.ws_slices), n4,

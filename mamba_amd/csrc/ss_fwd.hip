@@ -190,11 +190,17 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
     finish_pending(slot ^ 1);
 }
 
-// Fast path: dstate 16, variable B and C, seqlen a multiple of 64, dim and
-// channels per group multiples of 16, z gate fixed at compile time.  Every
-// step, state and channel is real, so the loop has no branch around a memory
+// Fast path: dstate 16, variable B and C, dim and channels per group
+// multiples of 16, z gate fixed at compile time.  Every step, state and
+// channel of the main loop is real, so it has no branch around a memory
 // access (on gfx950 the compiler waits for every outstanding load at such a
-// branch, which would serialise the prefetch).
+// branch, which would serialise the prefetch).  A seqlen that is not a
+// multiple of 64 ends in a partial super-chunk, the tail, run once after the
+// loop: its loads are clamped to the sequence and zero past it, its steps
+// past the sequence are identity steps (decay 1, input 0, as the reference
+// pads its last chunk: forward_kernel.cu:267-271), and its stores stop at
+// the sequence's end.  Rows that are not 4-element aligned (an odd seqlen,
+// for one) take element accesses in place of the vector ones (kVec false).
 //
 // Global traffic moves in 64-step super-chunks with one barrier each: lane r
 // of a row owns steps 4r..4r+3 of its channel and reads / writes them as one
@@ -230,7 +236,34 @@ __device__ __forceinline__ int bc64_slot(int n, int gi) { return n * kSC + 4 * (
 // reading steps 16q..16q+15 with ds_read_b128 cover all 64 banks once.
 __device__ __forceinline__ int ct_slot4(int t, int i) { return t * 16 + 4 * (i ^ ((t >> 2) & 3)); }
 
-template <typename IT, bool kZ>
+// Four consecutive elements at byte offset voff + soff: one 16-byte (fp32)
+// or 8-byte (16-bit) access when the rows are 4-element aligned (kVec),
+// else four element accesses (rows of any alignment, e.g. an odd seqlen).
+template <typename IT, bool kVec>
+__device__ __forceinline__ float4 load4(rsrc_t r, uint32_t voff, uint32_t soff) {
+    if constexpr (kVec) {
+        return bload4<IT>(r, voff, soff);
+    } else {
+        constexpr uint32_t es = sizeof(IT);
+        return make_float4(bload<IT>(r, voff, soff), bload<IT>(r, voff + es, soff),
+                           bload<IT>(r, voff + 2 * es, soff), bload<IT>(r, voff + 3 * es, soff));
+    }
+}
+template <typename IT, bool kVec>
+__device__ __forceinline__ void store4(rsrc_t r, uint32_t voff, float4 v) {
+    if constexpr (kVec) {
+        bstore4<IT>(r, voff, v);
+    } else {
+        constexpr uint32_t es = sizeof(IT);
+        bstore<IT>(r, voff, 0, v.x);
+        bstore<IT>(r, voff + es, 0, v.y);
+        bstore<IT>(r, voff + 2 * es, 0, v.z);
+        bstore<IT>(r, voff + 3 * es, 0, v.w);
+    }
+}
+
+// kVec: every row of the streams 4-element aligned (vector accesses).
+template <typename IT, bool kZ, bool kVec>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B [n][64 steps], C [64 steps][n]]
     __shared__ __attribute__((aligned(16))) float s_yp[kWaves * kRows * kYRow];    // [wave][row][n][16 steps]
@@ -253,8 +286,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
-    const int nsc_seg = int(p.seqlen / kSC) / nseg;   // super-chunks per segment (below 2^20)
+    // super-chunks, the last one partial when seqlen is not a multiple of 64
+    // (below 2^20); the last segment ends with that partial one, the tail
+    const int nsc_pad = int((p.seqlen + kSC - 1) / kSC);
+    const int nsc_seg = nsc_pad / nseg;
     const int sc0 = seg * nsc_seg, sc1 = sc0 + nsc_seg;
+    const int lt = int(p.seqlen - int64_t(nsc_pad - 1) * kSC);   // steps of the last super-chunk, 1..64
+    const bool tail = seg == nseg - 1 && lt < kSC;
+    const int scf = tail ? sc1 - 1 : sc1;                       // end of the full super-chunks
 
     // buffer resources at the workgroup's rows; lane (row, r) owns steps
     // 4r..4r+3 of channel c0 + row and, for the B / C staging, of state row
@@ -280,6 +319,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const uint32_t oo = uint32_t(row * p.o_ds + 4 * r) * es, oy = uint32_t(row * p.y_ds + 4 * r) * es;
     const uint32_t ox = uint32_t(row * kT + r) * 4u;
     const uint32_t x_chunk_bytes = uint32_t(p.dim * kT * 4);
+    // the tail's checkpoints: a resource that ends with this batch row's
+    // n_chunks chunks, so the stores of chunks past the sequence are dropped
+    const rsrc_t Rx_tail = make_rsrc_n(save_x ? p.x + (b * p.n_chunks * p.dim + c0) * kT : nullptr,
+                                       p.x_records == 0 ? 0 : int(uint32_t((p.n_chunks * p.dim - c0) * kT * 4)));
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -289,11 +332,34 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     struct Super { float4 u, d, z, B, C; };
     auto fetch = [&](int sc, Super& S) {       // 0 <= sc < nsc
         const uint32_t so = uint32_t(sc * kSC) * es;
-        S.u = bload4<IT>(Ru, ou, so);
-        S.d = bload4<IT>(Rd, od, so);
-        S.z = kZ ? bload4<IT>(Rz, oz, so) : make_float4(0.f, 0.f, 0.f, 0.f);
-        S.B = bload4<IT>(RB, oB, so);
-        S.C = bload4<IT>(RC, oC, so);
+        S.u = load4<IT, kVec>(Ru, ou, so);
+        S.d = load4<IT, kVec>(Rd, od, so);
+        S.z = kZ ? load4<IT, kVec>(Rz, oz, so) : make_float4(0.f, 0.f, 0.f, 0.f);
+        S.B = load4<IT, kVec>(RB, oB, so);
+        S.C = load4<IT, kVec>(RC, oC, so);
+    };
+    // the tail super-chunk sc: element loads at offsets clamped to its lt
+    // steps, zero past them
+    auto fetch_tail = [&](int sc, Super& S) {
+        const uint32_t so = uint32_t(sc * kSC) * es;
+        float v[5][4];
+        const int64_t rs[5] = {row * p.u_ds, row * p.dl_ds, row * p.z_ds, row * p.B_ns, row * p.C_ns};
+        const rsrc_t R[5] = {Ru, Rd, Rz, RB, RC};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 4 * r + i;
+            const int tc = t < lt ? t : lt - 1;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) {
+                const float x = (k == 2 && !kZ) ? 0.f : bload<IT>(R[k], uint32_t(rs[k] + tc) * es, so);
+                v[k][i] = t < lt ? x : 0.f;
+            }
+        }
+        S.u = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
+        S.d = make_float4(v[1][0], v[1][1], v[1][2], v[1][3]);
+        S.z = make_float4(v[2][0], v[2][1], v[2][2], v[2][3]);
+        S.B = make_float4(v[3][0], v[3][1], v[3][2], v[3][3]);
+        S.C = make_float4(v[4][0], v[4][1], v[4][2], v[4][3]);
     };
     auto stage = [&](const Super& S, int buf) {
         *reinterpret_cast<float4*>(s_bc + (buf * 2 + 0) * 16 * kSC + bc64_slot(row, r)) = S.B;
@@ -331,13 +397,35 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
         if constexpr (kZ) {
-            bstore4<IT>(make_rsrc_n(gy + int64_t(sc) * kSC, y_records), oy, y);
+            store4<IT, kVec>(make_rsrc_n(gy + int64_t(sc) * kSC, y_records), oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);
             y.w *= pz.w * sigmoidf_(pz.w);
         }
-        bstore4<IT>(make_rsrc(go + int64_t(sc) * kSC), oo, y);
+        store4<IT, kVec>(make_rsrc(go + int64_t(sc) * kSC), oo, y);
+    };
+    // as finish_super for the tail super-chunk: element stores of its lt steps
+    auto finish_super_tail = [&](int sc) {
+        float4 y = *reinterpret_cast<const float4*>(yo + 4 * r);
+        y.x = __builtin_fmaf(Dv, pu.x, y.x);
+        y.y = __builtin_fmaf(Dv, pu.y, y.y);
+        y.z = __builtin_fmaf(Dv, pu.z, y.z);
+        y.w = __builtin_fmaf(Dv, pu.w, y.w);
+        float yv[4] = {y.x, y.y, y.z, y.w}, zv[4] = {pz.x, pz.y, pz.z, pz.w};
+        const rsrc_t Ro = make_rsrc(go + int64_t(sc) * kSC);
+        const rsrc_t Ryt = make_rsrc_n(gy + int64_t(sc) * kSC, y_records);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (4 * r + i < lt) {
+                float o = yv[i];
+                if constexpr (kZ) {
+                    bstore<IT>(Ryt, oy + uint32_t(i) * es, 0, o);
+                    o *= zv[i] * sigmoidf_(zv[i]);
+                }
+                bstore<IT>(Ro, oo + uint32_t(i) * es, 0, o);
+            }
+        }
     };
     // y_t = sum over states of C h for the chunk whose states are in the
     // tile: lane r reads step r's 16 states, and multiplies them by that
@@ -360,13 +448,16 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     for (int n = 0; n < kT; ++n) cT[n] = 0.f;
 
     Super S;
-    fetch(sc0, S);
-    stage(S, 0);
-    for (int sc = sc0; sc < sc1; ++sc) {
+    // one super-chunk: the full ones prefetch the next and stage its B / C
+    // tile; the tail (TAIL) zeroes the decay exponents and inputs of the steps
+    // past the sequence (identity steps: a = 1, b = 0) and drops the
+    // checkpoints of chunks past it
+    auto super_chunk = [&](int sc, auto TAIL) {
+        constexpr bool kTail = decltype(TAIL)::value;
         const int buf = (sc - sc0) & 1;
         lds_barrier();   // B / C tile of sc staged
         const float4 cu = S.u, cd = S.d, cz = S.z;
-        fetch(sc + 1 < sc1 ? sc + 1 : sc1 - 1, S);
+        if constexpr (!kTail) fetch(sc + 1 < scf ? sc + 1 : scf - 1, S);
 
         float4 dt, dtu;
         {
@@ -374,6 +465,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             dt = softplus ? make_float4(softplus20(p0), softplus20(p1), softplus20(p2), softplus20(p3))
                           : make_float4(p0, p1, p2, p3);
             dtu = make_float4(dt.x * cu.x, dt.y * cu.y, dt.z * cu.z, dt.w * cu.w);
+            if constexpr (kTail) {
+                dt.x = 4 * r + 0 < lt ? dt.x : 0.f;
+                dt.y = 4 * r + 1 < lt ? dt.y : 0.f;
+                dt.z = 4 * r + 2 < lt ? dt.z : 0.f;
+                dt.w = 4 * r + 3 < lt ? dt.w : 0.f;
+            }
         }
         dpp_sources_ready4(dt, dtu);
         const float* sB = s_bc + (buf * 2 + 0) * 16 * kSC;
@@ -402,7 +499,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             // the previous chunk's sums (chunk 4 sc + q - 1) into the regroup area
             yo[((q + kQ - 1) % kQ) * kT + r] = dot16(ys, cT);
             if constexpr (q == 0) {
-                finish_super(sc > sc0 ? sc - 1 : sc0);   // (at sc0 a placeholder, rewritten later)
+                if constexpr (kTail) {
+                    if (sc > sc0) finish_super(sc - 1);
+                } else {
+                    finish_super(sc > sc0 ? sc - 1 : sc0);   // (at sc0 a placeholder, rewritten later)
+                }
                 pu = cu;     // this super-chunk's u, z wait for its outputs
                 pz = cz;
             }
@@ -412,7 +513,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                 h = __builtin_fmaf(a[k], h, bmul<4 * q + k / 4>(f4get(dtu, k % 4), Bq[k]));
                 yp[k] = h;
             });
-            bstore<float>(Rx, ox, uint32_t(kQ * sc + q) * x_chunk_bytes, h);
+            bstore<float>(kTail ? Rx_tail : Rx, ox, uint32_t(kQ * sc + q) * x_chunk_bytes, h);
 #pragma unroll
             for (int m = 0; m < 4; ++m)
                 *reinterpret_cast<float4*>(yrow + r * 16 + 4 * (m ^ ((r >> 1) & 3))) =
@@ -426,14 +527,25 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             }
         });
         // B / C tile of the next super-chunk into the other buffer
-        stage(S, buf ^ 1);
+        if constexpr (!kTail) stage(S, buf ^ 1);
+    };
+    if (scf > sc0) {
+        fetch(sc0, S);
+        stage(S, 0);
+    }
+    for (int sc = sc0; sc < scf; ++sc) super_chunk(sc, std::false_type{});
+    if (tail) {
+        fetch_tail(scf, S);
+        stage(S, (scf - sc0) & 1);
+        super_chunk(scf, std::true_type{});
     }
     // the last chunk's sums, then the last super-chunk's outputs
     {
         float ys[kT];
         read_tile(ys);
         yo[(kQ - 1) * kT + r] = dot16(ys, cT);
-        finish_super(sc1 - 1);
+        if (tail) finish_super_tail(sc1 - 1);
+        else finish_super(sc1 - 1);
     }
     if (p.last_state && seg == nseg - 1) p.last_state[(b * p.dim + c) * kT + r] = h;
 }
@@ -444,7 +556,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 // arithmetic, but only the state recurrence (no C, no outputs), and writes
 // the state after the segment's last step to seg_h and the segment's sum of
 // delta' to seg_s.  About three fifths of a full scan's work per step.
-template <typename IT>
+template <typename IT, bool kVec>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_b[2 * 16 * kSC];               // [buf][n][64 steps]
 
@@ -463,7 +575,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
-    const int nsc_seg = int(p.seqlen / kSC) / p.nseg;
+    // segments 0 .. nseg - 2 only: whole super-chunks (the tail ends the last)
+    const int nsc_seg = int((p.seqlen + kSC - 1) / kSC) / p.nseg;
     const int sc0 = seg * nsc_seg, sc1 = sc0 + nsc_seg;
 
     const rsrc_t Ru = make_rsrc(static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds);
@@ -480,9 +593,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     struct Seg { float4 u, d, B; };
     auto fetch = [&](int sc, Seg& S) {
         const uint32_t so = uint32_t(sc * kSC) * es;
-        S.u = bload4<IT>(Ru, ou, so);
-        S.d = bload4<IT>(Rd, od, so);
-        S.B = bload4<IT>(RB, oB, so);
+        S.u = load4<IT, kVec>(Ru, ou, so);
+        S.d = load4<IT, kVec>(Rd, od, so);
+        S.B = load4<IT, kVec>(RB, oB, so);
     };
     auto stage = [&](const Seg& S, int buf) {
         *reinterpret_cast<float4*>(s_b + buf * 16 * kSC + bc64_slot(row, r)) = S.B;
@@ -544,7 +657,7 @@ constexpr int kSegMax = 64;
 int fwd_segments(const FwdParams& p) {
     if (!fwd_fast_ok(p)) return 1;
     const int64_t wgs = p.batch * (p.dim / kChPerWG);
-    const int64_t nsc = p.seqlen / kSC;
+    const int64_t nsc = (p.seqlen + kSC - 1) / kSC;     // the last one partial for a ragged seqlen
     int nseg = 1;
     while (wgs * nseg < kSegTargetWGs && 2 * nseg <= kSegMax && nsc % (2 * nseg) == 0 &&
            nsc / (2 * nseg) >= kSegMinSC)
@@ -555,8 +668,9 @@ int fwd_segments(const FwdParams& p) {
 bool fwd_fast_ok(const FwdParams& p) {
     // every byte offset the kernel forms stays below 2^32: rows and seqlen
     // below 2^26 elements, and the checkpoint offset (chunk x dim x 64 B)
-    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= kSC && p.seqlen % kSC == 0 &&
-           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && p.stream_vec &&
+    // (a seqlen that is not a multiple of 64 ends in a partial super-chunk)
+    return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 1 &&
+           p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 &&
            small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns}) &&
            p.seqlen * p.dim < (int64_t(1) << 30);
 }
@@ -570,15 +684,22 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
     const bool vbc = p.var_B && p.var_C;
     if (fwd_fast_ok(p)) {
         const int nseg = p.nseg > 1 ? p.nseg : 1;
+        const bool vec = p.stream_vec != 0;
         if (nseg > 1) {
-            hipLaunchKernelGGL((ss_fwd_seg_state<IT>), dim3(unsigned(nblk * p.batch * (nseg - 1))), block, 0,
-                               stream, p);
+            const dim3 agrid(unsigned(nblk * p.batch * (nseg - 1)));
+            if (vec) hipLaunchKernelGGL((ss_fwd_seg_state<IT, true>), agrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_fwd_seg_state<IT, false>), agrid, block, 0, stream, p);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
         const dim3 sgrid(unsigned(nblk * p.batch * nseg));
-        if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true>), sgrid, block, 0, stream, p);
-        else hipLaunchKernelGGL((ss_fwd_fast<IT, false>), sgrid, block, 0, stream, p);
+        if (vec) {
+            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, true>), sgrid, block, 0, stream, p);
+        } else {
+            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, false>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, false>), sgrid, block, 0, stream, p);
+        }
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, false>), grid, block, 0, stream, p);

@@ -62,10 +62,21 @@ struct BwdParams {
     // of each; dB / dC are overwritten by the slice sum when ws is used)
     int32_t zero_grads;
     int64_t dA_n, dB_n, dC_n, dD_n;
+    // deterministic sums (fast kernels only): every channel block writes its
+    // dB / dC partials into a slice of ws of its own (one slice per channel
+    // block of a group, plain stores), and every (batch row, segment)
+    // workgroup its dA, dD and ddelta_bias partials into det_par
+    // ((batch * nseg) rows of dim * dstate + 2 * dim floats); fixed-order
+    // passes sum both, so the results are the same bits on every run
+    int32_t det;
+    float* det_par;
 };
 
-// dB / dC slices the fast backward uses for p (1: add into dB / dC directly)
+// dB / dC slices the fast backward uses for p (1: add into dB / dC directly;
+// with p.det one per channel block of a group)
 int bwd_ws_slices(const BwdParams& p);
+// the fast backward applies to p (deterministic sums need it)
+bool bwd_fast_ok(const BwdParams& p);
 // sequence segments the fast backward uses for p (1: serial); its pass A
 // writes each segment's adjoint carry to f.seg_h and its sum of delta' to
 // f.seg_s (the forward's layout and sizes, fwd_seg_bytes)

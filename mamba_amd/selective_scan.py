@@ -268,20 +268,40 @@ def _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus
 
 
 def workspace_bytes(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
-                    du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None):
+                    du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None, deterministic=None):
     """Bytes of scratch ``backward_into`` can use for these tensors (0: none)."""
     lib = nat.load()
     b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                        du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
+    _set_deterministic(lib, b, deterministic)
     n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))
     if n < 0:
         nat.check(nat.SS_ERR_INVALID, "selective_scan.workspace_bytes")
     return int(n)
 
 
+def _set_deterministic(lib, b, flag):
+    """Sets b.deterministic: the flag, or with None torch.use_deterministic_algorithms.
+    An explicit request the kernels cannot honour raises (from the library);
+    one that comes from torch's setting raises as torch's own ops do, or
+    warns and runs with atomic sums under warn_only."""
+    if flag is not None:
+        b.deterministic = int(bool(flag))
+        return
+    b.deterministic = int(torch.are_deterministic_algorithms_enabled())
+    if b.deterministic and lib.ss_bwd_workspace_bytes(ctypes.byref(b)) < 0:
+        msg = ("selective_scan.backward has no deterministic implementation for these arguments: "
+               + lib.ss_last_error().decode())
+        if not torch.is_deterministic_algorithms_warn_only_enabled():
+            raise RuntimeError(msg)
+        import warnings
+        warnings.warn(msg)
+        b.deterministic = 0
+
+
 def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                   du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None, workspace="auto",
-                  zero_grads=False):
+                  zero_grads=False, deterministic=None):
     """Backward into caller-allocated gradients.  du, ddelta (and dz) are
     overwritten; dA, dB, dC, dD, ddelta_bias are fp32 and accumulated into,
     or, with ``zero_grads``, cleared by the library first (their contents on
@@ -290,10 +310,15 @@ def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
     ``workspace``: "auto" allocates the scratch the library asks for (see
     ``workspace_bytes``) from torch's caching allocator; a uint8 / any CUDA
     tensor is used as given; None runs without one (same results).
+
+    ``deterministic``: sum dB, dC, dA, dD and ddelta_bias in a fixed order
+    (the same bits on every run; needs the fast kernels and a workspace);
+    None follows ``torch.use_deterministic_algorithms``.
     """
     lib = nat.load()
     b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                        du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
+    _set_deterministic(lib, b, deterministic)
     if isinstance(workspace, str):
         _require(workspace == "auto", f"workspace must be 'auto', None or a tensor, got {workspace!r}")
         n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))
@@ -312,13 +337,14 @@ def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
 
 def prepare_backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                      du, ddelta, dA, dB, dC, dD, ddelta_bias, *, z=None, y=None, dz=None, workspace="auto",
-                     zero_grads=False):
+                     zero_grads=False, deterministic=None):
     """``backward_into`` validated once, as a callable that relaunches it on
     the stream that is current now (see ``prepare_forward``); the workspace,
     if any, is allocated here and kept by the callable."""
     lib = nat.load()
     b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                        du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
+    _set_deterministic(lib, b, deterministic)
     if isinstance(workspace, str):
         _require(workspace == "auto", f"workspace must be 'auto', None or a tensor, got {workspace!r}")
         n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))

@@ -60,7 +60,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 11
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 12
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -361,12 +361,15 @@ def test_kernel_name_query(nat, lib):
     def bname(b):
         r = lib.ss_bwd_kernel_name(ctypes.byref(b))
         return None if r is None else r.decode()
-    # dstate 16, variable B / C, seqlen a multiple of 64, 16-channel groups: cooperative fast paths
+    # dstate 16, variable B / C, 16-channel groups: cooperative fast paths, at
+    # any seqlen (a ragged one ends in a partial tile of identity steps)
     assert fname(valid_fwd(nat, seqlen=128)) == "ss_fwd_fast"
     assert bname(valid_bwd(nat, seqlen=128)) == "ss_bwd_fast"
-    # a ragged length or another dstate takes the general kernels
-    assert fname(valid_fwd(nat, seqlen=100)) == "ss_fwd_kernel"
-    assert bname(valid_bwd(nat, seqlen=100)) == "ss_bwd_kernel"
+    assert fname(valid_fwd(nat, seqlen=100)) == "ss_fwd_fast"
+    assert fname(valid_fwd(nat, seqlen=7)) == "ss_fwd_fast"
+    assert bname(valid_bwd(nat, seqlen=100)) == "ss_bwd_fast"
+    assert bname(valid_bwd(nat, seqlen=1)) == "ss_bwd_fast"
+    # another dstate, or constant B / C, takes the general kernels
     assert fname(valid_fwd(nat, seqlen=128, dstate=32)) == "ss_fwd_kernel"
     # no work, and invalid arguments
     assert fname(valid_fwd(nat, batch=0)) == ""
@@ -384,8 +387,8 @@ def test_workspace_query(nat, lib):
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, batch=2, dim=1536, seqlen=128))) == 0
     b = valid_bwd(nat, batch=2, dim=3072, seqlen=128)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 2 * (2 * 16 * 128) * 4
-    # the general kernel (ragged length) uses none; invalid arguments give -1
-    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, dim=1536, seqlen=100))) == 0
+    # the general kernel (dstate 32) uses none; invalid arguments give -1
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, dim=1536, seqlen=100, dstate=32))) == 0
     bad = valid_bwd(nat)
     bad.dout = None
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(bad)) == -1
@@ -521,3 +524,24 @@ def test_noalloc_entry_checks_before_device_work(nat, lib):
     assert lib.ss_bwd_noalloc(ctypes.byref(big), None) == nat.SS_ERR_UNSUPPORTED
     msg = lib.ss_last_error().decode()
     assert str(need) in msg and str(nat.NOALLOC_SCRATCH_BYTES) in msg
+
+
+def test_deterministic_workspace_query(nat, lib):
+    """Deterministic sums: one dB / dC slice per 16-channel block of a group
+    plus the dA / dD / ddelta_bias partials of every (batch row, segment);
+    shapes the fast kernels do not take are refused before any device work."""
+    b = valid_bwd(nat, batch=2, dim=256, seqlen=512)
+    b.deterministic = 1
+    # (32 workgroups: 2 sequence segments, whose carries sit between the two)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == (2 * 16 * (2 * 16 * 512) * 4 + 2 * 2 * 256 * 17 * 4
+                                                          + 2 * 2 * 256 * 18 * 4)
+    # one long sequence: 8 segments, their carries, then 8 rows of partials
+    b = valid_bwd(nat, batch=1, dim=1536, seqlen=32768)
+    b.deterministic = 1
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == (2 * 96 * (16 * 32768) * 4 + 1 * 8 * 1536 * 17 * 4
+                                                          + 1 * 8 * 1536 * 18 * 4)
+    b = valid_bwd(nat, batch=1, dim=32, seqlen=100, dstate=32)     # dstate 32: the general kernel
+    b.deterministic = 1
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == -1
+    assert "deterministic" in lib.ss_last_error().decode()
+    assert lib.ss_bwd_noalloc(ctypes.byref(b), None) == nat.SS_ERR_UNSUPPORTED

@@ -83,9 +83,11 @@ def test_state_update_matches_oracle(case):
 @pytest.mark.parametrize("dt_,rank", [(torch.float32, 48), (torch.bfloat16, 48), (torch.float16, 7)])
 def test_state_update_low_rank_delta(dt_, rank):
     """dt given as (dt_low, dt_weight): the delta projection summed inside the
-    kernel equals the oracle fed dt = dt_low @ dt_weight.T in float64; dt_low
-    is a column slice of a wider row.  Rank 48 takes the 16-byte vector loads,
-    rank 7 the element loads with an unpaired last term."""
+    kernel equals the oracle fed dt = dt_low @ dt_weight.T in float64, rounded
+    to the input type as a dt tensor of that type is (the kernel rounds its
+    fp32 sum the same way); dt_low is a column slice of a wider row.  Rank 48
+    takes the 16-byte vector loads, rank 7 the element loads with an unpaired
+    last term."""
     from mamba_amd.ops.selective_state_update import selective_state_update
     _say(f"state update, low-rank delta, rank {rank} {dt_}")
     gen = torch.Generator().manual_seed(500 + rank)
@@ -102,7 +104,7 @@ def test_state_update_low_rank_delta(dt_, rank):
     xdb_d = xdb.to(DEV)
     out = selective_state_update(st, x.to(DEV), (xdb_d[:, :rank], w.to(DEV)), A.to(DEV), B.to(DEV), C.to(DEV),
                                  D.to(DEV), z=z.to(DEV), dt_bias=bias.to(DEV), dt_softplus=True)
-    dt64 = xdb[:, :rank].double() @ w.double().t()
+    dt64 = (xdb[:, :rank].double() @ w.double().t()).to(dt_).double()
     want_out, want_st = selective_state_update_ref(state0.double(), x.double(), dt64, A.double(), B.double(),
                                                    C.double(), D.double(), z=z.double(), dt_bias=bias.double(),
                                                    dt_softplus=True)

@@ -36,7 +36,7 @@ CASES = [
     (1, 16, 64, 40, torch.float32, 1, True, True, True, True, True, True),      # dstate 64
     (2, 64, 16, 256, torch.bfloat16, 1, True, True, True, True, True, True),    # bf16 I/O
     (1, 32, 16, 70, torch.float16, 1, True, True, True, True, True, True),      # fp16 I/O
-    # fast path: dstate 16, variable B/C, seqlen % 64 == 0, 16-channel groups
+    # fast path: dstate 16, variable B/C, 16-channel groups
     (1, 32, 16, 128, torch.float16, 2, True, True, True, True, True, True),     # fp16, 2 groups
     (2, 48, 16, 192, torch.float32, 1, True, True, False, True, True, True),    # no z, 3 workgroups
     (1, 16, 16, 64, torch.bfloat16, 1, True, True, True, False, False, True),   # one super-tile, no D / bias
@@ -45,6 +45,13 @@ CASES = [
     (1, 3072, 16, 128, torch.float32, 1, True, True, True, True, True, True),   # 192 blocks: 2 slices
     (1, 3200, 16, 64, torch.bfloat16, 2, True, True, True, True, True, True),   # 100 blocks per group: 2 slices
     (2, 512, 16, 256, torch.float32, 1, True, True, True, True, True, True),    # 32 blocks: direct accumulation
+    # ragged lengths on the fast kernels: a partial last tile of identity steps;
+    # odd strides take element accesses, 4-aligned ones vector accesses
+    (2, 64, 16, 1001, torch.bfloat16, 1, True, True, True, True, True, True),   # bf16, odd seqlen
+    (2, 32, 16, 2044, torch.float32, 1, True, True, True, True, True, True),    # 4-aligned rows, 60-step tail
+    (1, 64, 16, 4095, torch.float32, 1, True, True, True, True, True, True),    # sequence segments + tail
+    (1, 32, 16, 40, torch.float32, 2, True, True, True, True, True, True),      # 2 groups, one partial tile
+    (1, 16, 16, 17, torch.float16, 1, True, True, False, True, True, True),     # fp16, no z, 2 chunks
     # chunk-boundary invariance: lengths either side of 128 and 2048 steps
     (1, 16, 16, 127, torch.float32, 1, True, True, True, True, True, True),
     (1, 16, 16, 128, torch.float32, 1, True, True, True, True, True, True),
@@ -157,7 +164,7 @@ def test_fast_path_strided_z_and_last_state():
 
 @pytest.mark.parametrize("shape", [(2, 64, 16, 256, torch.float32), (2, 48, 16, 100, torch.bfloat16),
                                    (1, 32, 4, 70, torch.float32)],
-                         ids=["fast-f32", "general-bf16", "general-n4"])
+                         ids=["fast-f32", "fast-tail-bf16", "general-n4"])
 def test_forward_without_checkpoints(shape):
     """A forward that no backward follows (x, y not given) writes the same out,
     and last_state equals the last checkpoint, on the fast and general kernels."""
@@ -186,7 +193,7 @@ def test_forward_without_checkpoints(shape):
 
 
 SEG_CASES = [(1, 64, 16, 4096, torch.float32), (2, 32, 16, 2048, torch.bfloat16),
-             (1, 1536, 16, 8192, torch.bfloat16)]
+             (1, 1536, 16, 8192, torch.bfloat16), (1, 64, 16, 4093, torch.float32)]
 
 
 @pytest.mark.parametrize("shape", SEG_CASES, ids=[f"b{c[0]}-d{c[1]}-l{c[3]}-{str(c[4]).split('.')[-1]}"
@@ -243,8 +250,9 @@ def test_sequence_parallel_forward_then_backward_matches_oracle():
     assert_close(last.cpu(), rlast, 1e-3, 1e-3, "last_state (forward only)")
 
 
-@pytest.mark.parametrize("shape", [(1, 64, 16, 4096, torch.float32), (1, 1536, 16, 8192, torch.bfloat16)],
-                         ids=["b1-d64-l4096-f32", "b1-d1536-l8192-bf16"])
+@pytest.mark.parametrize("shape", [(1, 64, 16, 4096, torch.float32), (1, 1536, 16, 8192, torch.bfloat16),
+                                   (1, 64, 16, 4093, torch.float32)],
+                         ids=["b1-d64-l4096-f32", "b1-d1536-l8192-bf16", "b1-d64-l4093-f32"])
 def test_sequence_parallel_backward(shape):
     """Small batches: the backward's segments (adjoint carries scanned in parallel
     and joined) give the serial backward's gradients (to rounding)."""

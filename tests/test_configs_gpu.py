@@ -3,9 +3,10 @@
 * Block, d_model 1024 (d_inner 2048, dt_rank 64, dstate 16, conv 4), bf16,
   hidden states (8, 2048, 1024) ~ N(0, 1): the fast path's output on batch
   rows 0 and 7 against the float64 oracle of modules/mamba_simple.py:87-151
-  (mamba_simple_ref with the C scan), and the gradients of every parameter
-  and of the input against the reference's own op order
-  (use_fast_path=False) on the same GPU at full size.
+  (mamba_simple_ref with the C scan); at full size, the gradients of every
+  parameter and of the input against float64 autograd of the oracle, held
+  to the accuracy of the reference's own op order (use_fast_path=False)
+  run in bf16 on the same GPU.
 * The same block in fp32 on one sequence (1, 2048, 1024), output and every
   gradient against float64 autograd of the oracle (at batch 1 the scan
   kernels run in sequence segments: 128 channel blocks).
@@ -83,38 +84,51 @@ def test_block_d1024_b8_l2048_bf16_forward_vs_oracle():
         assert_close(out[r:r + 1], want, 2e-2, 5e-3, f"block output row {r}")
 
 
-def test_block_d1024_b8_l2048_bf16_gradients_vs_reference_order():
-    """Every gradient of the fused path against the reference's op sequence
-    (PyTorch ops around SelectiveScanFn), same module, inputs and dout.
-    Both are bf16 paths, each within about 1e-3 of float64 on the output
-    (previous test), so they differ by up to twice that: output floor 5e-3
-    as against the oracle.  Gradients: floor 5e-2 x the rms of the tensor,
-    and the rms of the difference within 2e-2 of the tensor's rms."""
-    _say("block d_model 1024, (8, 2048) bf16: fast path vs reference op order, all gradients")
+@pytest.mark.timeout(900)
+def test_block_d1024_b8_l2048_bf16_gradients_vs_oracle_and_reference_order():
+    """Every gradient of the fused path, at full size, against float64
+    autograd of the oracle, held to the accuracy of the reference's own op
+    sequence (PyTorch ops around SelectiveScanFn) run in bf16 on the same
+    GPU with the same module, inputs and dout: for each tensor, the rms of
+    the fused path's error at most twice the reference order's, and every
+    element within 2e-2 |want| + twice the reference order's largest error.
+    (Gradients of parameters are sums over 16384 positions of bf16
+    products; their small elements carry errors set by the size of the
+    summands, not by their own size, so a floor from the reference path's
+    own error is the fair yardstick.)"""
+    _say("block d_model 1024, (8, 2048) bf16: gradients vs float64 oracle, held to the reference op order's error")
     m = _block(torch.bfloat16, 43)
     g = torch.Generator().manual_seed(44)
-    hidden = torch.randn(8, 2048, 1024, generator=g).to(torch.bfloat16).to(DEV)
-    dout = torch.randn(8, 2048, 1024, generator=g).to(torch.bfloat16).to(DEV)
+    hidden = torch.randn(8, 2048, 1024, generator=g).to(torch.bfloat16)
+    dout = torch.randn(8, 2048, 1024, generator=g).to(torch.bfloat16)
     params = dict(m.named_parameters())
+    names = ["hidden"] + list(params)
     results = []
     for fast in (True, False):
         m.use_fast_path = fast
-        x = hidden.clone().requires_grad_(True)
+        x = hidden.to(DEV).requires_grad_(True)
         out = m(x)
-        grads = torch.autograd.grad(out, [x] + list(params.values()), dout)
-        results.append((out.detach(), dict(zip(["hidden"] + list(params), grads))))
+        grads = torch.autograd.grad(out, [x] + list(params.values()), dout.to(DEV))
+        results.append((out.detach().float().cpu(), {k: v.float().cpu() for k, v in zip(names, grads)}))
     torch.cuda.synchronize()
     (out_f, g_f), (out_r, g_r) = results
-    _say(f"output: worst ratio {_worst(out_f.float(), out_r.float(), 2e-2, 5e-3):.3f}")
-    for k in g_r:
-        want, got = g_r[k].float(), g_f[k].float()
-        _say(f"d{k}: rms {_rms(want):.3g}, err rms / rms {_rms(got - want) / _rms(want):.4f}, "
-             f"worst ratio {_worst(got, want, 2e-2, 5e-2 * _rms(want)):.3f}")
-    assert_close(out_f.float(), out_r.float(), 2e-2, 5e-3, "output")
-    for k in g_r:
-        want, got = g_r[k].float(), g_f[k].float()
-        assert _rms(got - want) <= 2e-2 * _rms(want), f"grad {k}: rms of the difference"
-        assert_close(got, want, 2e-2, 5e-2 * _rms(want), f"grad {k}")
+    sd = {k: v.requires_grad_(True) for k, v in _sd64(m).items()}
+    xr = hidden.double().requires_grad_(True)
+    want_out = mamba_simple_ref(sd, xr, scan=c_oracle.scan)
+    want_out.backward(dout.double())
+    want = {"hidden": xr.grad, **{k: sd[k].grad for k in params}}
+    assert_close(out_f, want_out.detach(), 2e-2, 5e-3, "output")
+    failures = []
+    for k in names:
+        ef, er = (g_f[k].double() - want[k]).abs(), (g_r[k].double() - want[k]).abs()
+        rf, rr = _rms(ef), _rms(er)
+        bound = 2e-2 * want[k].abs() + 2 * float(er.max())
+        ratio = float((ef / bound).max())
+        _say(f"d{k}: rms {_rms(want[k]):.3g}; err rms fused {rf:.3g}, reference order {rr:.3g}; "
+             f"worst element / bound {ratio:.3f}")
+        if rf > 2 * rr or ratio > 1:
+            failures.append(k)
+    assert not failures, f"gradients less accurate than the reference op order: {failures}"
 
 
 def test_block_d1024_b1_l2048_fp32_forward_backward_vs_oracle():

@@ -103,24 +103,9 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.n_chunks = a->n_chunks;
     p.var_B = a->is_var_B != 0; p.var_C = a->is_var_C != 0;
     p.has_z = a->has_z != 0; p.softplus = a->delta_softplus != 0;
+    // 16-byte tile loads of B / C in the general kernels
     p.vec_B = p.var_B && vec_rows(a->B, a->B_batch_stride, a->B_group_stride, a->B_dstate_stride, a->seqlen, es);
     p.vec_C = p.var_C && vec_rows(a->C, a->C_batch_stride, a->C_group_stride, a->C_dstate_stride, a->seqlen, es);
-    // every row of u, delta, z, out, y, B, C starts on a 4-element boundary
-    // (so 4 consecutive steps are one 16-byte fp32 or 8-byte 16-bit access)
-    {
-        const size_t a4 = 4 * es;
-        bool ok = aligned(a->u, a4) && aligned(a->delta, a4) && aligned(a->out, a4) &&  // out may be NULL (backward)
-                  a->u_batch_stride % 4 == 0 && a->u_dim_stride % 4 == 0 &&
-                  a->delta_batch_stride % 4 == 0 && a->delta_dim_stride % 4 == 0 &&
-                  a->out_batch_stride % 4 == 0 && a->out_dim_stride % 4 == 0;
-        if (a->has_z) ok = ok && aligned(a->z, a4) && a->z_batch_stride % 4 == 0 && a->z_dim_stride % 4 == 0 &&
-                           aligned(a->y, a4) && a->y_batch_stride % 4 == 0 && a->y_dim_stride % 4 == 0;
-        if (p.var_B) ok = ok && aligned(a->B, a4) && a->B_batch_stride % 4 == 0 && a->B_group_stride % 4 == 0 &&
-                          a->B_dstate_stride % 4 == 0;
-        if (p.var_C) ok = ok && aligned(a->C, a4) && a->C_batch_stride % 4 == 0 && a->C_group_stride % 4 == 0 &&
-                          a->C_dstate_stride % 4 == 0;
-        p.stream_vec = ok;
-    }
     p.u_bs = a->u_batch_stride; p.u_ds = a->u_dim_stride;
     p.dl_bs = a->delta_batch_stride; p.dl_ds = a->delta_dim_stride;
     p.z_bs = a->z_batch_stride; p.z_ds = a->z_dim_stride;
@@ -185,15 +170,6 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     ss::BwdParams p{};
     p.f = make_fwd_params(&a->f);
     p.wg_reduce = (p.f.dpg % ss::kChPerWG) == 0;
-    {
-        const size_t a4 = 4 * elem_size(a->f.itype);
-        bool ok = aligned(a->dout, a4) && aligned(a->du, a4) && aligned(a->ddelta, a4) &&
-                  a->dout_batch_stride % 4 == 0 && a->dout_dim_stride % 4 == 0 &&
-                  a->du_batch_stride % 4 == 0 && a->du_dim_stride % 4 == 0 &&
-                  a->ddelta_batch_stride % 4 == 0 && a->ddelta_dim_stride % 4 == 0;
-        if (a->f.has_z) ok = ok && aligned(a->dz, a4) && a->dz_batch_stride % 4 == 0 && a->dz_dim_stride % 4 == 0;
-        p.stream_vec_bwd = ok;
-    }
     p.do_bs = a->dout_batch_stride; p.do_ds = a->dout_dim_stride;
     p.du_bs = a->du_batch_stride; p.du_ds = a->du_dim_stride;
     p.dd_bs = a->ddelta_batch_stride; p.dd_ds = a->ddelta_dim_stride;

@@ -199,8 +199,11 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
 // loop: its loads are clamped to the sequence and zero past it, its steps
 // past the sequence are identity steps (decay 1, input 0, as the reference
 // pads its last chunk: forward_kernel.cu:267-271), and its stores stop at
-// the sequence's end.  Rows that are not 4-element aligned (an odd seqlen,
-// for one) take element accesses in place of the vector ones (kVec false).
+// the sequence's end.  The vector accesses need only element alignment:
+// the HSA runtime runs the shader memory pipeline in its unaligned mode (the
+// compiler itself emits 16-byte loads at byte-aligned addresses for this
+// target), so rows at any element offset (an odd seqlen, a sliced view) keep
+// the one-access-per-4-steps streams.
 //
 // Global traffic moves in 64-step super-chunks with one barrier each: lane r
 // of a row owns steps 4r..4r+3 of its channel and reads / writes them as one
@@ -236,34 +239,7 @@ __device__ __forceinline__ int bc64_slot(int n, int gi) { return n * kSC + 4 * (
 // reading steps 16q..16q+15 with ds_read_b128 cover all 64 banks once.
 __device__ __forceinline__ int ct_slot4(int t, int i) { return t * 16 + 4 * (i ^ ((t >> 2) & 3)); }
 
-// Four consecutive elements at byte offset voff + soff: one 16-byte (fp32)
-// or 8-byte (16-bit) access when the rows are 4-element aligned (kVec),
-// else four element accesses (rows of any alignment, e.g. an odd seqlen).
-template <typename IT, bool kVec>
-__device__ __forceinline__ float4 load4(rsrc_t r, uint32_t voff, uint32_t soff) {
-    if constexpr (kVec) {
-        return bload4<IT>(r, voff, soff);
-    } else {
-        constexpr uint32_t es = sizeof(IT);
-        return make_float4(bload<IT>(r, voff, soff), bload<IT>(r, voff + es, soff),
-                           bload<IT>(r, voff + 2 * es, soff), bload<IT>(r, voff + 3 * es, soff));
-    }
-}
-template <typename IT, bool kVec>
-__device__ __forceinline__ void store4(rsrc_t r, uint32_t voff, float4 v) {
-    if constexpr (kVec) {
-        bstore4<IT>(r, voff, v);
-    } else {
-        constexpr uint32_t es = sizeof(IT);
-        bstore<IT>(r, voff, 0, v.x);
-        bstore<IT>(r, voff + es, 0, v.y);
-        bstore<IT>(r, voff + 2 * es, 0, v.z);
-        bstore<IT>(r, voff + 3 * es, 0, v.w);
-    }
-}
-
-// kVec: every row of the streams 4-element aligned (vector accesses).
-template <typename IT, bool kZ, bool kVec>
+template <typename IT, bool kZ>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B [n][64 steps], C [64 steps][n]]
     __shared__ __attribute__((aligned(16))) float s_yp[kWaves * kRows * kYRow];    // [wave][row][n][16 steps]
@@ -332,11 +308,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     struct Super { float4 u, d, z, B, C; };
     auto fetch = [&](int sc, Super& S) {       // 0 <= sc < nsc
         const uint32_t so = uint32_t(sc * kSC) * es;
-        S.u = load4<IT, kVec>(Ru, ou, so);
-        S.d = load4<IT, kVec>(Rd, od, so);
-        S.z = kZ ? load4<IT, kVec>(Rz, oz, so) : make_float4(0.f, 0.f, 0.f, 0.f);
-        S.B = load4<IT, kVec>(RB, oB, so);
-        S.C = load4<IT, kVec>(RC, oC, so);
+        S.u = bload4<IT>(Ru, ou, so);
+        S.d = bload4<IT>(Rd, od, so);
+        S.z = kZ ? bload4<IT>(Rz, oz, so) : make_float4(0.f, 0.f, 0.f, 0.f);
+        S.B = bload4<IT>(RB, oB, so);
+        S.C = bload4<IT>(RC, oC, so);
     };
     // the tail super-chunk sc: element loads at offsets clamped to its lt
     // steps, zero past them
@@ -397,13 +373,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
         if constexpr (kZ) {
-            store4<IT, kVec>(make_rsrc_n(gy + int64_t(sc) * kSC, y_records), oy, y);
+            bstore4<IT>(make_rsrc_n(gy + int64_t(sc) * kSC, y_records), oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);
             y.w *= pz.w * sigmoidf_(pz.w);
         }
-        store4<IT, kVec>(make_rsrc(go + int64_t(sc) * kSC), oo, y);
+        bstore4<IT>(make_rsrc(go + int64_t(sc) * kSC), oo, y);
     };
     // as finish_super for the tail super-chunk: element stores of its lt steps
     auto finish_super_tail = [&](int sc) {
@@ -556,7 +532,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 // arithmetic, but only the state recurrence (no C, no outputs), and writes
 // the state after the segment's last step to seg_h and the segment's sum of
 // delta' to seg_s.  About three fifths of a full scan's work per step.
-template <typename IT, bool kVec>
+template <typename IT>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_b[2 * 16 * kSC];               // [buf][n][64 steps]
 
@@ -593,9 +569,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     struct Seg { float4 u, d, B; };
     auto fetch = [&](int sc, Seg& S) {
         const uint32_t so = uint32_t(sc * kSC) * es;
-        S.u = load4<IT, kVec>(Ru, ou, so);
-        S.d = load4<IT, kVec>(Rd, od, so);
-        S.B = load4<IT, kVec>(RB, oB, so);
+        S.u = bload4<IT>(Ru, ou, so);
+        S.d = bload4<IT>(Rd, od, so);
+        S.B = bload4<IT>(RB, oB, so);
     };
     auto stage = [&](const Seg& S, int buf) {
         *reinterpret_cast<float4*>(s_b + buf * 16 * kSC + bc64_slot(row, r)) = S.B;
@@ -684,22 +660,15 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
     const bool vbc = p.var_B && p.var_C;
     if (fwd_fast_ok(p)) {
         const int nseg = p.nseg > 1 ? p.nseg : 1;
-        const bool vec = p.stream_vec != 0;
         if (nseg > 1) {
             const dim3 agrid(unsigned(nblk * p.batch * (nseg - 1)));
-            if (vec) hipLaunchKernelGGL((ss_fwd_seg_state<IT, true>), agrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_fwd_seg_state<IT, false>), agrid, block, 0, stream, p);
+            hipLaunchKernelGGL((ss_fwd_seg_state<IT>), agrid, block, 0, stream, p);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
         const dim3 sgrid(unsigned(nblk * p.batch * nseg));
-        if (vec) {
-            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, true>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, true>), sgrid, block, 0, stream, p);
-        } else {
-            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, false>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, false>), sgrid, block, 0, stream, p);
-        }
+        if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true>), sgrid, block, 0, stream, p);
+        else hipLaunchKernelGGL((ss_fwd_fast<IT, false>), sgrid, block, 0, stream, p);
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, false>), grid, block, 0, stream, p);

@@ -14,8 +14,7 @@ struct FwdParams {
     int64_t batch, dim, seqlen, dstate, dpg;  // dpg: channels per group
     int64_t n_chunks;
     int32_t var_B, var_C, has_z, softplus;
-    int32_t vec_B, vec_C;                     // 16-byte aligned rows of variable B / C
-    int32_t stream_vec;                       // all (batch, dim) rows 4-element aligned
+    int32_t vec_B, vec_C;                     // 16-byte aligned rows of variable B / C (general kernels)
     int64_t u_bs, u_ds, dl_bs, dl_ds, z_bs, z_ds, o_bs, o_ds, y_bs, y_ds;
     int64_t A_ds, A_ns;
     int64_t B_bs, B_gs, B_ns, C_bs, C_gs, C_ns;
@@ -47,7 +46,6 @@ inline int64_t fwd_seg_bytes(const FwdParams& p, int nseg) {
 struct BwdParams {
     FwdParams f;
     int32_t wg_reduce;                        // all channels of a workgroup share one group
-    int32_t stream_vec_bwd;                   // dout, du, ddelta, dz rows 4-element aligned
     int64_t do_bs, do_ds, du_bs, du_ds, dd_bs, dd_ds, dz_bs, dz_ds;
     const void* dout; void* du; void* ddelta; void* dz;
     float* dA; float* dB; float* dC; float* dD; float* ddelta_bias;

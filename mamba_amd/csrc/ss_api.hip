@@ -170,6 +170,7 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     ss::BwdParams p{};
     p.f = make_fwd_params(&a->f);
     p.wg_reduce = (p.f.dpg % ss::kChPerWG) == 0;
+    p.bc_ld = a->f.seqlen;
     p.do_bs = a->dout_batch_stride; p.do_ds = a->dout_dim_stride;
     p.du_bs = a->du_batch_stride; p.du_ds = a->du_dim_stride;
     p.dd_bs = a->ddelta_batch_stride; p.dd_ds = a->ddelta_dim_stride;
@@ -194,38 +195,39 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
 }
 
 // Workspace layout for p: slices and bytes (0 when the fast backward does
-// not use one: other kernel, one slice, or dB / dC not 16-byte aligned).
+// not use one: other kernel, or one slice over 64-byte aligned dB / dC rows).
 // Backward workspace: the dB / dC slices (when they apply), then the
 // sequence-segment carries (when they apply).  *slice_bytes: the first part.
-// With deterministic sums (p.det, fast kernels only) every channel block of
-// a group has a slice of its own, even a lone one, and the dA / dD /
-// ddelta_bias partials follow the carries: (batch * nseg) rows of dim * 18
-// floats.
+// The slices' rows are padded to ss::bwd_ws_ld(seqlen) floats.  They apply
+// with more than 96 channel blocks per group, with deterministic sums (every
+// channel block of a group has a slice of its own, even a lone one, and the
+// dA / dD / ddelta_bias partials follow the carries: (batch * nseg) rows of
+// dim * 18 floats), and with a seqlen that is not a multiple of 16 (dB / dC
+// rows that do not start on 64-byte boundaries: the 16-step adds of the
+// kernel would straddle cache lines; one slice with aligned rows, summed
+// into dB / dC afterwards, costs less).
 int64_t ws_bytes_for(const ss::BwdParams& p, int* slices, int* nseg, int64_t* slice_bytes) {
     *slices = ss::bwd_ws_slices(p);
     *slice_bytes = 0;
-    const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * p.f.seqlen;
-    if (p.det) {
+    const bool fast = ss::bwd_fast_ok(p);
+    const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * ss::bwd_ws_ld(p.f.seqlen);
+    if (fast && (p.det || *slices > 1 || p.f.seqlen % 16 != 0)) {
         *slice_bytes = int64_t(2) * *slices * stride * int64_t(sizeof(float));
-    } else if (*slices <= 1 || !aligned(p.dB, 16) || !aligned(p.dC, 16)) {
-        *slices = 1;
     } else {
-        *slice_bytes = int64_t(2) * *slices * stride * int64_t(sizeof(float));
+        *slices = 1;
     }
     *nseg = ss::bwd_segments(p);
     const int64_t par = p.det ? p.f.batch * *nseg * p.f.dim * (p.f.dstate + 2) * int64_t(sizeof(float)) : 0;
     return *slice_bytes + ss::fwd_seg_bytes(p.f, *nseg) + par;
 }
 
-// Deterministic sums need the fast kernels and 16-byte aligned dB / dC.
+// Deterministic sums need the fast kernels.
 int check_det(const ss::BwdParams& p) {
     if (!p.det) return SS_OK;
     if (!ss::bwd_fast_ok(p))
         return fail(SS_ERR_UNSUPPORTED,
-                    "deterministic sums need the fast backward (dstate 16, variable B and C, seqlen a multiple "
-                    "of 32, dim and channels per group multiples of 16)");
-    if (!aligned(p.dB, 16) || !aligned(p.dC, 16))
-        return fail(SS_ERR_UNSUPPORTED, "deterministic sums need 16-byte aligned dB and dC");
+                    "deterministic sums need the fast backward (dstate 16, variable B and C, dim and channels "
+                    "per group multiples of 16)");
     return SS_OK;
 }
 
@@ -307,6 +309,7 @@ int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
             p.ws = static_cast<float*>(ws);
             p.ws_slices = slices;
             p.ws_stride = slice_bytes / int64_t(sizeof(float)) / (2 * slices);
+            p.bc_ld = ss::bwd_ws_ld(p.f.seqlen);
         }
         const int64_t seg_bytes = ss::fwd_seg_bytes(p.f, nseg);
         if (nseg > 1) {

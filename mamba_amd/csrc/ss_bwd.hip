@@ -448,9 +448,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
     const rsrc_t Rx = make_rsrc(p.x + (b * p.n_chunks * p.dim + c0) * kT);
     // dB / dC of this batch row and group, or of its slice of the workspace
+    // (rows of ld floats)
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
-    const rsrc_t RdB = make_rsrc((q.ws ? q.ws + 2 * slice * q.ws_stride : q.dB) + (b * G + g) * int64_t(kT) * L);
-    const rsrc_t RdC = make_rsrc((q.ws ? q.ws + (2 * slice + 1) * q.ws_stride : q.dC) + (b * G + g) * int64_t(kT) * L);
+    const int64_t ld = q.bc_ld;
+    const rsrc_t RdB = make_rsrc((q.ws ? q.ws + 2 * slice * q.ws_stride : q.dB) + (b * G + g) * int64_t(kT) * ld);
+    const rsrc_t RdC = make_rsrc((q.ws ? q.ws + (2 * slice + 1) * q.ws_stride : q.dC) + (b * G + g) * int64_t(kT) * ld);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + r) * es, od = uint32_t(row * p.dl_ds + r) * es;
     const uint32_t oo = uint32_t(row * q.do_ds + r) * es;
@@ -530,7 +532,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // dB / dC of chunk ck from wave-partial buffer buf: thread (n, t) sums the
     // 4 waves and adds once into global memory (16 consecutive steps per state)
     const int fn = tid >> 4, ft = tid & 15;
-    const uint32_t ofl0 = uint32_t(fn * L + ft) * 4u;
+    const uint32_t ofl0 = uint32_t(fn * ld + ft) * 4u;
     // split in the LDS reads and the sums + global adds, so that other work
     // can sit between them
     auto flush_read = [&](int buf, float (&v)[2 * kWaves]) {
@@ -540,8 +542,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             v[kWaves + ww] = s_wg[((buf * 2 + 1) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
         }
     };
-    // (TAIL: steps past the sequence, whose sums are zero, are added to its
-    // last step instead, so no address leaves the row)
+    // (TAIL: in rows of seqlen floats, steps past the sequence, whose sums
+    // are zero, are added to its last step instead, so no address leaves the
+    // row; the workspace's padded rows have slots for them)
     auto flush_commit = [&](int ck, const float (&v)[2 * kWaves], auto TAIL) {
         const float sB = (v[0] + v[1]) + (v[2] + v[3]);
         const float sC = (v[4] + v[5]) + (v[6] + v[7]);
@@ -549,7 +552,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         uint32_t ofl = ofl0;
         if constexpr (decltype(TAIL)::value) {
             const int t = ck * kT + ft;
-            if (t >= L) ofl = uint32_t(fn * L + int(L) - 1 - ck * kT) * 4u;
+            if (t >= ld) ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
         }
         if constexpr (kDet) {
             bstore<float>(RdB, ofl, so, sB);
@@ -897,7 +900,7 @@ bool bwd_fast_ok(const BwdParams& q) {
     // (a seqlen that is not a multiple of 32 ends in identity-padded chunks)
     return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 1 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && (!p.has_z || p.y != nullptr) &&
-           small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
+           small_strides({p.seqlen + 2 * kT, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
                           q.do_ds, q.du_ds, q.dd_ds, q.dz_ds}) &&
            p.seqlen * p.dim < (int64_t(1) << 30);
 }
@@ -951,6 +954,31 @@ __global__ __launch_bounds__(256) void ss_ws_reduce(const float4* __restrict__ w
         }
         dB[i] = sb;
         dC[i] = sc;
+    }
+}
+
+// As ss_ws_reduce for slices whose rows are padded to ld floats (or dB / dC
+// not 16-byte aligned): element t < seqlen of row i of dB / dC is the sum of
+// the slices' element i * ld + t, in slice order, then added to what dB / dC
+// held unless overwrite.  A workgroup per row.
+__global__ __launch_bounds__(256) void ss_ws_reduce_rows(const float* __restrict__ ws, int slices, int64_t stride,
+                                                         int64_t rows, int64_t L, int64_t ld, float* __restrict__ dB,
+                                                         float* __restrict__ dC, int overwrite) {
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        for (int64_t t = threadIdx.x; t < L; t += blockDim.x) {
+            const int64_t w = row * ld + t, o = row * L + t;
+            float sb = ws[w], sc = ws[stride + w];
+            for (int k = 1; k < slices; ++k) {
+                sb += ws[2 * k * stride + w];
+                sc += ws[(2 * k + 1) * stride + w];
+            }
+            if (!overwrite) {
+                sb += dB[o];
+                sc += dC[o];
+            }
+            dB[o] = sb;
+            dC[o] = sc;
+        }
     }
 }
 
@@ -1012,7 +1040,11 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     hipError_t e = launch_zero(p, sliced, stream);
     if (e != hipSuccess) return e;
     if (fast) {
-        const int64_t n4 = sliced ? p.ws_stride / 4 : 0;
+        // the slice sum as whole float4 rows: rows of seqlen floats, 16-byte
+        // aligned dB / dC
+        const bool flat = p.bc_ld == p.f.seqlen && (reinterpret_cast<uintptr_t>(p.dB) & 15) == 0 &&
+                          (reinterpret_cast<uintptr_t>(p.dC) & 15) == 0;
+        const int64_t n4 = sliced && flat ? p.ws_stride / 4 : 0;
         const unsigned rgrid = unsigned(n4 > 0 ? (n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048 : 1);
         const int nseg = p.f.nseg > 1 ? p.f.nseg : 1;
         if (nseg > 1) {
@@ -1034,10 +1066,15 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
             hipLaunchKernelGGL(ss_det_param_reduce, dim3(pgrid), dim3(256), 0, stream, p.det_par,
                                int(p.f.batch * nseg), p.f.dim, p.dA, p.dD, p.ddelta_bias, int(p.zero_grads));
         }
-        if (sliced) {
+        if (sliced && flat) {
             hipLaunchKernelGGL(ss_ws_reduce, dim3(rgrid), dim3(256), 0, stream,
                                reinterpret_cast<const float4*>(p.ws), int(p.ws_slices), n4,
                                reinterpret_cast<float4*>(p.dB), reinterpret_cast<float4*>(p.dC),
+                               int(p.zero_grads));
+        } else if (sliced) {
+            const int64_t rows = p.f.batch * (p.f.dim / p.f.dpg) * kT;
+            hipLaunchKernelGGL(ss_ws_reduce_rows, dim3(unsigned(rows < 2048 ? rows : 2048)), dim3(256), 0, stream,
+                               p.ws, int(p.ws_slices), p.ws_stride, rows, p.f.seqlen, p.bc_ld, p.dB, p.dC,
                                int(p.zero_grads));
         }
     } else if (spl <= 1) {

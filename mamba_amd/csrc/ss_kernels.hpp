@@ -56,6 +56,12 @@ struct BwdParams {
     float* ws;
     int32_t ws_slices;
     int64_t ws_stride;
+    // row length (floats) of the dB / dC rows the fast kernel adds into:
+    // seqlen for dB / dC themselves; in the workspace the rows are padded to
+    // whole chunk pairs (a multiple of 32 steps), so that every row starts on
+    // a 128-byte boundary and the steps of the identity-padded tail chunks
+    // have slots of their own
+    int64_t bc_ld;
     // clear dA, dB, dC, dD, ddelta_bias before accumulating (element counts
     // of each; dB / dC are overwritten by the slice sum when ws is used)
     int32_t zero_grads;
@@ -73,6 +79,8 @@ struct BwdParams {
 // dB / dC slices the fast backward uses for p (1: add into dB / dC directly;
 // with p.det one per channel block of a group)
 int bwd_ws_slices(const BwdParams& p);
+// row length of the workspace's dB / dC rows: seqlen rounded up to 32
+inline int64_t bwd_ws_ld(int64_t seqlen) { return (seqlen + 31) / 32 * 32; }
 // the fast backward applies to p (deterministic sums need it)
 bool bwd_fast_ok(const BwdParams& p);
 // sequence segments the fast backward uses for p (1: serial); its pass A

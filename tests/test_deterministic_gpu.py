@@ -60,11 +60,13 @@ def _backward(t, y, xck, det, zero=True, init=None):
 
 
 # (batch, dim, seqlen): serial fast kernel, 2 channel blocks per slice group
-# boundary (192 blocks: 192 slices), one long sequence (8 segments)
-CASES = [(2, 256, 512), (1, 3072, 256), (1, 256, 4096)]
+# boundary (192 blocks: 192 slices), one long sequence (8 segments), ragged
+# seqlens (1001: identity-padded tail chunks in slices with padded rows;
+# 2064: a wholly padded last chunk)
+CASES = [(2, 256, 512), (1, 3072, 256), (1, 256, 4096), (1, 256, 1001), (2, 64, 2064)]
 
 
-@pytest.mark.parametrize("case", CASES, ids=["serial", "many-blocks", "segments"])
+@pytest.mark.parametrize("case", CASES, ids=["serial", "many-blocks", "segments", "ragged-1001", "ragged-2064"])
 def test_deterministic_backward_is_reproducible_and_correct(case):
     from mamba_amd import selective_scan as ss
     batch, dim, L = case

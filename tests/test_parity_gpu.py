@@ -45,10 +45,12 @@ CASES = [
     (1, 3072, 16, 128, torch.float32, 1, True, True, True, True, True, True),   # 192 blocks: 2 slices
     (1, 3200, 16, 64, torch.bfloat16, 2, True, True, True, True, True, True),   # 100 blocks per group: 2 slices
     (2, 512, 16, 256, torch.float32, 1, True, True, True, True, True, True),    # 32 blocks: direct accumulation
-    # ragged lengths on the fast kernels: a partial last tile of identity steps;
-    # odd strides take element accesses, 4-aligned ones vector accesses
+    # ragged lengths on the fast kernels: a partial last tile of identity steps,
+    # row accesses at any element alignment; dB / dC through a slice with
+    # rows padded to 32 steps when seqlen is not a multiple of 16
     (2, 64, 16, 1001, torch.bfloat16, 1, True, True, True, True, True, True),   # bf16, odd seqlen
     (2, 32, 16, 2044, torch.float32, 1, True, True, True, True, True, True),    # 4-aligned rows, 60-step tail
+    (2, 32, 16, 2064, torch.float32, 1, True, True, True, True, True, True),    # last chunk wholly padded, dB direct
     (1, 64, 16, 4095, torch.float32, 1, True, True, True, True, True, True),    # sequence segments + tail
     (1, 32, 16, 40, torch.float32, 2, True, True, True, True, True, True),      # 2 groups, one partial tile
     (1, 16, 16, 17, torch.float16, 1, True, True, False, True, True, True),     # fp16, no z, 2 chunks

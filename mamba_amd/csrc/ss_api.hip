@@ -202,16 +202,18 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
 // with more than 96 channel blocks per group, with deterministic sums (every
 // channel block of a group has a slice of its own, even a lone one, and the
 // dA / dD / ddelta_bias partials follow the carries: (batch * nseg) rows of
-// dim * 18 floats), and with a seqlen that is not a multiple of 16 (dB / dC
-// rows that do not start on 64-byte boundaries: the 16-step adds of the
-// kernel would straddle cache lines; one slice with aligned rows, summed
-// into dB / dC afterwards, costs less).
+// dim * 18 floats), and with a seqlen that is not a multiple of 32: dB / dC
+// rows that do not start on 64-byte boundaries (the 16-step adds of the
+// kernel would straddle cache lines), or a last chunk wholly past the
+// sequence (its zero adds would land on steps that other chunks add to).
+// One slice with aligned, padded rows, summed into dB / dC afterwards,
+// costs less.
 int64_t ws_bytes_for(const ss::BwdParams& p, int* slices, int* nseg, int64_t* slice_bytes) {
     *slices = ss::bwd_ws_slices(p);
     *slice_bytes = 0;
     const bool fast = ss::bwd_fast_ok(p);
     const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * ss::bwd_ws_ld(p.f.seqlen);
-    if (fast && (p.det || *slices > 1 || p.f.seqlen % 16 != 0)) {
+    if (fast && (p.det || *slices > 1 || p.f.seqlen % 32 != 0)) {
         *slice_bytes = int64_t(2) * *slices * stride * int64_t(sizeof(float));
     } else {
         *slices = 1;

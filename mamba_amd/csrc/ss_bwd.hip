@@ -542,17 +542,26 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             v[kWaves + ww] = s_wg[((buf * 2 + 1) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
         }
     };
-    // (TAIL: in rows of seqlen floats, steps past the sequence, whose sums
-    // are zero, are added to its last step instead, so no address leaves the
-    // row; the workspace's padded rows have slots for them)
+    // (TAIL: the workspace's padded rows have slots for the steps past the
+    // sequence.  In rows of seqlen floats, which only a call without
+    // workspace uses for a ragged seqlen, their sums (zero) go to steps inside
+    // it, so no address leaves the row: a chunk wholly past the sequence adds
+    // them onto the previous chunk's 16 steps, one per address (onto one
+    // address, all workgroups' adds of the chunk were serialised in the
+    // atomic unit: seqlen 2064 fp32 took 570 us against 338 us at 2048), a
+    // partial chunk onto the last step.)
     auto flush_commit = [&](int ck, const float (&v)[2 * kWaves], auto TAIL) {
         const float sB = (v[0] + v[1]) + (v[2] + v[3]);
         const float sC = (v[4] + v[5]) + (v[6] + v[7]);
         uint32_t so = uint32_t(ck * kT) * 4u;
         uint32_t ofl = ofl0;
         if constexpr (decltype(TAIL)::value) {
-            const int t = ck * kT + ft;
-            if (t >= ld) ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
+            if (ck * kT >= ld) {
+                so = uint32_t((ck - 1) * kT) * 4u;
+            } else {
+                const int t = ck * kT + ft;
+                if (t >= ld) ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
+            }
         }
         if constexpr (kDet) {
             bstore<float>(RdB, ofl, so, sB);

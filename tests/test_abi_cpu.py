@@ -404,14 +404,14 @@ def test_workspace_query(nat, lib):
     # 3072 channels: 2 slices, then 4 segments (192 blocks -> 768 workgroups)
     b = valid_bwd(nat, batch=1, dim=3072, seqlen=32768)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 2 * (16 * 32768) * 4 + 1 * 4 * 3072 * 17 * 4
-    # a seqlen that is not a multiple of 16: one slice whose rows are padded
-    # to a multiple of 32 steps (1001 -> 1024), even with few channel blocks
-    # (768 workgroups: no sequence segments)
+    # a seqlen that is not a multiple of 32: one slice whose rows are padded
+    # to a multiple of 32 steps (1001 -> 1024, 2064 -> 2080), even with few
+    # channel blocks (768 workgroups: no sequence segments)
     b = valid_bwd(nat, batch=8, dim=1536, seqlen=1001)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 1 * (8 * 16 * 1024) * 4
-    # a multiple of 16 but not of 32 keeps dB / dC (rows 64-byte aligned) ...
-    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, batch=8, dim=1536, seqlen=2064))) == 0
-    # ... and pads the slices' rows when slices are used (2064 -> 2080)
+    b = valid_bwd(nat, batch=8, dim=1536, seqlen=2064)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 1 * (8 * 16 * 2080) * 4
+    # ... and with several slices (2 for 192 channel blocks)
     b = valid_bwd(nat, batch=4, dim=3072, seqlen=2064)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 2 * (4 * 16 * 2080) * 4
 

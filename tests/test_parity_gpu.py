@@ -47,10 +47,10 @@ CASES = [
     (2, 512, 16, 256, torch.float32, 1, True, True, True, True, True, True),    # 32 blocks: direct accumulation
     # ragged lengths on the fast kernels: a partial last tile of identity steps,
     # row accesses at any element alignment; dB / dC through a slice with
-    # rows padded to 32 steps when seqlen is not a multiple of 16
+    # rows padded to 32 steps when seqlen is not a multiple of 32
     (2, 64, 16, 1001, torch.bfloat16, 1, True, True, True, True, True, True),   # bf16, odd seqlen
     (2, 32, 16, 2044, torch.float32, 1, True, True, True, True, True, True),    # 4-aligned rows, 60-step tail
-    (2, 32, 16, 2064, torch.float32, 1, True, True, True, True, True, True),    # last chunk wholly padded, dB direct
+    (2, 32, 16, 2064, torch.float32, 1, True, True, True, True, True, True),    # last chunk wholly padded
     (1, 64, 16, 4095, torch.float32, 1, True, True, True, True, True, True),    # sequence segments + tail
     (1, 32, 16, 40, torch.float32, 2, True, True, True, True, True, True),      # 2 groups, one partial tile
     (1, 16, 16, 17, torch.float16, 1, True, True, False, True, True, True),     # fp16, no z, 2 chunks
@@ -290,12 +290,22 @@ def test_sequence_parallel_backward(shape):
         assert_close(a, b, tol, tol * max(1.0, float(b.abs().max())), name)
 
 
-def test_backward_with_and_without_workspace():
+# (batch, dim, seqlen, workspace bytes): 192 channel blocks (2 slices);
+# ragged seqlens, whose workspace is one slice with rows padded to 32 steps
+# and whose direct accumulation adds the zero sums of the steps past the
+# sequence inside the row (1001: a partial chunk and one wholly past it;
+# 2064: one wholly past it)
+WS_CASES = [(1, 3072, 128, 2 * 2 * (1 * 16 * 128) * 4), (8, 64, 1001, None), (8, 32, 2064, None)]
+
+
+@pytest.mark.parametrize("case", WS_CASES, ids=["slices", "ragged-1001", "ragged-2064"])
+def test_backward_with_and_without_workspace(case):
     """The dB / dC slices (workspace) and direct accumulation give the same gradients."""
     from mamba_amd import selective_scan as ss
-    print("\n[parity] workspace vs direct b1-d3072-n16-l128 fp32", flush=True)
+    batch, dim, L, ws_bytes = case
+    print(f"\n[parity] workspace vs direct b{batch}-d{dim}-n16-l{L} fp32", flush=True)
     dev = torch.device("cuda:0")
-    x = make_inputs(1, 3072, 16, 128, seed=21)   # 192 channel blocks: 2 slices
+    x = make_inputs(batch, dim, 16, L, seed=21)
     t = {k: x[k].to(dev) for k in NAMES}
     dout = x["dout"].to(dev)
     out, xck, y = ss.forward(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], True, z=t["z"])
@@ -306,12 +316,15 @@ def test_backward_with_and_without_workspace():
         dz = torch.empty_like(t["z"])
         args = (t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], dout, xck, True, *g)
         if mode == "auto":
-            assert ss.workspace_bytes(*args, z=t["z"], y=y, dz=dz) == 2 * 2 * (1 * 16 * 128) * 4
+            n = ss.workspace_bytes(*args, z=t["z"], y=y, dz=dz)
+            assert n == ws_bytes if ws_bytes is not None else n >= 2 * batch * 16 * ((L + 31) // 32 * 32) * 4
         ss.backward_into(*args, z=t["z"], y=y, dz=dz, workspace=mode)
         torch.cuda.synchronize()
         res[mode] = [v.cpu() for v in g] + [dz.cpu()]
+    # (the workspace also brings sequence segments at the small shapes, whose
+    # joined carries round differently: the segment tests' tolerance)
     for a, b_, name in zip(res["auto"], res[None], ("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz")):
-        assert_close(a, b_, 1e-5, 1e-5, name)
+        assert_close(a, b_, 1e-4, 1e-4 * max(1.0, float(b_.abs().max())), name)
 
 
 @pytest.mark.parametrize("mode", ["auto", None])

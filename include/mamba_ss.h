@@ -135,12 +135,12 @@ typedef struct ss_bwd_args {
        channels, and dA, dD and ddelta_bias over batch rows and sequence
        segments, in a fixed order instead of by atomic adds, so repeated calls
        on the same inputs give the same bits.  Needs the fast kernels (dstate
-       16, variable B and C, seqlen a multiple of 32, dim and channels per
-       group multiples of 16; SS_ERR_UNSUPPORTED otherwise), 16-byte aligned
-       dB / dC, and a workspace of ss_bwd_workspace_bytes() bytes (one dB /
-       dC partial per 16-channel block: batch * dim / 8 * dstate * seqlen
-       floats).  No counterpart in the reference, whose sums are atomic
-       (backward_kernel.cu:472-475,553-578). */
+       16, variable B and C, dim and channels per group multiples of 16;
+       SS_ERR_UNSUPPORTED otherwise) and a workspace of
+       ss_bwd_workspace_bytes() bytes (one dB / dC partial per 16-channel
+       block: batch * dim / 8 * dstate * seqlen floats, seqlen rounded up to
+       a multiple of 32).  No counterpart in the reference, whose sums are
+       atomic (backward_kernel.cu:472-475,553-578). */
     int32_t deterministic;
 } ss_bwd_args;
 

@@ -409,8 +409,10 @@ __device__ __forceinline__ void bstore(rsrc_t r, uint32_t voff, uint32_t soff, f
         __builtin_amdgcn_raw_buffer_store_b16(h, r, int(voff), int(soff), 0);
     }
 }
-// Four consecutive elements (voff + soff bytes, 4-element aligned) as float4:
-// one 16-byte (fp32) or 8-byte (16-bit types) access per lane.
+// Four consecutive elements (voff + soff bytes, element aligned) as float4:
+// one 16-byte (fp32) or 8-byte (16-bit types) access per lane.  The shader
+// memory pipeline runs in its unaligned mode under the HSA runtime, so the
+// access need not be aligned to its size.
 template <typename T>
 __device__ __forceinline__ float4 bload4(rsrc_t r, uint32_t voff, uint32_t soff) {
     if constexpr (sizeof(T) == 4) {

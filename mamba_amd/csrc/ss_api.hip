@@ -94,6 +94,13 @@ bool vec_rows(const void* base, int64_t bs, int64_t gs, int64_t ns, int64_t L, s
     return aligned(base, 16) && bs % per16 == 0 && gs % per16 == 0 && ns % per16 == 0 && L >= 0;
 }
 
+// Bytes from a (batch, rows, seqlen) array's base to the end of its last
+// element (strides in elements, non-negative); 0 for an absent array.
+int64_t seq_end(const void* ptr, int64_t batch, int64_t rows, int64_t seqlen, int64_t bs, int64_t rs, size_t es) {
+    if (!ptr || batch <= 0 || rows <= 0 || seqlen <= 0) return 0;
+    return ((batch - 1) * bs + (rows - 1) * rs + seqlen) * int64_t(es);
+}
+
 ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     ss::FwdParams p{};
     const size_t es = elem_size(a->itype);
@@ -120,10 +127,18 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.out = a->out; p.x = a->x;
     p.y = a->has_z ? a->y : nullptr;
     p.last_state = a->last_state;
-    p.x_records = p.x ? -1 : 0;
-    p.y_records = p.y ? -1 : 0;
     p.nseg = 1;
     p.y_bs = a->y_batch_stride; p.y_ds = a->y_dim_stride;
+    const int64_t B = a->batch, D = a->dim, L = a->seqlen, G = D / p.dpg, N = a->dstate;
+    p.u_end = seq_end(p.u, B, D, L, p.u_bs, p.u_ds, es);
+    p.dl_end = seq_end(p.delta, B, D, L, p.dl_bs, p.dl_ds, es);
+    p.z_end = seq_end(p.z, B, D, L, p.z_bs, p.z_ds, es);
+    p.o_end = seq_end(p.out, B, D, L, p.o_bs, p.o_ds, es);
+    p.y_end = seq_end(p.y, B, D, L, p.y_bs, p.y_ds, es);
+    // variable B / C: (batch, groups, dstate, seqlen)
+    p.B_end = p.var_B && N > 0 ? seq_end(p.B, B, G, L, p.B_bs, p.B_gs, es) + (N - 1) * p.B_ns * int64_t(es) : 0;
+    p.C_end = p.var_C && N > 0 ? seq_end(p.C, B, G, L, p.C_bs, p.C_gs, es) + (N - 1) * p.C_ns * int64_t(es) : 0;
+    p.x_end = p.x ? B * p.n_chunks * D * N * int64_t(sizeof(float)) : 0;
     return p;
 }
 
@@ -171,6 +186,18 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     p.f = make_fwd_params(&a->f);
     p.wg_reduce = (p.f.dpg % ss::kChPerWG) == 0;
     p.bc_ld = a->f.seqlen;
+    {
+        const size_t es = elem_size(a->f.itype);
+        const int64_t B = a->f.batch, D = a->f.dim, L = a->f.seqlen;
+        p.do_end = seq_end(a->dout, B, D, L, a->dout_batch_stride, a->dout_dim_stride, es);
+        p.du_end = seq_end(a->du, B, D, L, a->du_batch_stride, a->du_dim_stride, es);
+        p.dd_end = seq_end(a->ddelta, B, D, L, a->ddelta_batch_stride, a->ddelta_dim_stride, es);
+        p.dz_end = a->f.has_z ? seq_end(a->dz, B, D, L, a->dz_batch_stride, a->dz_dim_stride, es) : 0;
+        // dB / dC: contiguous fp32 of B's / C's shape
+        const int64_t nbc = B * (D / p.f.dpg) * a->f.dstate * L * int64_t(sizeof(float));
+        p.dB_end = a->dB ? nbc : 0;
+        p.dC_end = a->dC ? nbc : 0;
+    }
     p.do_bs = a->dout_batch_stride; p.do_ds = a->dout_dim_stride;
     p.du_bs = a->du_batch_stride; p.du_ds = a->du_dim_stride;
     p.dd_bs = a->ddelta_batch_stride; p.dd_ds = a->ddelta_dim_stride;
@@ -311,6 +338,7 @@ int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
             p.ws = static_cast<float*>(ws);
             p.ws_slices = slices;
             p.ws_stride = slice_bytes / int64_t(sizeof(float)) / (2 * slices);
+            p.ws_end = slice_bytes;
             p.bc_ld = ss::bwd_ws_ld(p.f.seqlen);
         }
         const int64_t seg_bytes = ss::fwd_seg_bytes(p.f, nseg);

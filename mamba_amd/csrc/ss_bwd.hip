@@ -435,24 +435,28 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // channel c0 + row and, for the B / C staging, step r of state row.  The
     // chunk advance is the uniform offset.  Offsets stay below 2^32 (checked
     // by bwd_fast_ok).
-    const rsrc_t Ru = make_rsrc(static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds);
-    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
-    const rsrc_t Ro = make_rsrc(static_cast<const IT*>(q.dout) + b * q.do_bs + c0 * q.do_ds);
-    const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
-    const rsrc_t Ry = make_rsrc(kZ ? static_cast<const IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : nullptr);
-    const rsrc_t RB = make_rsrc(static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs);
-    const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
-    const rsrc_t Rdu = make_rsrc(static_cast<IT*>(q.du) + b * q.du_bs + c0 * q.du_ds);
-    const rsrc_t Rdd = make_rsrc(static_cast<IT*>(q.ddelta) + b * q.dd_bs + c0 * q.dd_ds);
-    const rsrc_t Rdz = make_rsrc(kZ ? static_cast<IT*>(q.dz) + b * q.dz_bs + c0 * q.dz_ds : nullptr);
+    constexpr int64_t es64 = sizeof(IT);
+    const rsrc_t Ru = make_rsrc_in(p.u, (b * p.u_bs + c0 * p.u_ds) * es64, p.u_end);
+    const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
+    const rsrc_t Ro = make_rsrc_in(q.dout, (b * q.do_bs + c0 * q.do_ds) * es64, q.do_end);
+    const rsrc_t Rz = kZ ? make_rsrc_in(p.z, (b * p.z_bs + c0 * p.z_ds) * es64, p.z_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t Ry = kZ ? make_rsrc_in(p.y, (b * p.y_bs + c0 * p.y_ds) * es64, p.y_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t RB = make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end);
+    const rsrc_t RC = make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end);
+    const rsrc_t Rdu = make_rsrc_in(q.du, (b * q.du_bs + c0 * q.du_ds) * es64, q.du_end);
+    const rsrc_t Rdd = make_rsrc_in(q.ddelta, (b * q.dd_bs + c0 * q.dd_ds) * es64, q.dd_end);
+    const rsrc_t Rdz = kZ ? make_rsrc_in(q.dz, (b * q.dz_bs + c0 * q.dz_ds) * es64, q.dz_end) : make_rsrc_n(nullptr, 0);
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
-    const rsrc_t Rx = make_rsrc(p.x + (b * p.n_chunks * p.dim + c0) * kT);
+    const rsrc_t Rx = make_rsrc_in(p.x, (b * p.n_chunks * p.dim + c0) * kT * 4, p.x_end);
     // dB / dC of this batch row and group, or of its slice of the workspace
     // (rows of ld floats)
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
     const int64_t ld = q.bc_ld;
-    const rsrc_t RdB = make_rsrc((q.ws ? q.ws + 2 * slice * q.ws_stride : q.dB) + (b * G + g) * int64_t(kT) * ld);
-    const rsrc_t RdC = make_rsrc((q.ws ? q.ws + (2 * slice + 1) * q.ws_stride : q.dC) + (b * G + g) * int64_t(kT) * ld);
+    const int64_t bc_off = (b * G + g) * int64_t(kT) * ld * 4;
+    const rsrc_t RdB = q.ws ? make_rsrc_in(q.ws, 2 * slice * q.ws_stride * 4 + bc_off, q.ws_end)
+                            : make_rsrc_in(q.dB, bc_off, q.dB_end);
+    const rsrc_t RdC = q.ws ? make_rsrc_in(q.ws, (2 * slice + 1) * q.ws_stride * 4 + bc_off, q.ws_end)
+                            : make_rsrc_in(q.dC, bc_off, q.dC_end);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + r) * es, od = uint32_t(row * p.dl_ds + r) * es;
     const uint32_t oo = uint32_t(row * q.do_ds + r) * es;
@@ -823,10 +827,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
     const int nck_seg = int((p.seqlen + 2 * kT - 1) / (2 * kT)) * 2 / p.nseg;   // padded as in ss_bwd_fast
     const int k0 = seg * nck_seg, k1 = k0 + nck_seg;
 
-    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
-    const rsrc_t Ro = make_rsrc(static_cast<const IT*>(q.dout) + b * q.do_bs + c0 * q.do_ds);
-    const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
-    const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
+    constexpr int64_t es64 = sizeof(IT);
+    const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
+    const rsrc_t Ro = make_rsrc_in(q.dout, (b * q.do_bs + c0 * q.do_ds) * es64, q.do_end);
+    const rsrc_t Rz = kZ ? make_rsrc_in(p.z, (b * p.z_bs + c0 * p.z_ds) * es64, p.z_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t RC = make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end);
     constexpr uint32_t es = sizeof(IT);
 
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;

@@ -371,8 +371,8 @@ __device__ __forceinline__ SS_GLOBAL T* goff(SS_GLOBAL T* p, uint32_t bytes) {
 // Buffer resources: a workgroup-uniform base held in SGPRs, addressed by a
 // 32-bit per-lane byte offset (VGPR) plus a uniform byte offset (SGPR), so
 // neither the row base nor the chunk advance costs VALU address arithmetic.
-// The range is left unbounded (num_records = 2^32 - 1): the launchers check
-// that every offset a kernel forms stays below 2^32.
+// The launchers check that every offset a kernel forms stays below 2^32, and
+// the scan kernels' resources end with their arrays (make_rsrc_in).
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int kRsrcWord3 = 0x00020000;   // gfx9-family raw buffer, 32-bit data format
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
@@ -386,6 +386,18 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
 // access through the resource a waterfall loop.
 __device__ __forceinline__ rsrc_t make_rsrc_n(const void* base, int nrec) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrec, kRsrcWord3);
+}
+// A resource at byte `off` of an array whose elements end `end` bytes after
+// its base pointer: the hardware's range check drops any access past the
+// array (loads read 0), and every access when `end` is 0 (an absent optional
+// array).  The record count is made wave-uniform so that the resource stays
+// in SGPRs (a per-lane count would make every access a waterfall loop).
+__device__ __forceinline__ rsrc_t make_rsrc_in(const void* array, int64_t off, int64_t end) {
+    const int64_t left = end - off;
+    const uint32_t nrec = left <= 0 ? 0u : (left >= int64_t(0xffffffffu) ? 0xffffffffu : uint32_t(left));
+    const char* base = array ? static_cast<const char*>(array) + off : nullptr;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0,
+                                             __builtin_amdgcn_readfirstlane(int(nrec)), kRsrcWord3);
 }
 // Element (voff + soff bytes) of an IT array as float.
 template <typename T>

@@ -273,21 +273,21 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 
     // buffer resources at the workgroup's rows; lane (row, r) owns steps
     // 4r..4r+3 of channel c0 + row and, for the B / C staging, of state row
-    const rsrc_t Ru = make_rsrc(static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds);
-    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
-    const rsrc_t Rz = make_rsrc(kZ ? static_cast<const IT*>(p.z) + b * p.z_bs + c0 * p.z_ds : nullptr);
-    const rsrc_t RB = make_rsrc(static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs);
-    const rsrc_t RC = make_rsrc(static_cast<const IT*>(p.C) + b * p.C_bs + g * p.C_gs);
+    constexpr int64_t es64 = sizeof(IT);
+    const rsrc_t Ru = make_rsrc_in(p.u, (b * p.u_bs + c0 * p.u_ds) * es64, p.u_end);
+    const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
+    const rsrc_t Rz = kZ ? make_rsrc_in(p.z, (b * p.z_bs + c0 * p.z_ds) * es64, p.z_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t RB = make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end);
+    const rsrc_t RC = make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end);
     // out / y are written with 16-byte stores, which take their advance in the
-    // resource base and no uniform offset (see bstore4)
-    IT* const go = static_cast<IT*>(p.out) + b * p.o_bs + c0 * p.o_ds;
-    // without a y (or x) buffer the stores go through a zero-byte resource
-    // and are dropped: a forward that no backward follows writes neither
-    const bool save_y = kZ && p.y != nullptr, save_x = p.x != nullptr;
-    const int y_records = kZ ? p.y_records : 0;
-    IT* const gy = save_y ? static_cast<IT*>(p.y) + b * p.y_bs + c0 * p.y_ds : go;
+    // resource base and no uniform offset (see bstore4).  Without a y (or x)
+    // buffer the stores go through a zero-byte resource and are dropped: a
+    // forward that no backward follows writes neither.
+    const int64_t o_off = (b * p.o_bs + c0 * p.o_ds) * es64, y_off = (b * p.y_bs + c0 * p.y_ds) * es64;
+    const int64_t y_end = kZ ? p.y_end : 0;
     // x: (batch, chunk, dim, dstate)
-    const rsrc_t Rx = make_rsrc_n(save_x ? p.x + (b * p.n_chunks * p.dim + c0) * kT : nullptr, p.x_records);
+    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
+    const rsrc_t Rx = make_rsrc_in(p.x, x_off, p.x_end);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
     const uint32_t oz = uint32_t(row * p.z_ds + 4 * r) * es;
@@ -297,8 +297,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const uint32_t x_chunk_bytes = uint32_t(p.dim * kT * 4);
     // the tail's checkpoints: a resource that ends with this batch row's
     // n_chunks chunks, so the stores of chunks past the sequence are dropped
-    const rsrc_t Rx_tail = make_rsrc_n(save_x ? p.x + (b * p.n_chunks * p.dim + c0) * kT : nullptr,
-                                       p.x_records == 0 ? 0 : int(uint32_t((p.n_chunks * p.dim - c0) * kT * 4)));
+    const int64_t x_row_end = (b + 1) * p.n_chunks * p.dim * kT * 4;
+    const rsrc_t Rx_tail = make_rsrc_in(p.x, x_off, p.x_end < x_row_end ? p.x_end : x_row_end);
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -373,13 +373,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
         if constexpr (kZ) {
-            bstore4<IT>(make_rsrc_n(gy + int64_t(sc) * kSC, y_records), oy, y);
+            bstore4<IT>(make_rsrc_in(p.y, y_off + int64_t(sc) * kSC * es64, y_end), oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);
             y.w *= pz.w * sigmoidf_(pz.w);
         }
-        bstore4<IT>(make_rsrc(go + int64_t(sc) * kSC), oo, y);
+        bstore4<IT>(make_rsrc_in(p.out, o_off + int64_t(sc) * kSC * es64, p.o_end), oo, y);
     };
     // as finish_super for the tail super-chunk: element stores of its lt steps
     auto finish_super_tail = [&](int sc) {
@@ -389,8 +389,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
         float yv[4] = {y.x, y.y, y.z, y.w}, zv[4] = {pz.x, pz.y, pz.z, pz.w};
-        const rsrc_t Ro = make_rsrc(go + int64_t(sc) * kSC);
-        const rsrc_t Ryt = make_rsrc_n(gy + int64_t(sc) * kSC, y_records);
+        const rsrc_t Ro = make_rsrc_in(p.out, o_off + int64_t(sc) * kSC * es64, p.o_end);
+        const rsrc_t Ryt = make_rsrc_in(p.y, y_off + int64_t(sc) * kSC * es64, y_end);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             if (4 * r + i < lt) {
@@ -555,9 +555,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     const int nsc_seg = int((p.seqlen + kSC - 1) / kSC) / p.nseg;
     const int sc0 = seg * nsc_seg, sc1 = sc0 + nsc_seg;
 
-    const rsrc_t Ru = make_rsrc(static_cast<const IT*>(p.u) + b * p.u_bs + c0 * p.u_ds);
-    const rsrc_t Rd = make_rsrc(static_cast<const IT*>(p.delta) + b * p.dl_bs + c0 * p.dl_ds);
-    const rsrc_t RB = make_rsrc(static_cast<const IT*>(p.B) + b * p.B_bs + g * p.B_gs);
+    constexpr int64_t es64 = sizeof(IT);
+    const rsrc_t Ru = make_rsrc_in(p.u, (b * p.u_bs + c0 * p.u_ds) * es64, p.u_end);
+    const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
+    const rsrc_t RB = make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
     const uint32_t oB = uint32_t(row * p.B_ns + 4 * r) * es;

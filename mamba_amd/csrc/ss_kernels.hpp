@@ -23,11 +23,12 @@ struct FwdParams {
     void* out; float* x;
     void* y;                                  // pre-gate output (z gate only); may be null in forward
     float* last_state;                        // forward: h after the last step, (batch, dim, dstate); may be null
-    // buffer record counts of the x and y stores of the fast forward: -1
-    // (the whole range) when the buffer is there, 0 when it is not (the
-    // hardware range check then drops every store); set by the host, so the
-    // resources stay scalar
-    int32_t x_records, y_records;
+    // bytes from each array's base pointer to the end of its last element (0
+    // for an absent array): the fast kernels' buffer resources end there, so
+    // the hardware's range check drops any access past an array, and every
+    // store to an absent optional output (x, y: a forward that no backward
+    // follows writes neither)
+    int64_t u_end, dl_end, z_end, o_end, y_end, B_end, C_end, x_end;
     // sequence-parallel scan (fast paths): the sequence is cut into nseg
     // equal segments handled by separate workgroups; seg_h (batch, nseg,
     // dim, 16) holds each segment's end state (forward) or adjoint carry
@@ -56,6 +57,9 @@ struct BwdParams {
     float* ws;
     int32_t ws_slices;
     int64_t ws_stride;
+    // byte extents of dout, du, ddelta, dz, dB, dC and the slices of ws (as
+    // FwdParams' *_end)
+    int64_t do_end, du_end, dd_end, dz_end, dB_end, dC_end, ws_end;
     // row length (floats) of the dB / dC rows the fast kernel adds into:
     // seqlen for dB / dC themselves; in the workspace the rows are padded to
     // whole chunk pairs (a multiple of 32 steps), so that every row starts on

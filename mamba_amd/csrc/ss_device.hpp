@@ -410,15 +410,19 @@ __device__ __forceinline__ float bload(rsrc_t r, uint32_t voff, uint32_t soff) {
         else return float(__builtin_bit_cast(_Float16, uint16_t(v)));
     }
 }
-template <typename T>
+// Cache policy of a buffer store: kStoreNT marks the data non-temporal
+// (the cache keeps it for the shortest time), for streams nothing in the
+// same kernel reads again.
+constexpr int kStoreDefault = 0, kStoreNT = 2;
+template <typename T, int kPolicy = kStoreDefault>
 __device__ __forceinline__ void bstore(rsrc_t r, uint32_t voff, uint32_t soff, float v) {
     if constexpr (sizeof(T) == 4) {
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, int(voff), int(soff), 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, int(voff), int(soff), kPolicy);
     } else {
         uint16_t h;
         if constexpr (__is_same(T, bf16_t)) h = io<bf16_t>::round(v);
         else h = __builtin_bit_cast(uint16_t, _Float16(v));
-        __builtin_amdgcn_raw_buffer_store_b16(h, r, int(voff), int(soff), 0);
+        __builtin_amdgcn_raw_buffer_store_b16(h, r, int(voff), int(soff), kPolicy);
     }
 }
 // Four consecutive elements (voff + soff bytes, element aligned) as float4:
@@ -448,20 +452,20 @@ __device__ __forceinline__ float4 bload4(rsrc_t r, uint32_t voff, uint32_t soff)
 // The compiler inserts the wait states for that only when the store's
 // uniform offset is not a register, so this store takes no uniform offset:
 // callers fold their advance into the resource base.
-template <typename T>
+template <typename T, int kPolicy = kStoreDefault>
 __device__ __forceinline__ void bstore4(rsrc_t r, uint32_t voff, float4 v) {
     if constexpr (sizeof(T) == 4) {
         const u32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
-        __builtin_amdgcn_raw_buffer_store_b128(w, r, int(voff), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(w, r, int(voff), 0, kPolicy);
     } else if constexpr (__is_same(T, bf16_t)) {
         const u32x2 w = {io<bf16_t>::pack2(v.x, v.y), io<bf16_t>::pack2(v.z, v.w)};
-        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), 0, kPolicy);
     } else {
         const u32x2 w = {uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.x))) |
                              (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.y))) << 16),
                          uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.z))) |
                              (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v.w))) << 16)};
-        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(w, r, int(voff), 0, kPolicy);
     }
 }
 __device__ __forceinline__ float f4get(const float4& v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }

@@ -222,7 +222,11 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
 //    super-chunk are regrouped through LDS into the owners' float4 for the
 //    stores, one super-chunk late;
 //  - the checkpoint of the state is one store per lane and chunk (a wave's
-//    4 channels x 16 states are 256 contiguous bytes).
+//    4 channels x 16 states are 256 contiguous bytes);
+//  - out, y and the checkpoints are stored non-temporal: nothing in the
+//    kernel reads them again (fp32 forward 145.5-150.2 -> 142.5-149.3 us,
+//    bf16 933 -> 916 us, same box; the backward's stores measured no faster
+//    that way and keep the default policy).
 constexpr int kSC = 64;                      // steps per super-chunk
 constexpr int kQ = kSC / kT;                 // chunks per super-chunk
 constexpr int kYRow = kT * kT + 16;          // per-row product tile, padded so rows j, j + 1 use different bank halves
@@ -373,13 +377,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
         if constexpr (kZ) {
-            bstore4<IT>(make_rsrc_in(p.y, y_off + int64_t(sc) * kSC * es64, y_end), oy, y);
+            bstore4<IT, kStoreNT>(make_rsrc_in(p.y, y_off + int64_t(sc) * kSC * es64, y_end), oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);
             y.w *= pz.w * sigmoidf_(pz.w);
         }
-        bstore4<IT>(make_rsrc_in(p.out, o_off + int64_t(sc) * kSC * es64, p.o_end), oo, y);
+        bstore4<IT, kStoreNT>(make_rsrc_in(p.out, o_off + int64_t(sc) * kSC * es64, p.o_end), oo, y);
     };
     // as finish_super for the tail super-chunk: element stores of its lt steps
     auto finish_super_tail = [&](int sc) {
@@ -396,10 +400,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             if (4 * r + i < lt) {
                 float o = yv[i];
                 if constexpr (kZ) {
-                    bstore<IT>(Ryt, oy + uint32_t(i) * es, 0, o);
+                    bstore<IT, kStoreNT>(Ryt, oy + uint32_t(i) * es, 0, o);
                     o *= zv[i] * sigmoidf_(zv[i]);
                 }
-                bstore<IT>(Ro, oo + uint32_t(i) * es, 0, o);
+                bstore<IT, kStoreNT>(Ro, oo + uint32_t(i) * es, 0, o);
             }
         }
     };
@@ -489,7 +493,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                 h = __builtin_fmaf(a[k], h, bmul<4 * q + k / 4>(f4get(dtu, k % 4), Bq[k]));
                 yp[k] = h;
             });
-            bstore<float>(kTail ? Rx_tail : Rx, ox, uint32_t(kQ * sc + q) * x_chunk_bytes, h);
+            bstore<float, kStoreNT>(kTail ? Rx_tail : Rx, ox, uint32_t(kQ * sc + q) * x_chunk_bytes, h);
 #pragma unroll
             for (int m = 0; m < 4; ++m)
                 *reinterpret_cast<float4*>(yrow + r * 16 + 4 * (m ^ ((r >> 1) & 3))) =

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 12
+#define SS_ABI_VERSION 13
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -378,7 +378,26 @@ int ss_conv1d_update(const ss_conv1d_update_args* a, void* stream);
  * (batch, n_out / k_in) rows; weight: (n_out, k_in) rows; unit column
  * strides, row strides multiples of 4 elements, 8-byte aligned bases; k_in a
  * multiple of 16; dtype bf16 or fp16; bias of that dtype or fp32.  No
- * counterpart in the reference (it has no decode path). */
+ * counterpart in the reference (it has no decode path).
+ *
+ * ABI v13 adds two optional parts:
+ * - workspace: with it the library may split K over several workgroups per
+ *   16 x 16 output tile (a decode product streams the weight with only a few
+ *   tiles, and each compute unit fetches a bounded number of cache lines at
+ *   once); the last workgroup of a tile to finish sums the fp32 partial
+ *   tiles in a fixed order, so results do not depend on timing.  Size from
+ *   ss_decode_linear_workspace_bytes (0: no split for this shape, the
+ *   workspace is not used).  The caller zeroes it once before its first
+ *   use; every call leaves it ready for the next one (its tile counters back
+ *   at zero), whatever the shape, so calls of different shapes can share
+ *   one.  Calls that share a workspace must not run at the same time.
+ * - conv: outputs n < conv->dim then pass through the causal conv1d update
+ *   that ss_conv1d_update describes for x = the product (+ bias) rounded to
+ *   dtype (conv->x and conv->out are ignored; the conv output is written to
+ *   y[b, n], the conv state is advanced in place); outputs n >= conv->dim
+ *   are written as they are.  This is the block's input projection followed
+ *   by its conv step in one launch.  conv->itype must equal dtype,
+ *   conv->batch equal batch, conv->dim <= n_out. */
 typedef struct ss_decode_linear_args {
     int64_t batch, n_out, k_in;
     int32_t dtype;                       /* SS_BF16 or SS_F16: x, weight, y */
@@ -388,8 +407,14 @@ typedef struct ss_decode_linear_args {
     const void* weight;
     const void* bias;                    /* may be NULL */
     void* y;
+    void* workspace;                     /* may be NULL (ABI v13) */
+    int64_t workspace_bytes;
+    const ss_conv1d_update_args* conv;   /* may be NULL (ABI v13) */
 } ss_decode_linear_args;
 
+/* Workspace bytes ss_decode_linear can use for this shape (0: none); -1 on
+ * invalid sizes (see ss_last_error).  Depends on batch, n_out and k_in only. */
+int64_t ss_decode_linear_workspace_bytes(const ss_decode_linear_args* a);
 int ss_decode_linear(const ss_decode_linear_args* a, void* stream);
 
 #ifdef __cplusplus

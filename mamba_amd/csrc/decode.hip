@@ -56,12 +56,36 @@ __device__ __forceinline__ void unpack16(const uint4 v, float (&o)[16 / sizeof(I
     }
 }
 
-template <typename IT>
+// kN16: dstate 16 with contiguous, 16-byte aligned state and A rows (the
+// host checks): the state, A, B and C of the channel are requested before
+// the delta dot product, so the thread waits for memory twice instead of
+// once per group of 4 states; the arithmetic and its order are those of the
+// general path.
+template <typename IT, bool kN16>
 __global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update_args a, bool vec, bool lowvec) {
     const int64_t i = int64_t(blockIdx.x) * kDT + threadIdx.x;
     if (i >= a.batch * a.dim) return;                   // no barrier in this kernel
     const int64_t b = i / a.dim, d = i % a.dim;
     const int64_t g = d / (a.dim / a.n_groups);
+    const IT* Bp = static_cast<const IT*>(a.B) + b * a.B_batch_stride + g * a.B_group_stride;
+    const IT* Cp = static_cast<const IT*>(a.C) + b * a.C_batch_stride + g * a.C_group_stride;
+    const float* Ap = a.A + d * a.A_dim_stride;
+    float* h = a.state + b * a.state_batch_stride + d * a.state_dim_stride;
+    float hv[16], av[16], bv[16], cv[16];
+    if constexpr (kN16) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 h4 = *reinterpret_cast<const float4*>(h + 4 * q);
+            const float4 a4 = *reinterpret_cast<const float4*>(Ap + 4 * q);
+            hv[4 * q] = h4.x, hv[4 * q + 1] = h4.y, hv[4 * q + 2] = h4.z, hv[4 * q + 3] = h4.w;
+            av[4 * q] = a4.x, av[4 * q + 1] = a4.y, av[4 * q + 2] = a4.z, av[4 * q + 3] = a4.w;
+        }
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+            bv[n] = io<IT>::load(Bp + n * a.B_dstate_stride);
+            cv[n] = io<IT>::load(Cp + n * a.C_dstate_stride);
+        }
+    }
     const IT* xs = static_cast<const IT*>(a.x);
     const IT* dts = static_cast<const IT*>(a.delta);
     const float x = io<IT>::load(xs + b * a.x_batch_stride + d * a.x_dim_stride);
@@ -105,13 +129,19 @@ __global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update
     if (a.has_delta_bias) dt += a.delta_bias[d];
     if (a.delta_softplus) dt = softplus20(dt);
     const float dtx = dt * x;
-    const IT* Bp = static_cast<const IT*>(a.B) + b * a.B_batch_stride + g * a.B_group_stride;
-    const IT* Cp = static_cast<const IT*>(a.C) + b * a.C_batch_stride + g * a.C_group_stride;
-    const float* Ap = a.A + d * a.A_dim_stride;
-    float* h = a.state + b * a.state_batch_stride + d * a.state_dim_stride;
 
     float y = 0.f;
-    if (vec) {                                          // state, A rows contiguous and 16-byte aligned
+    if constexpr (kN16) {
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+            const float dA = __builtin_amdgcn_exp2f(dt * av[n] * kLog2e);
+            hv[n] = __builtin_fmaf(dA, hv[n], dtx * bv[n]);
+            y = __builtin_fmaf(cv[n], hv[n], y);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4*>(h + 4 * q) = make_float4(hv[4 * q], hv[4 * q + 1], hv[4 * q + 2], hv[4 * q + 3]);
+    } else if (vec) {                                          // state, A rows contiguous and 16-byte aligned
         for (int64_t n = 0; n < a.dstate; n += 4) {
             float4 hv = *reinterpret_cast<const float4*>(h + n);
             const float4 av = *reinterpret_cast<const float4*>(Ap + n);
@@ -175,10 +205,19 @@ hipError_t state_update_launch(const ss_state_update_args* a, hipStream_t stream
                         al16(a->delta_low) && al16(a->delta_weight) && (a->delta_low_batch_stride * es) % 16 == 0 &&
                         (a->delta_weight_dim_stride * es) % 16 == 0 && (a->delta_rank * es) % 16 == 0;
     const dim3 grid{unsigned((a->batch * a->dim + kDT - 1) / kDT)};
+    if (vec && a->dstate == 16) {
+        switch (a->itype) {
+            case SS_F32: hipLaunchKernelGGL((state_update_kernel<float, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+            case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+            case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (a->itype) {
-        case SS_F32: hipLaunchKernelGGL((state_update_kernel<float>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
-        case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
-        case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+        case SS_F32: hipLaunchKernelGGL((state_update_kernel<float, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+        case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+        case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

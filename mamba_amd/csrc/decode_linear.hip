@@ -7,15 +7,44 @@
 // and does little arithmetic per byte; the library GEMMs choose large tiles
 // for it and take several times the weight's streaming time.
 //
-// A workgroup computes a 16 (n) x 16 (b) tile of Y.  Its 4 waves take every
-// 4th 16-wide step of K; each step is one v_mfma_f32_16x16x16_bf16 (or f16)
-// with the W tile (16 n x 16 k) as A and the X tile (16 k x 16 b) as B:
-//   A: lane l holds W[n0 + (l & 15)][k + 4 (l >> 4) .. + 3]
-//   B: lane l holds X[b0 + (l & 15)][k + 4 (l >> 4) .. + 3]
+// A workgroup computes a 16 (n) x 16 (b) tile of Y, or one slice of K of
+// it, with NW waves that take every NW-th K step; each K step is one or two
+// v_mfma_f32_16x16x16_bf16 (or f16) with the W tile (16 n x 16 k) as A and
+// the X tile (16 k x 16 b) as B:
+//   A: lane l holds W[n0 + (l & 15)][4 (l >> 4) .. + 3] of a 16-wide k set
+//   B: lane l holds X[b0 + (l & 15)][the same k set]
 //   D: lane l holds Y[b0 + (l & 15)][n0 + 4 (l >> 4) + v], v = 0..3
-// The 4 partial tiles are summed through LDS; the bias is added in fp32 and
-// the result rounded once.  Rows n >= N and b >= B read as zero (clamped
-// addresses) and are not stored, so every access stays in bounds.
+// With 16-byte aligned rows and k_in a multiple of 32 a lane loads 8
+// elements (16 bytes) of its W row and X row per K step of 32: elements 0-3
+// feed one MFMA and 4-7 the next (each MFMA sums over its own k set, the
+// same for A and B); otherwise 4 elements (8 bytes) per K step of 16.  The
+// wave count grows with the steps a workgroup has (4, 8 or 16) so that a
+// wave requests all its steps before it uses any.  The partial tiles of the
+// waves are summed through LDS.
+//
+// Split K: a workgroup's time grows with the K it covers (measured on a
+// 16 x 16 tile: 3.1 us at K = 48, 5.7 at 768, 9.0 at 1536, whatever the
+// wave count), and a decode product can have very few tiles (5 for the
+// x-projection of a 1536-wide block).  For such shapes (fewer than
+// kLinSplitMaxTiles tiles) and a workspace, the K range of a tile is cut
+// into slices, one workgroup each; each puts its fp32 partial tile into a
+// slot, and the last of a tile's workgroups to arrive (a per-tile counter)
+// sums the slots in slice order, so the result does not depend on which
+// one finishes last, and puts the counter back to zero for the next call.
+// The exchange costs about three dependent atomic round trips, so it pays
+// only where the tiles are few (x-projection 9.0 -> 5.25 us with 4 slices,
+// 5.8 with 16; the 192-tile input projection loses).  It
+// uses atomics only: an agent-scope fence writes back and invalidates the
+// whole L2 of its XCD, which made every workgroup's weight reads miss (53 us
+// instead of 5.7 for the 768 x 3072 input projection).  The counters have a
+// fixed region ahead of the partials, so calls of different shapes can
+// share a workspace.
+//
+// Epilogue: the bias is added in fp32 and the result rounded once; with a
+// conv update the rounded product of an output n < conv.dim is the input of
+// that channel's causal conv step (state shifted in place, conv output
+// written to Y).  Rows n >= N and b >= B read as zero (clamped addresses)
+// and are not stored, so every access stays in bounds.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -32,9 +61,6 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLinWaves = 4;
-constexpr int kLinBatch = 16;          // K steps per wave in flight at once
-
 template <typename T>
 __device__ __forceinline__ f32x4 mfma16(s16x4 a, s16x4 b, f32x4 c) {
     if constexpr (__is_same(T, bf16_t)) {
@@ -45,71 +71,203 @@ __device__ __forceinline__ f32x4 mfma16(s16x4 a, s16x4 b, f32x4 c) {
     }
 }
 
+// KV elements of a row (KV = 4: 8 bytes, KV = 8: 16 bytes)
+template <int KV>
+using rowvec = short __attribute__((ext_vector_type(KV)));
+
+// v rounded to T and back to float (round to nearest even)
 template <typename T>
-__global__ __launch_bounds__(64 * kLinWaves) void decode_linear_kernel(const ss_decode_linear_args a) {
-    __shared__ f32x4 part[kLinWaves][64];
+__device__ __forceinline__ float round_io(float v) {
+    if constexpr (__is_same(T, bf16_t)) return __uint_as_float(uint32_t(io<bf16_t>::round(v)) << 16);
+    else return float(_Float16(v));
+}
+
+struct LinExtra {
+    int64_t ksplit;                    // workgroups per output tile (1: no split)
+    int64_t kslice;                    // K elements per slice
+    int* counters;                     // per tile, in the workspace
+    float* partials;                   // (tile, slice, 256) fp32, in the workspace
+    int32_t has_conv, pad_;
+    ss_conv1d_update_args conv;
+};
+
+template <typename T, int NW, int KV>
+__global__ __launch_bounds__(64 * NW) void decode_linear_kernel(const ss_decode_linear_args a, const LinExtra e) {
+    constexpr int KS = 4 * KV;                        // k per step: 16 or 32
+    constexpr int kBatch = KV == 8 ? 8 : 16;          // steps of a wave in flight at once
+    __shared__ float part[NW * 256];
+    __shared__ int last;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int i = lane & 15, q = lane >> 4;
-    const int64_t n0 = int64_t(blockIdx.x) * 16, b0 = int64_t(blockIdx.y) * 16;
+    const int64_t tile_n = blockIdx.x / e.ksplit, kidx = blockIdx.x % e.ksplit;
+    const int64_t n0 = tile_n * 16, b0 = int64_t(blockIdx.y) * 16;
     const int64_t n = n0 + i, b = b0 + i;
     const bool nv = n < a.n_out, bv = b < a.batch;
-    // 4 consecutive elements (8 bytes) of this lane's W row and X row per K step
-    const uint16_t* wrow = static_cast<const uint16_t*>(a.weight) + (nv ? n : 0) * a.w_row_stride + 4 * q;
-    const uint16_t* xrow = static_cast<const uint16_t*>(a.x) + (bv ? b : 0) * a.x_row_stride + 4 * q;
-    const int64_t ksteps = a.k_in / 16;
+    const uint16_t* wrow = static_cast<const uint16_t*>(a.weight) + (nv ? n : 0) * a.w_row_stride + KV * q;
+    const uint16_t* xrow = static_cast<const uint16_t*>(a.x) + (bv ? b : 0) * a.x_row_stride + KV * q;
+    // this workgroup's K steps: [kb, ke) (slices are whole steps)
+    const int64_t kb = kidx * e.kslice / KS;
+    const int64_t kend = (kidx + 1) * e.kslice < a.k_in ? (kidx + 1) * e.kslice : a.k_in;
+    const int64_t ke = kend / KS;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    // kLinBatch steps of this wave are requested before any is used, so a
-    // wave waits for memory once per batch (once in all for k_in <= 1024);
-    // steps past the end read the last step again and are zeroed
-    for (int64_t kt0 = w; kt0 < ksteps; kt0 += kLinWaves * kLinBatch) {
-        s16x4 av[kLinBatch], xv[kLinBatch];
+    // kBatch steps of this wave are requested before any is used; steps past
+    // the end read the last step again and are zeroed
+    for (int64_t kt0 = kb + w; kt0 < ke; kt0 += NW * kBatch) {
+        rowvec<KV> av[kBatch], xv[kBatch];
 #pragma unroll
-        for (int u = 0; u < kLinBatch; ++u) {
-            const int64_t kt = kt0 + kLinWaves * u;
-            const int64_t kc = kt < ksteps ? kt : ksteps - 1;
-            av[u] = *reinterpret_cast<const s16x4*>(wrow + kc * 16);
-            xv[u] = *reinterpret_cast<const s16x4*>(xrow + kc * 16);
+        for (int u = 0; u < kBatch; ++u) {
+            const int64_t kt = kt0 + NW * u;
+            const int64_t kc = kt < ke ? kt : ke - 1;
+            av[u] = *reinterpret_cast<const rowvec<KV>*>(wrow + kc * KS);
+            xv[u] = *reinterpret_cast<const rowvec<KV>*>(xrow + kc * KS);
         }
 #pragma unroll
-        for (int u = 0; u < kLinBatch; ++u) {
-            const bool live = kt0 + kLinWaves * u < ksteps;
-            const s16x4 z = {0, 0, 0, 0};
-            acc = mfma16<T>((live && nv) ? av[u] : z, (live && bv) ? xv[u] : z, acc);
-        }
-    }
-    part[w][lane] = acc;
-    __syncthreads();
-    if (w != 0) return;
-    f32x4 s = part[0][lane];
-#pragma unroll
-    for (int ww = 1; ww < kLinWaves; ++ww) s += part[ww][lane];
-    if (!bv) return;
-    T* yrow = static_cast<T*>(a.y) + b * a.y_row_stride;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const int64_t nn = n0 + 4 * q + v;
-        if (nn < a.n_out) {
-            float o = s[v];
-            if (a.bias) {
-                o += a.bias_dtype == SS_F32 ? static_cast<const float*>(a.bias)[nn]
-                                            : io<T>::load(static_cast<const T*>(a.bias) + nn);
+        for (int u = 0; u < kBatch; ++u) {
+            const bool live = kt0 + NW * u < ke;
+            const rowvec<KV> z = {};
+            const rowvec<KV> av_ = (live && nv) ? av[u] : z, xv_ = (live && bv) ? xv[u] : z;
+            if constexpr (KV == 8) {
+                acc = mfma16<T>(av_.lo, xv_.lo, acc);
+                acc = mfma16<T>(av_.hi, xv_.hi, acc);
+            } else {
+                acc = mfma16<T>(av_, xv_, acc);
             }
-            io<T>::store(yrow + nn, o);
         }
     }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[(w * 64 + lane) * 4 + v] = acc[v];
+    __syncthreads();
+    // thread t < 256 sums output (lane t / 4, component t % 4) over the waves
+    const int t = threadIdx.x;
+    float o = 0.f;
+    if (t < 256) {
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) o += part[ww * 256 + t];
+    }
+    if (e.ksplit > 1) {
+        // every exchange between the workgroups of a tile is an atomic
+        // read-modify-write, performed where the whole device sees it, so no
+        // cache write-back or invalidation is needed: the partial goes into
+        // its slot by 64-bit atomic swaps (two outputs each), which complete
+        // (vmcnt 0) before the counter is advanced; the workgroup that
+        // advances it last takes the slots back with atomic swaps (a
+        // read-modify-write, which the compiler does not turn into a plain
+        // load as it does an OR of 0), in slice order
+        const int64_t tile = int64_t(blockIdx.y) * (int64_t(gridDim.x) / e.ksplit) + tile_n;
+        unsigned long long* pt = reinterpret_cast<unsigned long long*>(e.partials + tile * e.ksplit * 256);
+        if (t < 128) {
+            float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < NW; ++ww) {
+                o0 += part[ww * 256 + 2 * t];
+                o1 += part[ww * 256 + 2 * t + 1];
+            }
+            (void)atomicExch(pt + kidx * 128 + t,
+                             (static_cast<unsigned long long>(__float_as_uint(o1)) << 32) | __float_as_uint(o0));
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (t == 0) last = atomicAdd(e.counters + tile, 1) == int(e.ksplit) - 1;
+        __syncthreads();
+        if (!last) return;
+        if (t < 128) {
+            // every slot is requested before the first is added (one wait)
+            unsigned long long sv[kLinMaxSplit];
+#pragma unroll
+            for (int k = 0; k < kLinMaxSplit; ++k) sv[k] = k < e.ksplit ? atomicExch(pt + k * 128 + t, 0ull) : 0ull;
+            float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+            for (int k = 0; k < kLinMaxSplit; ++k) {
+                o0 += __uint_as_float(uint32_t(sv[k]));
+                o1 += __uint_as_float(uint32_t(sv[k] >> 32));
+            }
+            part[2 * t] = o0;                         // every read of part is behind the barriers above
+            part[2 * t + 1] = o1;
+        }
+        if (t == 0) (void)atomicExch(e.counters + tile, 0);
+        __syncthreads();
+        if (t < 256) o = part[t];
+    }
+    if (t >= 256) return;
+    const int ol = t >> 2, v = t & 3;
+    const int64_t ob = b0 + (ol & 15), on = n0 + 4 * (ol >> 4) + v;
+    if (ob >= a.batch || on >= a.n_out) return;
+    if (a.bias) {
+        o += a.bias_dtype == SS_F32 ? static_cast<const float*>(a.bias)[on]
+                                    : io<T>::load(static_cast<const T*>(a.bias) + on);
+    }
+    if (e.has_conv && on < e.conv.dim) {
+        // the causal conv step of channel on, fed the product as it would be
+        // stored (rounded to T), in the order of the conv update kernel
+        const ss_conv1d_update_args& c = e.conv;
+        const int W = int(c.width);
+        T* st = static_cast<T*>(c.conv_state) + ob * c.state_batch_stride + on * c.state_dim_stride;
+        float sv[4];
+        for (int k = 0; k < W - 1; ++k) sv[k] = io<T>::load(st + (k + 1) * c.state_width_stride);
+        sv[W - 1] = round_io<T>(o);
+        float cacc = c.has_bias ? c.bias[on] : 0.f;
+        for (int k = 0; k < W; ++k) {
+            cacc = __builtin_fmaf(c.weight[on * c.w_dim_stride + k * c.w_width_stride], sv[k], cacc);
+            io<T>::store(st + k * c.state_width_stride, sv[k]);
+        }
+        if (c.silu) cacc *= sigmoidf_(cacc);
+        o = cacc;
+    }
+    io<T>::store(static_cast<T*>(a.y) + ob * a.y_row_stride + on, o);
+}
+
+template <typename T, int KV>
+void launch_kv(const ss_decode_linear_args* a, const LinExtra& e, hipStream_t stream) {
+    const dim3 grid{unsigned((a->n_out + 15) / 16 * e.ksplit), unsigned((a->batch + 15) / 16)};
+    const int64_t steps = (e.kslice + 4 * KV - 1) / (4 * KV);   // K steps per workgroup
+    if (steps <= 16) hipLaunchKernelGGL((decode_linear_kernel<T, 4, KV>), grid, dim3(256), 0, stream, *a, e);
+    else if (steps <= 32) hipLaunchKernelGGL((decode_linear_kernel<T, 8, KV>), grid, dim3(512), 0, stream, *a, e);
+    else hipLaunchKernelGGL((decode_linear_kernel<T, 16, KV>), grid, dim3(1024), 0, stream, *a, e);
 }
 
 template <typename T>
-void launch_t(const ss_decode_linear_args* a, hipStream_t stream) {
-    const dim3 grid{unsigned((a->n_out + 15) / 16), unsigned((a->batch + 15) / 16)};
-    hipLaunchKernelGGL((decode_linear_kernel<T>), grid, dim3(64 * kLinWaves), 0, stream, *a);
+void launch_t(const ss_decode_linear_args* a, const LinExtra& e, hipStream_t stream) {
+    const bool wide = a->k_in % 32 == 0 && a->x_row_stride % 8 == 0 && a->w_row_stride % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->weight) & 15) == 0;
+    if (wide) launch_kv<T, 8>(a, e, stream);
+    else launch_kv<T, 4>(a, e, stream);
 }
 
 }  // namespace
 
+DecodeLinearSplit decode_linear_split(int64_t batch, int64_t n_out, int64_t k_in) {
+    DecodeLinearSplit sp{1, k_in, 0};
+    const int64_t unit = k_in % 32 == 0 ? 32 : 16;               // slices are whole K steps of either kernel
+    const int64_t units = k_in / unit;
+    const int64_t tiles = ((n_out + 15) / 16) * ((batch + 15) / 16);
+    if (tiles <= 0 || units < 4 || tiles >= kLinSplitMaxTiles) return sp;
+    const int64_t ks = kLinMaxSplit < units / 2 ? kLinMaxSplit : units / 2;   // at least 2 units per slice
+    if (ks < 2) return sp;
+    const int64_t per = (units + ks - 1) / ks;
+    sp.ksplit = (units + per - 1) / per;
+    sp.kslice = per * unit;
+    if (sp.ksplit < 2) return DecodeLinearSplit{1, k_in, 0};
+    sp.workspace_bytes = kLinCounterBytes + tiles * sp.ksplit * 256 * 4;
+    return sp;
+}
+
 hipError_t decode_linear_launch(const ss_decode_linear_args* a, hipStream_t stream) {
-    if (a->dtype == SS_BF16) launch_t<bf16_t>(a, stream);
-    else launch_t<_Float16>(a, stream);
+    LinExtra e{};
+    e.ksplit = 1;
+    e.kslice = a->k_in;
+    const DecodeLinearSplit sp = decode_linear_split(a->batch, a->n_out, a->k_in);
+    if (a->workspace && sp.ksplit > 1 && a->workspace_bytes >= sp.workspace_bytes) {
+        e.ksplit = sp.ksplit;
+        e.kslice = sp.kslice;
+        e.counters = static_cast<int*>(a->workspace);
+        e.partials = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + kLinCounterBytes);
+    }
+    if (a->conv) {
+        e.has_conv = 1;
+        e.conv = *a->conv;
+    }
+    if (a->dtype == SS_BF16) launch_t<bf16_t>(a, e, stream);
+    else launch_t<_Float16>(a, e, stream);
     return hipGetLastError();
 }
 

@@ -615,9 +615,29 @@ int ss_decode_linear(const ss_decode_linear_args* a, void* stream) {
     if (a->bias && a->bias_dtype != a->dtype && a->bias_dtype != SS_F32)
         return fail(SS_ERR_UNSUPPORTED, "bias dtype %d must be the row dtype or fp32", a->bias_dtype);
     if (a->k_in % 16 != 0) return fail(SS_ERR_UNSUPPORTED, "k_in=%lld is not a multiple of 16", (long long)a->k_in);
+    if (a->workspace_bytes < 0) return fail(SS_ERR_INVALID, "negative workspace_bytes");
+    if (a->workspace && !aligned(a->workspace, 16)) return fail(SS_ERR_INVALID, "workspace must be 16-byte aligned");
+    if (const ss_conv1d_update_args* c = a->conv) {
+        if (c->itype != a->dtype) return fail(SS_ERR_INVALID, "conv itype %d differs from dtype %d", c->itype, a->dtype);
+        if (c->batch != a->batch)
+            return fail(SS_ERR_INVALID, "conv batch=%lld differs from batch=%lld", (long long)c->batch, (long long)a->batch);
+        if (c->dim < 0 || c->dim > a->n_out)
+            return fail(SS_ERR_INVALID, "conv dim=%lld outside [0, n_out=%lld]", (long long)c->dim, (long long)a->n_out);
+        if (c->width < 1 || c->width > 4) return fail(SS_ERR_UNSUPPORTED, "width=%lld outside [1, 4]", (long long)c->width);
+        if (c->dim > 0 && a->batch > 0) {
+            if (!c->conv_state || !c->weight || (c->has_bias && !c->bias))
+                return fail(SS_ERR_INVALID, "conv_state / conv weight / conv bias is NULL");
+            if (!aligned(c->conv_state, 2) || !aligned(c->weight, 4) || (c->has_bias && !aligned(c->bias, 4)))
+                return fail(SS_ERR_INVALID, "conv_state / conv weight / conv bias is misaligned");
+            const int64_t st[] = {c->state_batch_stride, c->state_dim_stride, c->state_width_stride, c->w_dim_stride,
+                                  c->w_width_stride};
+            for (int64_t v : st)
+                if (v < 0) return fail(SS_ERR_INVALID, "negative conv stride");
+        }
+    }
     if (a->batch == 0 || a->n_out == 0) return ok();
     if (a->k_in == 0) return fail(SS_ERR_UNSUPPORTED, "k_in=0");
-    if ((a->n_out + 15) / 16 > INT32_MAX || (a->batch + 15) / 16 > 65535)
+    if ((a->n_out + 15) / 16 * ss::kLinMaxSplit > INT32_MAX || (a->batch + 15) / 16 > 65535)
         return fail(SS_ERR_UNSUPPORTED, "n_out or batch too large");
     if (!a->x || !a->weight || !a->y) return fail(SS_ERR_INVALID, "x / weight / y is NULL");
     if (!aligned(a->x, 8) || !aligned(a->weight, 8) || !aligned(a->y, 2))
@@ -629,6 +649,20 @@ int ss_decode_linear(const ss_decode_linear_args* a, void* stream) {
     hipError_t e = ss::decode_linear_launch(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "decode linear launch failed: %s", hipGetErrorString(e));
     return ok();
+}
+
+int64_t ss_decode_linear_workspace_bytes(const ss_decode_linear_args* a) {
+    if (!a) {
+        fail(SS_ERR_INVALID, "null argument block");
+        return -1;
+    }
+    if (a->batch < 0 || a->n_out < 0 || a->k_in < 0 || a->k_in % 16 != 0) {
+        fail(SS_ERR_INVALID, "invalid size (batch=%lld n_out=%lld k_in=%lld)", (long long)a->batch,
+             (long long)a->n_out, (long long)a->k_in);
+        return -1;
+    }
+    ok();
+    return ss::decode_linear_split(a->batch, a->n_out, a->k_in).workspace_bytes;
 }
 
 int64_t ss_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim) {

@@ -115,7 +115,22 @@ hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, h
 // single-token decode: selective-scan state update and conv1d state update
 hipError_t state_update_launch(const ss_state_update_args* a, hipStream_t stream);
 hipError_t conv_update_launch(const ss_conv1d_update_args* a, hipStream_t stream);
-// decode-size linear layer (matrix cores)
+// decode-size linear layer (matrix cores); K split over ksplit workgroups
+// per output tile (slices of kslice elements) when a workspace of
+// workspace_bytes is given (ksplit 1, workspace_bytes 0: no split)
+struct DecodeLinearSplit {
+    int64_t ksplit, kslice, workspace_bytes;
+};
+// only shapes with fewer output tiles than this are split (measured: the
+// split pays for 5 tiles and loses at 192), into at most kLinMaxSplit
+// slices (5 tiles: 4 slices 5.25 us, 8 slices 5.5, 16 slices 5.8)
+constexpr int64_t kLinSplitMaxTiles = 64;
+constexpr int64_t kLinMaxSplit = 4;
+// the workspace starts with one int counter per tile of the largest split
+// shape
+constexpr int64_t kLinCounterBytes = 256;
+static_assert(kLinSplitMaxTiles * 4 <= kLinCounterBytes, "counter region");
+DecodeLinearSplit decode_linear_split(int64_t batch, int64_t n_out, int64_t k_in);
 hipError_t decode_linear_launch(const ss_decode_linear_args* a, hipStream_t stream);
 // RMSNorm (+ residual); g == nullptr: forward, else backward (two kernels:
 // per-workgroup dweight rows into g->workspace, then their fixed-order sum)

@@ -158,7 +158,9 @@ class GraphedStep:
                 model.step(self.ids, inference_cache)
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph), torch.no_grad():
+        # captured on the warm-up stream: per-stream buffers the kernels use
+        # (the decode linear layer's split workspace) already exist there
+        with torch.cuda.graph(self.graph, stream=side), torch.no_grad():
             self.logits = model.step(self.ids, inference_cache)
         with torch.no_grad():
             for (c, s), (c0, s0) in zip(inference_cache, saved):

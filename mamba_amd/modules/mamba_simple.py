@@ -23,7 +23,6 @@ import math
 import torch
 import torch.nn as nn
 
-from ..ops.causal_conv1d import causal_conv1d_update
 from ..ops.decode_linear import decode_linear
 from ..ops.selective_scan_interface import SelectiveScanFn, mamba_inner_fn, mamba_inner_prefill
 from ..ops.selective_state_update import selective_state_update
@@ -130,10 +129,12 @@ class MambaSimple(nn.Module):
         shape; conv_state and ssm_state are advanced in place."""
         squeeze = hidden_states.dim() == 3
         h = hidden_states.reshape(-1, self.model_dim)
-        xz = decode_linear(h, self.input_proj.weight, self.input_proj.bias)          # (batch, 2 * inner)
-        x, z = xz[:, :self.inner_dim], xz[:, self.inner_dim:]
         A, D, dt_bias, conv_w, conv_b = self._decode_params()
-        x = causal_conv1d_update(x, conv_state, conv_w, conv_b, "silu")
+        # the input projection with the conv step fused in: xz[:, :inner] is
+        # already the conv output (the conv state advanced), xz[:, inner:] is z
+        xz = decode_linear(h, self.input_proj.weight, self.input_proj.bias,
+                           conv=(conv_state, conv_w, conv_b, "silu"))                # (batch, 2 * inner)
+        x, z = xz[:, :self.inner_dim], xz[:, self.inner_dim:]
         x_db = decode_linear(x, self.ssm_param_proj.weight)                          # (batch, R + 2N)
         R, N = self.delta_rank, self.state_dim
         # the delta projection (x_db[:, :R] @ W.T) is summed inside the state

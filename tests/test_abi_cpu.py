@@ -60,7 +60,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 12
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 13
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -492,6 +492,33 @@ def test_rmsnorm_workspace_query(lib):
     assert lib.ss_rmsnorm_bwd_workspace_bytes(20, 768) == 3 * 768 * 4
     assert lib.ss_rmsnorm_bwd_workspace_bytes(0, 768) == 0
     assert lib.ss_rmsnorm_bwd_workspace_bytes(-1, 768) == -1
+
+
+def test_decode_linear_workspace_query(nat, lib):
+    # K is split over workgroups only for shapes with fewer than 64 16 x 16
+    # output tiles, into at most 4 slices of at least 2 K units (32 elements,
+    # or 16 when k_in is not a multiple of 32); the workspace is a fixed 256
+    # bytes of tile counters (one per tile of the largest split shape, so every
+    # shape finds its counters at zero) plus one fp32 16 x 16 partial tile per
+    # (tile, slice)
+    def q(batch, n_out, k_in):
+        a = nat.DecodeLinearArgs()
+        a.batch, a.n_out, a.k_in = batch, n_out, k_in
+        return lib.ss_decode_linear_workspace_bytes(ctypes.byref(a))
+    assert q(16, 80, 1536) == 256 + 5 * 4 * 1024             # x-projection: 5 tiles, 4 slices of 384
+    assert q(16, 768, 1536) == 256 + 48 * 4 * 1024           # output projection: 48 tiles
+    assert q(16, 37, 80) == 256 + 3 * 2 * 1024               # 3 tiles, 5 units of 16: slices of 3 and 2
+    assert q(16, 16, 128) == 256 + 1 * 2 * 1024              # 1 tile, 4 units: 2 slices
+    assert q(33, 64, 256) == 256 + 12 * 4 * 1024             # 3 batch tiles x 4: 4 slices of 64
+    assert q(16, 1008, 768) == 256 + 63 * 4 * 1024           # 63 tiles: the largest split shape
+    assert q(16, 37, 48) == 0                                # 3 units: too few to split
+    assert q(16, 1024, 768) == 0                             # 64 tiles: no split
+    assert q(16, 3072, 768) == 0                             # input projection: 192 tiles
+    assert q(16, 50280, 768) == 0
+    assert q(0, 768, 1536) == 0
+    assert q(16, 768, 24) == -1 and b"16" in lib.ss_last_error()
+    for batch, n_out, k_in in [(16, 80, 1536), (1, 1, 1 << 20), (16, 1008, 1 << 20), (64, 240, 2048)]:
+        assert q(batch, n_out, k_in) <= 1 << 20                # the Python layer's per-stream workspace
 
 
 def test_rmsnorm_python_boundary_refuses_cpu_tensors():

@@ -260,3 +260,82 @@ def test_decode_linear_matches_fp32_product(case):
     assert y.dtype == dt and y.shape == (batch, n)
     scale = float(want.abs().max())
     assert_close(y.float().cpu(), want.cpu(), 1e-2, 1e-2 * scale, "y")
+
+
+SPLIT_CASES = [
+    # batch, k_in, n_out, conv channels (0: none), bias dtype (None: no bias), dtype
+    (16, 768, 3072, 1536, torch.bfloat16, torch.bfloat16),   # the block's input projection + conv (192 tiles: no split)
+    (16, 1536, 80, 0, None, torch.bfloat16),                 # x-projection: 5 tiles, 4 slices
+    (16, 1536, 768, 0, torch.bfloat16, torch.bfloat16),      # output projection: 48 tiles, 4 slices
+    (16, 768, 1008, 256, torch.float32, torch.bfloat16),     # 63 tiles (the largest split shape), conv
+    (5, 80, 37, 20, torch.float32, torch.float16),           # ragged tiles, 16-element K steps, 2 slices
+    (33, 256, 64, 64, None, torch.bfloat16),                 # 3 batch tiles, 4 slices, the conv on every output
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[f"b{c[0]}-k{c[1]}-n{c[2]}-conv{c[3]}" for c in SPLIT_CASES])
+def test_decode_linear_split_and_fused_conv(case):
+    # K split over workgroups (last-arriving workgroup sums the partial tiles)
+    # against the fp32 product and the unsplit kernel; the workspace counters
+    # are back at zero after each call and a second call gives the same bits;
+    # the fused conv step equals decode_linear followed by causal_conv1d_update
+    # on the same product (outputs and conv state bit for bit)
+    from mamba_amd.ops import decode_linear as dlm
+    from mamba_amd.ops.causal_conv1d import causal_conv1d_update
+    batch, k, n, cdim, bdt, dt = case
+    _say(f"decode linear split {case}")
+    gen = torch.Generator().manual_seed(500 + k + n)
+    x = torch.randn(batch, k, generator=gen).to(dt).to(DEV)
+    w = (torch.randn(n, k, generator=gen) / k ** 0.5).to(dt).to(DEV)
+    b = torch.randn(n, generator=gen).to(bdt).to(DEV) if bdt is not None else None
+    assert dlm._fits(x, w, b)
+    want = x.float() @ w.float().t() + (b.float() if b is not None else 0.0)
+    scale = float(want.abs().max())
+    y1 = dlm.decode_linear(x, w, b)
+    y0 = dlm.decode_linear(x, w, b, split=False)
+    torch.cuda.synchronize()
+    ws = dlm._workspaces[(DEV.index if DEV.index is not None else 0, torch.cuda.current_stream(DEV).cuda_stream)]
+    tiles = ((n + 15) // 16) * ((batch + 15) // 16)
+    assert int(ws[:tiles * 4].view(torch.int32).abs().sum()) == 0, "tile counters not reset"
+    assert_close(y1.float().cpu(), want.cpu(), 1e-2, 1e-2 * scale, "split")
+    assert_close(y0.float().cpu(), want.cpu(), 1e-2, 1e-2 * scale, "unsplit")
+    assert torch.equal(dlm.decode_linear(x, w, b), y1), "split result differs between calls"
+    if cdim:
+        st0 = torch.randn(batch, cdim, 4, generator=gen).to(dt).to(DEV)
+        cw = torch.randn(cdim, 4, generator=gen).to(DEV)
+        cb = torch.randn(cdim, generator=gen).to(DEV)
+        for split, ylin in ((True, y1), (False, y0)):
+            st_f, st_r = st0.clone(), st0.clone()
+            yf = dlm.decode_linear(x, w, b, conv=(st_f, cw, cb, "silu"), split=split)
+            xr = causal_conv1d_update(ylin[:, :cdim].contiguous(), st_r, cw, cb, "silu")
+            torch.cuda.synchronize()
+            assert torch.equal(yf[:, :cdim], xr), f"fused conv output (split {split})"
+            assert torch.equal(yf[:, cdim:], ylin[:, cdim:]), f"outputs past the conv channels (split {split})"
+            assert torch.equal(st_f, st_r), f"conv state (split {split})"
+
+
+def test_decode_linear_split_replays_in_a_graph():
+    # the split kernel captured in a HIP graph (its workspace made before the
+    # capture, on the capture stream): replays, with eager work between them,
+    # give the eager bits
+    from mamba_amd.ops import decode_linear as dlm
+    _say("decode linear split in a graph")
+    gen = torch.Generator().manual_seed(77)
+    x = torch.randn(16, 1536, generator=gen).bfloat16().to(DEV)
+    w = (torch.randn(400, 1536, generator=gen) / 40).bfloat16().to(DEV)     # 25 tiles, 4 slices
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eager = dlm.decode_linear(x, w)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y = dlm.decode_linear(x, w)
+    for rep in range(4):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {rep}"
+        _ = (x.float() * 2).sum().item()

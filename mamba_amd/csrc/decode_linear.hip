@@ -31,10 +31,13 @@
 // slot, and the last of a tile's workgroups to arrive (a per-tile counter)
 // sums the slots in slice order, so the result does not depend on which
 // one finishes last, and puts the counter back to zero for the next call.
-// The exchange costs about three dependent atomic round trips, so it pays
-// only where the tiles are few (x-projection 9.0 -> 5.25 us with 4 slices,
-// 5.8 with 16; the 192-tile input projection loses).  It
-// uses atomics only: an agent-scope fence writes back and invalidates the
+// The exchange costs about three dependent atomic round trips and grows
+// with the atomics it issues, so it pays only where the tiles are few
+// (x-projection, 5 tiles: 9.0 -> 5.25 us with 4 slices, 5.8 with 16; output
+// projection, 48 tiles: 9.06 -> 6.04 us with 4; the 192-tile input
+// projection loses with 2), and each slot moves as 64-bit swaps of two
+// outputs.  It uses atomics only: an agent-scope fence writes back and
+// invalidates the
 // whole L2 of its XCD, which made every workgroup's weight reads miss (53 us
 // instead of 5.7 for the 768 x 3072 input projection).  The counters have a
 // fixed region ahead of the partials, so calls of different shapes can

@@ -36,7 +36,10 @@ __device__ __forceinline__ float round_to(float v) {
 
 namespace {
 
-constexpr int kDT = 256;              // threads per workgroup
+// threads per workgroup: a decode launch is bound by the cache lines each
+// compute unit fetches (a unit has a limited number of misses in flight),
+// so small workgroups spread a step's lines over more units
+constexpr int kDT = 64;
 
 // The 16 bytes of v as 16 / sizeof(IT) floats.
 template <typename IT>
@@ -62,7 +65,8 @@ __device__ __forceinline__ void unpack16(const uint4 v, float (&o)[16 / sizeof(I
 // once per group of 4 states; the arithmetic and its order are those of the
 // general path.
 template <typename IT, bool kN16>
-__global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update_args a, bool vec, bool lowvec) {
+__global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update_args a, bool vec, bool lowvec,
+                                                          bool bcvec) {
     const int64_t i = int64_t(blockIdx.x) * kDT + threadIdx.x;
     if (i >= a.batch * a.dim) return;                   // no barrier in this kernel
     const int64_t b = i / a.dim, d = i % a.dim;
@@ -80,10 +84,25 @@ __global__ __launch_bounds__(kDT) void state_update_kernel(const ss_state_update
             hv[4 * q] = h4.x, hv[4 * q + 1] = h4.y, hv[4 * q + 2] = h4.z, hv[4 * q + 3] = h4.w;
             av[4 * q] = a4.x, av[4 * q + 1] = a4.y, av[4 * q + 2] = a4.z, av[4 * q + 3] = a4.w;
         }
+        if (bcvec) {                                    // B, C rows contiguous and 16-byte aligned
+            constexpr int E = 16 / int(sizeof(IT));
 #pragma unroll
-        for (int n = 0; n < 16; ++n) {
-            bv[n] = io<IT>::load(Bp + n * a.B_dstate_stride);
-            cv[n] = io<IT>::load(Cp + n * a.C_dstate_stride);
+            for (int q = 0; q < 16 / E; ++q) {
+                float bq[E], cq[E];
+                unpack16<IT>(reinterpret_cast<const uint4*>(Bp)[q], bq);
+                unpack16<IT>(reinterpret_cast<const uint4*>(Cp)[q], cq);
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    bv[q * E + e] = bq[e];
+                    cv[q * E + e] = cq[e];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int n = 0; n < 16; ++n) {
+                bv[n] = io<IT>::load(Bp + n * a.B_dstate_stride);
+                cv[n] = io<IT>::load(Cp + n * a.C_dstate_stride);
+            }
         }
     }
     const IT* xs = static_cast<const IT*>(a.x);
@@ -204,20 +223,23 @@ hipError_t state_update_launch(const ss_state_update_args* a, hipStream_t stream
     const bool lowvec = a->delta_low && a->delta_low_rank_stride == 1 && a->delta_weight_rank_stride == 1 &&
                         al16(a->delta_low) && al16(a->delta_weight) && (a->delta_low_batch_stride * es) % 16 == 0 &&
                         (a->delta_weight_dim_stride * es) % 16 == 0 && (a->delta_rank * es) % 16 == 0;
+    const bool bcvec = a->B_dstate_stride == 1 && a->C_dstate_stride == 1 && al16(a->B) && al16(a->C) &&
+                       (a->B_batch_stride * es) % 16 == 0 && (a->B_group_stride * es) % 16 == 0 &&
+                       (a->C_batch_stride * es) % 16 == 0 && (a->C_group_stride * es) % 16 == 0;
     const dim3 grid{unsigned((a->batch * a->dim + kDT - 1) / kDT)};
     if (vec && a->dstate == 16) {
         switch (a->itype) {
-            case SS_F32: hipLaunchKernelGGL((state_update_kernel<float, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
-            case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
-            case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+            case SS_F32: hipLaunchKernelGGL((state_update_kernel<float, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec, bcvec); break;
+            case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec, bcvec); break;
+            case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16, true>), grid, dim3(kDT), 0, stream, *a, vec, lowvec, bcvec); break;
             default: return hipErrorInvalidValue;
         }
         return hipGetLastError();
     }
     switch (a->itype) {
-        case SS_F32: hipLaunchKernelGGL((state_update_kernel<float, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
-        case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
-        case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec); break;
+        case SS_F32: hipLaunchKernelGGL((state_update_kernel<float, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec, bcvec); break;
+        case SS_BF16: hipLaunchKernelGGL((state_update_kernel<bf16_t, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec, bcvec); break;
+        case SS_F16: hipLaunchKernelGGL((state_update_kernel<_Float16, false>), grid, dim3(kDT), 0, stream, *a, vec, lowvec, bcvec); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -145,7 +145,7 @@ __device__ __forceinline__ void load_w1(const TW* w, int64_t vi, float (&o)[VE])
 template <typename T, typename TW, int VE, bool kPre>
 __global__ __launch_bounds__(64 * kFwdWaves) void rmsnorm_fwd_kernel(const NormParams p) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = int64_t(blockIdx.x) * kFwdWaves + (threadIdx.x >> 6);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= p.rows) return;                          // no barrier in this kernel
     const T* xr = static_cast<const T*>(p.x) + row * p.x_rs;
     const T* rr = p.r ? static_cast<const T*>(p.r) + row * p.r_rs : nullptr;
@@ -416,7 +416,9 @@ hipError_t launch_tw(const NormParams& p, bool vec, bool bwd, int64_t nparts, vo
     if (!bwd) {
         const dim3 grid(unsigned((p.rows + kFwdWaves - 1) / kFwdWaves));
         const bool pre = p.rows <= kRmsNormPreRows && p.dim <= 64 * kNSF * VE;
-        if (vec && pre) hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, TW, VE, true>), grid, dim3(64 * kFwdWaves), 0, stream, p);
+        // few rows: one row per workgroup, so the rows' cache lines are
+        // fetched by as many compute units
+        if (vec && pre) hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, TW, VE, true>), dim3(unsigned(p.rows)), dim3(64), 0, stream, p);
         else if (vec) hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, TW, VE, false>), grid, dim3(64 * kFwdWaves), 0, stream, p);
         else hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, TW, 1, false>), grid, dim3(64 * kFwdWaves), 0, stream, p);
         return hipGetLastError();

@@ -1,9 +1,10 @@
 """GPU parity of single-token decode, through the HIP library.
 
 * ss_state_update against the float64 step oracle: dstate 16 (16-byte state
-  path) and 5 (element path), a strided state, 1 and 2 groups, with and
-  without D / z / bias, fp32 / bf16 / fp16 I/O; delta as the low-rank pair
-  (dt_low, dt_weight) summed in the kernel (vector and element loads);
+  path) and 5 (element path), a strided state, strided B / C, 1 and 2
+  groups, with and without D / z / bias, fp32 / bf16 / fp16 I/O; delta as
+  the low-rank pair (dt_low, dt_weight) summed in the kernel (vector and
+  element loads);
 * ss_conv1d_update against the step oracle: widths 1-4, with and without
   bias and SiLU; the shifted state is bit-exact;
 * token-by-token state updates from a zero state reproduce
@@ -78,6 +79,39 @@ def test_state_update_matches_oracle(case):
     tol = TOL[dt_]
     assert_close(st.cpu(), want_st, 1e-5, 1e-5, "state")
     assert_close(out.cpu(), want_out.double(), tol, tol, "out")
+
+
+@pytest.mark.parametrize("dt_", [torch.float32, torch.bfloat16])
+def test_state_update_strided_B_C(dt_):
+    """dstate 16 with a contiguous state (the path that loads state, A, B and C
+    before the delta) but B and C as views with a dstate stride of 2 (element
+    loads instead of 16-byte ones) against the oracle, and against the same
+    call with contiguous copies of B and C (the same bits)."""
+    from mamba_amd.ops.selective_state_update import selective_state_update
+    _say(f"state update, strided B / C, {dt_}")
+    gen = torch.Generator().manual_seed(321)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    batch, dim, N = 3, 128, 16
+    x, dt, z = r(batch, dim).to(dt_), r(batch, dim).to(dt_), r(batch, dim).to(dt_)
+    A = -torch.rand(dim, N, generator=gen) * 3
+    Bw, Cw = r(batch, 1, 2 * N).to(dt_), r(batch, 1, 2 * N).to(dt_)
+    D, bias = r(dim), r(dim) * 0.5
+    state0 = r(batch, dim, N)
+    outs = []
+    for strided in (True, False):
+        Bd, Cd = Bw.to(DEV)[..., ::2], Cw.to(DEV)[..., ::2]
+        if not strided:
+            Bd, Cd = Bd.contiguous(), Cd.contiguous()
+        st = state0.to(DEV).clone()
+        out = selective_state_update(st, x.to(DEV), dt.to(DEV), A.to(DEV), Bd, Cd, D.to(DEV), z=z.to(DEV),
+                                     dt_bias=bias.to(DEV), dt_softplus=True)
+        outs.append((out, st))
+    want_out, want_st = selective_state_update_ref(state0, x, dt, A, Bw[..., ::2], Cw[..., ::2], D, z=z,
+                                                   dt_bias=bias, dt_softplus=True)
+    tol = TOL[dt_]
+    assert_close(outs[0][1].cpu(), want_st, 1e-5, 1e-5, "state")
+    assert_close(outs[0][0].cpu(), want_out.double(), tol, tol, "out")
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), "strided vs contiguous B / C"
 
 
 @pytest.mark.parametrize("dt_,rank", [(torch.float32, 48), (torch.bfloat16, 48), (torch.float16, 7)])

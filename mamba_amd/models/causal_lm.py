@@ -136,9 +136,10 @@ class CausalLM(nn.Module):
 class GraphedStep:
     """``CausalLM.step`` for a fixed batch and cache, captured once into a HIP graph.
 
-    A decode step is some ten small launches per block (GEMVs, the conv and
-    state updates, the norm); replaying them as one graph removes the host
-    launch cost.  Each call copies the token ids into the captured input,
+    A decode step is five small launches per block (the norm, the input
+    projection with the conv step, the x-projection, the state update, the
+    output projection); replaying them as one graph removes the host launch
+    cost.  Each call copies the token ids into the captured input,
     replays, and returns the captured logits buffer (overwritten by the next
     call).  The cache tensors are the captured ones: keep using the same
     cache object.  Nothing in a step clears memory with a memset, so the

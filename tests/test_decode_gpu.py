@@ -15,7 +15,12 @@
   agrees with forward() on its own output;
 * GraphedStep (the step captured into a HIP graph): six replays, with eager
   work and synchronisations between them, bit-identical to the eager step
-  (logits and cache).
+  (logits and cache);
+* decode_linear (ss_decode_linear): fixed and 24 seeded random shapes
+  against the fp32 product and the unsplit kernel, the K split (tile
+  counters back at zero, the same bits on a second call, graph replays)
+  and the fused conv step (the bits of decode_linear followed by
+  causal_conv1d_update).
 
 Tolerances: fp32 1e-4 (outputs of a step, relative to the largest
 magnitude where stated), bf16 / fp16 2e-2.
@@ -373,3 +378,46 @@ def test_decode_linear_split_replays_in_a_graph():
         torch.cuda.synchronize()
         assert torch.equal(y, eager), f"replay {rep}"
         _ = (x.float() * 2).sum().item()
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_decode_linear_random_shapes(i):
+    # seeded random shapes through decode_linear (split or not, as the library
+    # decides; the 16- and 8-byte load paths; ragged output and batch tiles;
+    # with and without the fused conv step) against the fp32 product, the
+    # unsplit kernel, and decode_linear followed by causal_conv1d_update (the
+    # same bits)
+    import random
+    from mamba_amd.ops import decode_linear as dlm
+    from mamba_amd.ops.causal_conv1d import causal_conv1d_update
+    rnd = random.Random(700 + i)
+    batch = rnd.choice([1, 2, 5, 16, 17, 33, 64])
+    k = 16 * rnd.choice([1, 2, 3, 5, 8, 24, 48, 96, 128])
+    n = rnd.choice([1, 7, 16, 37, 80, 200, 500, 1008, 1024])
+    dt = rnd.choice([torch.bfloat16, torch.float16])
+    bdt = rnd.choice([None, dt, torch.float32])
+    cdim = rnd.choice([0, 0, n, max(1, n // 2)])
+    width = rnd.choice([2, 3, 4])
+    _say(f"decode linear random {i}: batch {batch} k {k} n {n} {dt} bias {bdt} conv {cdim} width {width}")
+    gen = torch.Generator().manual_seed(800 + i)
+    x = torch.randn(batch, k, generator=gen).to(dt).to(DEV)
+    w = (torch.randn(n, k, generator=gen) / k ** 0.5).to(dt).to(DEV)
+    b = torch.randn(n, generator=gen).to(bdt).to(DEV) if bdt is not None else None
+    assert dlm._fits(x, w, b)
+    want = x.float() @ w.float().t() + (b.float() if b is not None else 0.0)
+    scale = max(1.0, float(want.abs().max()))
+    y1 = dlm.decode_linear(x, w, b)
+    y0 = dlm.decode_linear(x, w, b, split=False)
+    assert_close(y1.float().cpu(), want.cpu(), 1e-2, 1e-2 * scale, "split")
+    assert_close(y0.float().cpu(), want.cpu(), 1e-2, 1e-2 * scale, "unsplit")
+    if cdim:
+        st0 = torch.randn(batch, cdim, width, generator=gen).to(dt).to(DEV)
+        cw = torch.randn(cdim, width, generator=gen).to(DEV)
+        cb = torch.randn(cdim, generator=gen).to(DEV)
+        st_f, st_r = st0.clone(), st0.clone()
+        yf = dlm.decode_linear(x, w, b, conv=(st_f, cw, cb, "silu"))
+        xr = causal_conv1d_update(y1[:, :cdim].contiguous(), st_r, cw, cb, "silu")
+        torch.cuda.synchronize()
+        assert torch.equal(yf[:, :cdim], xr), "fused conv output"
+        assert torch.equal(yf[:, cdim:], y1[:, cdim:]), "outputs past the conv channels"
+        assert torch.equal(st_f, st_r), "conv state"

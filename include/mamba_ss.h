@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 13
+#define SS_ABI_VERSION 14
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -397,7 +397,18 @@ int ss_conv1d_update(const ss_conv1d_update_args* a, void* stream);
  *   y[b, n], the conv state is advanced in place); outputs n >= conv->dim
  *   are written as they are.  This is the block's input projection followed
  *   by its conv step in one launch.  conv->itype must equal dtype,
- *   conv->batch equal batch, conv->dim <= n_out. */
+ *   conv->batch equal batch, conv->dim <= n_out.
+ *
+ * ABI v14 adds norm: when it is not NULL the product's input rows are
+ * norm's output, computed in the same launch as ss_rmsnorm_fwd computes it
+ * (the same bits): x = rmsnorm(norm->x + norm->residual); norm->residual_out
+ * and norm->rstd are written as ss_rmsnorm_fwd writes them, norm->out is
+ * ignored, and the x / x_row_stride fields of this block are not used.  This
+ * is the block's RMSNorm and input projection in one launch.  norm->rows
+ * must equal batch, norm->dim equal k_in (at most 1024), norm->dtype equal
+ * dtype; norm->x, residual and residual_out need 16-byte aligned rows
+ * (bases and row strides), weight 16-byte alignment.  The K split is not
+ * used with it. */
 typedef struct ss_decode_linear_args {
     int64_t batch, n_out, k_in;
     int32_t dtype;                       /* SS_BF16 or SS_F16: x, weight, y */
@@ -410,6 +421,7 @@ typedef struct ss_decode_linear_args {
     void* workspace;                     /* may be NULL (ABI v13) */
     int64_t workspace_bytes;
     const ss_conv1d_update_args* conv;   /* may be NULL (ABI v13) */
+    const ss_rmsnorm_args* norm;         /* may be NULL (ABI v14) */
 } ss_decode_linear_args;
 
 /* Workspace bytes ss_decode_linear can use for this shape (0: none); -1 on

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 13
+ABI_VERSION = 14
 # bytes of the fixed device scratch of ss_bwd_noalloc (SS_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -144,6 +144,7 @@ class DecodeLinearArgs(ctypes.Structure):
         ("x_row_stride", _i64), ("w_row_stride", _i64), ("y_row_stride", _i64),
         ("x", _p), ("weight", _p), ("bias", _p), ("y", _p),
         ("workspace", _p), ("workspace_bytes", _i64), ("conv", ctypes.POINTER(Conv1dUpdateArgs)),
+        ("norm", ctypes.POINTER(RmsNormArgs)),
     ]
 
 

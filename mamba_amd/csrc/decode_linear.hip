@@ -90,16 +90,120 @@ struct LinExtra {
     int64_t kslice;                    // K elements per slice
     int* counters;                     // per tile, in the workspace
     float* partials;                   // (tile, slice, 256) fp32, in the workspace
-    int32_t has_conv, pad_;
+    int32_t has_conv, has_norm;
     ss_conv1d_update_args conv;
+    ss_rmsnorm_args norm;
 };
 
-template <typename T, int NW, int KV>
+// 16-byte vector of T <-> 8 floats (bf16 / fp16 only)
+template <typename T>
+__device__ __forceinline__ void unpack8(const uint4& v, float (&o)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if constexpr (__is_same(T, bf16_t)) {
+            o[2 * k] = __uint_as_float(w[k] << 16);
+            o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+        } else {
+            o[2 * k] = float(__builtin_bit_cast(_Float16, uint16_t(w[k] & 0xffffu)));
+            o[2 * k + 1] = float(__builtin_bit_cast(_Float16, uint16_t(w[k] >> 16)));
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t pack2_io(float lo, float hi) {
+    if constexpr (__is_same(T, bf16_t)) {
+        return io<bf16_t>::pack2(lo, hi);
+    } else {
+        return uint32_t(__builtin_bit_cast(uint16_t, _Float16(lo))) |
+               (uint32_t(__builtin_bit_cast(uint16_t, _Float16(hi))) << 16);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
+    return make_uint4(pack2_io<T>(v[0], v[1]), pack2_io<T>(v[2], v[3]), pack2_io<T>(v[4], v[5]),
+                      pack2_io<T>(v[6], v[7]));
+}
+
+// Rows b0 .. b0 + 15 of the RMSNorm input (x + residual) normalised into xs
+// (rows of ld elements), one wave per row, with the arithmetic of the
+// RMSNorm forward kernel for a row of one register segment: lane l owns the
+// 8-element vectors l and l + 64 of the row (k_in <= 1024), sums s^2 with
+// fmas in element order and then over the wave by xor shuffles, and
+// rounds s = x + residual and the output to T the same way, so the rows
+// equal that kernel's output bit for bit.  With write_s, s goes to
+// residual_out (and 1 / rms to rstd).
+template <typename T>
+__device__ __forceinline__ void norm_rows(const ss_rmsnorm_args& n, int64_t b0, int64_t batch, int64_t k_in,
+                                          uint16_t* xs, int64_t ld, int w, int nw, int lane, bool write_s) {
+    const int64_t nvec = k_in / 8;
+    for (int rr = w; rr < 16; rr += nw) {
+        const int64_t row = b0 + rr;
+        if (row >= batch) break;                       // wave-uniform; no barrier inside
+        const T* xr = static_cast<const T*>(n.x) + row * n.x_row_stride;
+        const T* rr_ = n.residual ? static_cast<const T*>(n.residual) + row * n.residual_row_stride : nullptr;
+        float sv[2][8], w1[2][8];
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int64_t vi = int64_t(k) * 64 + lane;
+            if (vi < nvec) {
+                if (n.w_dtype == SS_F32) {
+                    const float4* wp = reinterpret_cast<const float4*>(static_cast<const float*>(n.weight) + vi * 8);
+                    const float4 w0 = wp[0], w4 = wp[1];
+                    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) w1[k][e] = 1.f + wv[e];
+                } else {
+                    float wv[8];
+                    unpack8<T>(*reinterpret_cast<const uint4*>(static_cast<const T*>(n.weight) + vi * 8), wv);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) w1[k][e] = 1.f + wv[e];
+                }
+                unpack8<T>(*reinterpret_cast<const uint4*>(xr + vi * 8), sv[k]);
+                if (rr_) {
+                    float rv[8];
+                    unpack8<T>(*reinterpret_cast<const uint4*>(rr_ + vi * 8), rv);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sv[k][e] = round_io<T>(sv[k][e] + rv[e]);
+                    if (write_s && n.residual_out)
+                        *reinterpret_cast<uint4*>(static_cast<T*>(n.residual_out) + row * n.residual_out_row_stride +
+                                                  vi * 8) = pack8<T>(sv[k]);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(sv[k][e], sv[k][e], acc);
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+        const float rstd = rsqrtf(acc / float(k_in) + n.eps);
+        if (write_s && n.rstd && lane == 0) n.rstd[row] = rstd;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int64_t vi = int64_t(k) * 64 + lane;
+            if (vi < nvec) {
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (sv[k][e] * rstd) * w1[k][e];
+                *reinterpret_cast<uint4*>(xs + rr * ld + vi * 8) = pack8<T>(o);
+            }
+        }
+    }
+}
+
+// kNorm: the input rows are computed in the kernel by the RMSNorm of
+// e.norm (x + residual) and read from LDS (extern xs, 16 rows of k_in + 8
+// elements: the padding puts the 16 rows of a 16-byte read on different
+// banks)
+template <typename T, int NW, int KV, bool kNorm>
 __global__ __launch_bounds__(64 * NW) void decode_linear_kernel(const ss_decode_linear_args a, const LinExtra e) {
     constexpr int KS = 4 * KV;                        // k per step: 16 or 32
     constexpr int kBatch = KV == 8 ? 8 : 16;          // steps of a wave in flight at once
     __shared__ float part[NW * 256];
     __shared__ int last;
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int i = lane & 15, q = lane >> 4;
     const int64_t tile_n = blockIdx.x / e.ksplit, kidx = blockIdx.x % e.ksplit;
@@ -107,7 +211,9 @@ __global__ __launch_bounds__(64 * NW) void decode_linear_kernel(const ss_decode_
     const int64_t n = n0 + i, b = b0 + i;
     const bool nv = n < a.n_out, bv = b < a.batch;
     const uint16_t* wrow = static_cast<const uint16_t*>(a.weight) + (nv ? n : 0) * a.w_row_stride + KV * q;
-    const uint16_t* xrow = static_cast<const uint16_t*>(a.x) + (bv ? b : 0) * a.x_row_stride + KV * q;
+    const int64_t xld = a.k_in + 8;
+    const uint16_t* xrow = kNorm ? xs + i * xld + KV * q
+                                 : static_cast<const uint16_t*>(a.x) + (bv ? b : 0) * a.x_row_stride + KV * q;
     // this workgroup's K steps: [kb, ke) (slices are whole steps)
     const int64_t kb = kidx * e.kslice / KS;
     const int64_t kend = (kidx + 1) * e.kslice < a.k_in ? (kidx + 1) * e.kslice : a.k_in;
@@ -115,13 +221,28 @@ __global__ __launch_bounds__(64 * NW) void decode_linear_kernel(const ss_decode_
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     // kBatch steps of this wave are requested before any is used; steps past
     // the end read the last step again and are zeroed
-    for (int64_t kt0 = kb + w; kt0 < ke; kt0 += NW * kBatch) {
-        rowvec<KV> av[kBatch], xv[kBatch];
+    rowvec<KV> av[kBatch], xv[kBatch];
+    auto load_w = [&](int64_t kt0) {
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int64_t kt = kt0 + NW * u;
             const int64_t kc = kt < ke ? kt : ke - 1;
             av[u] = *reinterpret_cast<const rowvec<KV>*>(wrow + kc * KS);
+        }
+    };
+    if constexpr (kNorm) {
+        // the first batch of weights is requested before the rows are
+        // normalised, so the two waits for memory overlap
+        if (kb + w < ke) load_w(kb + w);
+        norm_rows<T>(e.norm, b0, a.batch, a.k_in, xs, xld, w, NW, lane, blockIdx.x == 0);
+        __syncthreads();
+    }
+    for (int64_t kt0 = kb + w; kt0 < ke; kt0 += NW * kBatch) {
+        if (!kNorm || kt0 != kb + w) load_w(kt0);
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int64_t kt = kt0 + NW * u;
+            const int64_t kc = kt < ke ? kt : ke - 1;
             xv[u] = *reinterpret_cast<const rowvec<KV>*>(xrow + kc * KS);
         }
 #pragma unroll
@@ -219,19 +340,28 @@ __global__ __launch_bounds__(64 * NW) void decode_linear_kernel(const ss_decode_
     io<T>::store(static_cast<T*>(a.y) + ob * a.y_row_stride + on, o);
 }
 
-template <typename T, int KV>
-void launch_kv(const ss_decode_linear_args* a, const LinExtra& e, hipStream_t stream) {
+template <typename T, int KV, bool kNorm>
+void launch_kvn(const ss_decode_linear_args* a, const LinExtra& e, hipStream_t stream) {
     const dim3 grid{unsigned((a->n_out + 15) / 16 * e.ksplit), unsigned((a->batch + 15) / 16)};
     const int64_t steps = (e.kslice + 4 * KV - 1) / (4 * KV);   // K steps per workgroup
-    if (steps <= 16) hipLaunchKernelGGL((decode_linear_kernel<T, 4, KV>), grid, dim3(256), 0, stream, *a, e);
-    else if (steps <= 32) hipLaunchKernelGGL((decode_linear_kernel<T, 8, KV>), grid, dim3(512), 0, stream, *a, e);
-    else hipLaunchKernelGGL((decode_linear_kernel<T, 16, KV>), grid, dim3(1024), 0, stream, *a, e);
+    const size_t lds = kNorm ? size_t(16 * (a->k_in + 8) * 2) : 0;
+    if (steps <= 16) hipLaunchKernelGGL((decode_linear_kernel<T, 4, KV, kNorm>), grid, dim3(256), lds, stream, *a, e);
+    else if (steps <= 32) hipLaunchKernelGGL((decode_linear_kernel<T, 8, KV, kNorm>), grid, dim3(512), lds, stream, *a, e);
+    else hipLaunchKernelGGL((decode_linear_kernel<T, 16, KV, kNorm>), grid, dim3(1024), lds, stream, *a, e);
+}
+
+template <typename T, int KV>
+void launch_kv(const ss_decode_linear_args* a, const LinExtra& e, hipStream_t stream) {
+    if (e.has_norm) launch_kvn<T, KV, true>(a, e, stream);
+    else launch_kvn<T, KV, false>(a, e, stream);
 }
 
 template <typename T>
 void launch_t(const ss_decode_linear_args* a, const LinExtra& e, hipStream_t stream) {
-    const bool wide = a->k_in % 32 == 0 && a->x_row_stride % 8 == 0 && a->w_row_stride % 8 == 0 &&
-                      (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->weight) & 15) == 0;
+    // (with the norm the rows come from LDS, 16-byte aligned)
+    const bool xok = e.has_norm || (a->x_row_stride % 8 == 0 && (reinterpret_cast<uintptr_t>(a->x) & 15) == 0);
+    const bool wide = a->k_in % 32 == 0 && xok && a->w_row_stride % 8 == 0 &&
+                      (reinterpret_cast<uintptr_t>(a->weight) & 15) == 0;
     if (wide) launch_kv<T, 8>(a, e, stream);
     else launch_kv<T, 4>(a, e, stream);
 }
@@ -259,7 +389,7 @@ hipError_t decode_linear_launch(const ss_decode_linear_args* a, hipStream_t stre
     e.ksplit = 1;
     e.kslice = a->k_in;
     const DecodeLinearSplit sp = decode_linear_split(a->batch, a->n_out, a->k_in);
-    if (a->workspace && sp.ksplit > 1 && a->workspace_bytes >= sp.workspace_bytes) {
+    if (a->workspace && sp.ksplit > 1 && a->workspace_bytes >= sp.workspace_bytes && !a->norm) {
         e.ksplit = sp.ksplit;
         e.kslice = sp.kslice;
         e.counters = static_cast<int*>(a->workspace);
@@ -268,6 +398,10 @@ hipError_t decode_linear_launch(const ss_decode_linear_args* a, hipStream_t stre
     if (a->conv) {
         e.has_conv = 1;
         e.conv = *a->conv;
+    }
+    if (a->norm) {
+        e.has_norm = 1;
+        e.norm = *a->norm;
     }
     if (a->dtype == SS_BF16) launch_t<bf16_t>(a, e, stream);
     else launch_t<_Float16>(a, e, stream);

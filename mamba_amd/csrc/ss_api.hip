@@ -635,16 +635,37 @@ int ss_decode_linear(const ss_decode_linear_args* a, void* stream) {
                 if (v < 0) return fail(SS_ERR_INVALID, "negative conv stride");
         }
     }
+    if (const ss_rmsnorm_args* n = a->norm) {
+        if (n->rows != a->batch || n->dim != a->k_in)
+            return fail(SS_ERR_INVALID, "norm rows=%lld dim=%lld must equal batch=%lld and k_in=%lld",
+                        (long long)n->rows, (long long)n->dim, (long long)a->batch, (long long)a->k_in);
+        if (n->dtype != a->dtype) return fail(SS_ERR_INVALID, "norm dtype %d differs from dtype %d", n->dtype, a->dtype);
+        if (n->w_dtype != a->dtype && n->w_dtype != SS_F32)
+            return fail(SS_ERR_UNSUPPORTED, "norm weight dtype %d must be the row dtype or fp32", n->w_dtype);
+        if (a->k_in > 1024) return fail(SS_ERR_UNSUPPORTED, "the fused norm takes k_in <= 1024 (k_in=%lld)", (long long)a->k_in);
+        if (!(n->eps >= 0.f)) return fail(SS_ERR_INVALID, "norm eps must be >= 0");
+        if (a->batch > 0) {
+            if (!n->x || !n->weight) return fail(SS_ERR_INVALID, "norm x / weight is NULL");
+            const bool rows16 = aligned(n->x, 16) && n->x_row_stride % 8 == 0 && n->x_row_stride >= n->dim &&
+                                (!n->residual || (aligned(n->residual, 16) && n->residual_row_stride % 8 == 0 &&
+                                                  n->residual_row_stride >= n->dim)) &&
+                                (!n->residual || !n->residual_out ||
+                                 (aligned(n->residual_out, 16) && n->residual_out_row_stride % 8 == 0 &&
+                                  n->residual_out_row_stride >= n->dim)) &&
+                                aligned(n->weight, 16) && (!n->rstd || aligned(n->rstd, 4));
+            if (!rows16) return fail(SS_ERR_INVALID, "the fused norm needs 16-byte aligned rows covering dim");
+        }
+    }
     if (a->batch == 0 || a->n_out == 0) return ok();
     if (a->k_in == 0) return fail(SS_ERR_UNSUPPORTED, "k_in=0");
     if ((a->n_out + 15) / 16 * ss::kLinMaxSplit > INT32_MAX || (a->batch + 15) / 16 > 65535)
         return fail(SS_ERR_UNSUPPORTED, "n_out or batch too large");
-    if (!a->x || !a->weight || !a->y) return fail(SS_ERR_INVALID, "x / weight / y is NULL");
-    if (!aligned(a->x, 8) || !aligned(a->weight, 8) || !aligned(a->y, 2))
+    if ((!a->norm && !a->x) || !a->weight || !a->y) return fail(SS_ERR_INVALID, "x / weight / y is NULL");
+    if ((!a->norm && !aligned(a->x, 8)) || !aligned(a->weight, 8) || !aligned(a->y, 2))
         return fail(SS_ERR_INVALID, "x / weight must be 8-byte aligned, y 2-byte aligned");
     if (a->bias && !aligned(a->bias, a->bias_dtype == SS_F32 ? 4 : 2)) return fail(SS_ERR_INVALID, "bias is misaligned");
-    if (a->x_row_stride < a->k_in || a->w_row_stride < a->k_in || a->y_row_stride < a->n_out ||
-        a->x_row_stride % 4 || a->w_row_stride % 4)
+    if ((!a->norm && (a->x_row_stride < a->k_in || a->x_row_stride % 4)) || a->w_row_stride < a->k_in ||
+        a->y_row_stride < a->n_out || a->w_row_stride % 4)
         return fail(SS_ERR_INVALID, "row strides must cover the rows, x / weight strides multiples of 4");
     hipError_t e = ss::decode_linear_launch(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "decode linear launch failed: %s", hipGetErrorString(e));

@@ -100,8 +100,10 @@ class CausalLM(nn.Module):
         hidden_states = self.embedding(input_ids)
         residual = None
         for layer, (conv_state, ssm_state) in zip(self.layers, inference_cache):
-            normed, residual = layer.norm(hidden_states, residual=residual, prenorm=True)
-            hidden_states = layer.dropout(layer.mamba.step(normed, conv_state, ssm_state))
+            # normed, residual = layer.norm(hidden_states, residual, prenorm=True), then
+            # the block step on normed: one call, the norm inside the input projection
+            out, residual = layer.mamba.step_prenorm(hidden_states, residual, layer.norm, conv_state, ssm_state)
+            hidden_states = layer.dropout(out)
         return self.lm_head(self.norm(hidden_states, residual=residual))
 
     @torch.no_grad()
@@ -136,8 +138,8 @@ class CausalLM(nn.Module):
 class GraphedStep:
     """``CausalLM.step`` for a fixed batch and cache, captured once into a HIP graph.
 
-    A decode step is five small launches per block (the norm, the input
-    projection with the conv step, the x-projection, the state update, the
+    A decode step is four small launches per block (the norm, input
+    projection and conv step in one, the x-projection, the state update, the
     output projection); replaying them as one graph removes the host launch
     cost.  Each call copies the token ids into the captured input,
     replays, and returns the captured logits buffer (overwritten by the next

@@ -134,6 +134,35 @@ class MambaSimple(nn.Module):
         # already the conv output (the conv state advanced), xz[:, inner:] is z
         xz = decode_linear(h, self.input_proj.weight, self.input_proj.bias,
                            conv=(conv_state, conv_w, conv_b, "silu"))                # (batch, 2 * inner)
+        out = self._step_tail(xz, ssm_state)
+        return out.unsqueeze(1) if squeeze else out
+
+    def step_prenorm(self, hidden_states, residual, norm, conv_state, ssm_state):
+        """step() of ``norm(hidden_states, residual=residual, prenorm=True)``'s output
+        (the block's RMSNorm in front of it, as CausalLM's blocks apply it): returns
+        (out, hidden_states + residual), the second the residual stream the prenorm
+        RMSNorm returns (hidden_states itself without residual).  With the norm's
+        fast path the RMSNorm runs inside the input projection's launch."""
+        squeeze = hidden_states.dim() == 3
+        h = hidden_states.reshape(-1, self.model_dim)
+        r = residual.reshape(-1, self.model_dim) if residual is not None else None
+        A, D, dt_bias, conv_w, conv_b = self._decode_params()
+        conv = (conv_state, conv_w, conv_b, "silu")
+        if norm.use_fast_path and h.is_cuda:
+            xz, s = decode_linear(h, self.input_proj.weight, self.input_proj.bias, conv=conv,
+                                  norm=(r, norm.weight, norm.eps))
+        else:
+            normed, s = norm(h, residual=r, prenorm=True)
+            xz = decode_linear(normed, self.input_proj.weight, self.input_proj.bias, conv=conv)
+        out = self._step_tail(xz, ssm_state)
+        if squeeze:
+            return out.unsqueeze(1), s.view(hidden_states.shape)
+        return out, s.view(hidden_states.shape)
+
+    def _step_tail(self, xz, ssm_state):
+        """The step after the input projection and conv: xz (batch, 2 * inner) holds the
+        conv output and z; returns the block output (batch, model_dim)."""
+        A, D, dt_bias, _, _ = self._decode_params()
         x, z = xz[:, :self.inner_dim], xz[:, self.inner_dim:]
         x_db = decode_linear(x, self.ssm_param_proj.weight)                          # (batch, R + 2N)
         R, N = self.delta_rank, self.state_dim
@@ -141,8 +170,7 @@ class MambaSimple(nn.Module):
         # update; its bias goes in there too
         y = selective_state_update(ssm_state, x, (x_db[:, :R], self.delta_proj.weight), A, x_db[:, R:R + N],
                                    x_db[:, R + N:], D, z=z, dt_bias=dt_bias, dt_softplus=True)
-        out = decode_linear(y, self.output_proj.weight, self.output_proj.bias)
-        return out.unsqueeze(1) if squeeze else out
+        return decode_linear(y, self.output_proj.weight, self.output_proj.bias)
 
     def _decode_params(self):
         """A = -exp(log_A), D, the delta bias and the conv weight / bias in fp32, computed

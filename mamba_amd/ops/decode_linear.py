@@ -14,6 +14,14 @@ by ``causal_conv1d_update`` of the product rounded to x's dtype (the conv
 state advances in place), the rest are returned as they are.  This is the
 block's input projection and conv update in one launch.
 
+``norm=(residual, norm_weight, eps)`` fuses the RMSNorm in front of the
+product: x is then the RMSNorm input, the product's input rows are
+``rms_norm_fn(x, norm_weight, residual, eps, prenorm=True)``'s output, bit for
+bit, computed in the same launch, and the call returns ``(y, s)`` with s =
+x + residual (x itself without residual), the residual stream that the
+prenorm RMSNorm returns.  Shapes the fused launch does not take (rows that
+are not 16-byte aligned, k_in above 1024) run the RMSNorm kernel first.
+
 The split needs a small workspace (its tile counters and fp32 partial tiles,
 at most about 0.5 MiB); one is kept per (device, stream), allocated zeroed
 the first time that stream calls outside a graph capture, and reused by every
@@ -80,9 +88,27 @@ def _conv_args(conv, batch, n_out, dtype, device):
     return c, (w, b)
 
 
-def decode_linear(x, weight, bias=None, conv=None, split=True):
+def _rows16(t):
+    return t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+
+
+def _norm_fits(x, residual, norm_weight):
+    return (x.shape[1] <= 1024 and _rows16(x) and (residual is None or (
+                residual.shape == x.shape and residual.dtype == x.dtype and _rows16(residual)))
+            and norm_weight.dim() == 1 and norm_weight.shape[0] == x.shape[1]
+            and norm_weight.dtype in (x.dtype, torch.float32) and norm_weight.is_contiguous()
+            and norm_weight.data_ptr() % 16 == 0)
+
+
+def decode_linear(x, weight, bias=None, conv=None, split=True, norm=None):
     """See the module docstring; ``split=False`` runs without the K split (one
     workgroup per output tile)."""
+    if norm is not None:
+        residual, norm_weight, eps = norm
+        if not (_fits(x, weight, bias) and _norm_fits(x, residual, norm_weight)):
+            from .rms_norm import rms_norm_fn
+            normed, s = rms_norm_fn(x, norm_weight, residual, eps, prenorm=True)
+            return decode_linear(normed, weight, bias, conv=conv, split=split), s
     if not _fits(x, weight, bias):
         y = F.linear(x, weight, bias)
         if conv is not None:
@@ -103,6 +129,21 @@ def decode_linear(x, weight, bias=None, conv=None, split=True):
     if conv is not None:
         c, keep = _conv_args(conv, batch, n_out, x.dtype, x.device)
         a.conv = ctypes.pointer(c)
+    s = None
+    if norm is not None:
+        residual, norm_weight, eps = norm
+        s = torch.empty_like(x) if residual is not None else x
+        na = nat.RmsNormArgs()
+        na.rows, na.dim = batch, k_in
+        na.dtype, na.w_dtype = _ITYPES[x.dtype], _ITYPES[norm_weight.dtype]
+        na.eps = float(eps)
+        na.x_row_stride = x.stride(0)
+        if residual is not None:
+            na.residual_row_stride, na.residual_out_row_stride = residual.stride(0), s.stride(0)
+            na.residual, na.residual_out = _ptr(residual), _ptr(s)
+        na.x, na.weight = _ptr(x), _ptr(norm_weight)
+        a.norm = ctypes.pointer(na)
+        a.x, a.x_row_stride = None, 0
     with torch.cuda.device(x.device):
         if split and lib.ss_decode_linear_workspace_bytes(ctypes.byref(a)) > 0:
             ws = _workspace(x.device)
@@ -110,4 +151,4 @@ def decode_linear(x, weight, bias=None, conv=None, split=True):
                 a.workspace, a.workspace_bytes = _ptr(ws), ws.numel()
         nat.check(lib.ss_decode_linear(ctypes.byref(a), _stream(x.device)), "decode_linear")
     del keep
-    return y
+    return (y, s) if norm is not None else y

@@ -60,7 +60,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 13
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 14
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""

@@ -20,7 +20,8 @@
   against the fp32 product and the unsplit kernel, the K split (tile
   counters back at zero, the same bits on a second call, graph replays)
   and the fused conv step (the bits of decode_linear followed by
-  causal_conv1d_update).
+  causal_conv1d_update); the fused RMSNorm (the bits of rms_norm_fn
+  followed by decode_linear, output, residual stream and conv state).
 
 Tolerances: fp32 1e-4 (outputs of a step, relative to the largest
 magnitude where stated), bf16 / fp16 2e-2.
@@ -421,3 +422,48 @@ def test_decode_linear_random_shapes(i):
         assert torch.equal(yf[:, :cdim], xr), "fused conv output"
         assert torch.equal(yf[:, cdim:], y1[:, cdim:]), "outputs past the conv channels"
         assert torch.equal(st_f, st_r), "conv state"
+
+
+NORM_CASES = [
+    # batch, k_in, n_out, residual, norm weight dtype (None: the row dtype), conv channels, dtype
+    (16, 768, 3072, True, None, 1536, torch.bfloat16),       # the LM block's norm + input projection + conv
+    (16, 768, 3072, False, None, 1536, torch.bfloat16),      # the first block: no residual yet
+    (5, 1024, 200, True, torch.float32, 0, torch.bfloat16),  # fp32 weight, ragged tiles, the largest fused k_in
+    (33, 256, 64, True, None, 32, torch.float16),            # 3 batch tiles
+    (16, 1536, 128, True, None, 0, torch.bfloat16),          # k_in above 1024: the RMSNorm kernel first
+]
+
+
+@pytest.mark.parametrize("case", NORM_CASES, ids=[f"b{c[0]}-k{c[1]}-n{c[2]}{'-res' if c[3] else ''}"
+                                                  f"{'-w32' if c[4] else ''}-conv{c[5]}" for c in NORM_CASES])
+def test_decode_linear_fused_norm(case):
+    # the RMSNorm inside the product's launch against rms_norm_fn (prenorm)
+    # followed by decode_linear: the same bits for the output, the residual
+    # stream and the conv state
+    from mamba_amd.ops import decode_linear as dlm
+    from mamba_amd.ops.rms_norm import rms_norm_fn
+    batch, k, n, with_res, wdt, cdim, dt = case
+    _say(f"decode linear with fused norm {case}")
+    gen = torch.Generator().manual_seed(900 + k + n + batch)
+    x = torch.randn(batch, k, generator=gen).to(dt).to(DEV)
+    res = torch.randn(batch, k, generator=gen).to(dt).to(DEV) if with_res else None
+    nw = (0.1 * torch.randn(k, generator=gen)).to(wdt or dt).to(DEV)
+    w = (torch.randn(n, k, generator=gen) / k ** 0.5).to(dt).to(DEV)
+    b = torch.randn(n, generator=gen).to(dt).to(DEV)
+    conv = None
+    if cdim:
+        st0 = torch.randn(batch, cdim, 4, generator=gen).to(dt).to(DEV)
+        cw, cb = torch.randn(cdim, 4, generator=gen).to(DEV), torch.randn(cdim, generator=gen).to(DEV)
+    st_f = st0.clone() if cdim else None
+    y, s = dlm.decode_linear(x, w, b, conv=(st_f, cw, cb, "silu") if cdim else None, norm=(res, nw, 1e-5))
+    normed, s_r = rms_norm_fn(x, nw, res, 1e-5, prenorm=True)
+    st_r = st0.clone() if cdim else None
+    # (unsplit: the fused launch does not split K, so the sums run in its order)
+    y_r = dlm.decode_linear(normed, w, b, conv=(st_r, cw, cb, "silu") if cdim else None, split=False)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_r), "residual stream"
+    assert torch.equal(y, y_r), "output"
+    if cdim:
+        assert torch.equal(st_f, st_r), "conv state"
+    want = normed.float() @ w.float().t() + b.float()
+    assert_close(y[:, cdim:].float().cpu(), want[:, cdim:].cpu(), 1e-2, 1e-2 * float(want.abs().max()), "vs fp32")

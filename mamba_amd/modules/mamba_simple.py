@@ -129,7 +129,7 @@ class MambaSimple(nn.Module):
         shape; conv_state and ssm_state are advanced in place."""
         squeeze = hidden_states.dim() == 3
         h = hidden_states.reshape(-1, self.model_dim)
-        A, D, dt_bias, conv_w, conv_b = self._decode_params()
+        *_, conv_w, conv_b = self._decode_params()
         # the input projection with the conv step fused in: xz[:, :inner] is
         # already the conv output (the conv state advanced), xz[:, inner:] is z
         xz = decode_linear(h, self.input_proj.weight, self.input_proj.bias,
@@ -146,7 +146,7 @@ class MambaSimple(nn.Module):
         squeeze = hidden_states.dim() == 3
         h = hidden_states.reshape(-1, self.model_dim)
         r = residual.reshape(-1, self.model_dim) if residual is not None else None
-        A, D, dt_bias, conv_w, conv_b = self._decode_params()
+        *_, conv_w, conv_b = self._decode_params()
         conv = (conv_state, conv_w, conv_b, "silu")
         if norm.use_fast_path and h.is_cuda:
             xz, s = decode_linear(h, self.input_proj.weight, self.input_proj.bias, conv=conv,

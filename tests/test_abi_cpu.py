@@ -521,6 +521,72 @@ def test_decode_linear_workspace_query(nat, lib):
         assert q(batch, n_out, k_in) <= 1 << 20                # the Python layer's per-stream workspace
 
 
+def valid_linear(nat, batch=16, n_out=3072, k_in=768):
+    a = nat.DecodeLinearArgs()
+    a.batch, a.n_out, a.k_in = batch, n_out, k_in
+    a.dtype = a.bias_dtype = nat.SS_BF16
+    a.x_row_stride, a.w_row_stride, a.y_row_stride = k_in, k_in, n_out
+    a.x, a.weight, a.y = FAKE, FAKE + (1 << 24), FAKE + (1 << 25)
+    return a
+
+
+@pytest.mark.parametrize("case", ["conv_itype", "conv_batch", "conv_dim", "conv_width", "conv_null_state",
+                                  "norm_rows", "norm_dim", "norm_k_in", "norm_dtype", "norm_w_dtype",
+                                  "norm_misaligned", "norm_stride", "norm_neg_eps", "ws_misaligned", "ws_neg",
+                                  "k_in", "null_y"])
+def test_decode_linear_rejects(nat, lib, case):
+    # every check runs before any device work, so these calls need no GPU
+    a = valid_linear(nat)
+    c = nat.Conv1dUpdateArgs()
+    c.batch, c.dim, c.width, c.itype, c.has_bias, c.silu = 16, 1536, 4, nat.SS_BF16, 1, 1
+    c.state_batch_stride, c.state_dim_stride, c.state_width_stride = 1536 * 4, 4, 1
+    c.w_dim_stride, c.w_width_stride = 4, 1
+    c.conv_state, c.weight, c.bias = FAKE + (1 << 26), FAKE + (1 << 27), FAKE + (1 << 28)
+    n = valid_norm(nat, rows=16, dim=768)
+    if case.startswith("conv"):
+        a.conv = ctypes.pointer(c)
+        if case == "conv_itype":
+            c.itype = nat.SS_F16
+        elif case == "conv_batch":
+            c.batch = 15
+        elif case == "conv_dim":
+            c.dim = 3073
+        elif case == "conv_width":
+            c.width = 5
+        elif case == "conv_null_state":
+            c.conv_state = None
+    elif case.startswith("norm"):
+        a.norm = ctypes.pointer(n)
+        if case == "norm_rows":
+            n.rows = 8
+        elif case == "norm_dim":
+            n.dim = 512
+        elif case == "norm_k_in":
+            a.k_in = n.dim = 1536
+            a.x_row_stride = a.w_row_stride = 1536
+        elif case == "norm_dtype":
+            n.dtype = nat.SS_F16
+        elif case == "norm_w_dtype":
+            n.w_dtype = nat.SS_F16
+        elif case == "norm_misaligned":
+            n.residual = FAKE + 8
+        elif case == "norm_stride":
+            n.x_row_stride = 772                       # rows not 16-byte aligned
+        elif case == "norm_neg_eps":
+            n.eps = -1.0
+    elif case == "ws_misaligned":
+        a.workspace, a.workspace_bytes = FAKE + 4, 1 << 20
+    elif case == "ws_neg":
+        a.workspace, a.workspace_bytes = FAKE, -1
+    elif case == "k_in":
+        a.k_in = 24
+    elif case == "null_y":
+        a.y = None
+    rc = lib.ss_decode_linear(ctypes.byref(a), None)
+    assert rc in (nat.SS_ERR_INVALID, nat.SS_ERR_UNSUPPORTED), case
+    assert lib.ss_last_error().decode()
+
+
 def test_rmsnorm_python_boundary_refuses_cpu_tensors():
     from mamba_amd.ops.rms_norm import rms_norm_fn
     with pytest.raises(ValueError, match="no CPU path"):

@@ -23,7 +23,7 @@ prenorm RMSNorm returns.  Shapes the fused launch does not take (rows that
 are not 16-byte aligned, k_in above 1024) run the RMSNorm kernel first.
 
 The split needs a small workspace (its tile counters and fp32 partial tiles,
-at most about 0.5 MiB); one is kept per (device, stream), allocated zeroed
+at most about 0.25 MiB); one is kept per (device, stream), allocated zeroed
 the first time that stream calls outside a graph capture, and reused by every
 later call on it, captured ones included (the kernel leaves it ready for the
 next call).  A call captured on a stream that has none yet runs without the
@@ -41,7 +41,7 @@ from ..selective_scan import _ITYPES, _ptr, _stream
 from .causal_conv1d import _params32, _require, _silu_flag, causal_conv1d_update
 
 _MAX_ROWS = 64
-_WS_BYTES = 1 << 20            # covers every split the library picks (at most 512 tiles x 1 KiB + counters)
+_WS_BYTES = 1 << 20            # covers every split the library picks (at most 63 tiles x 4 slices x 1 KiB + counters)
 _workspaces = {}
 _ws_lock = threading.Lock()
 

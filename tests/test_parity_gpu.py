@@ -34,6 +34,9 @@ CASES = [
     (1, 16, 4, 50, torch.float32, 1, True, True, True, True, True, True),       # dstate 4
     (1, 16, 32, 50, torch.float32, 1, True, True, True, True, True, True),      # dstate 32 (2 state groups)
     (1, 16, 64, 40, torch.float32, 1, True, True, True, True, True, True),      # dstate 64
+    (1, 16, 128, 40, torch.float32, 1, True, True, True, True, True, True),     # dstate 128
+    (1, 16, 200, 37, torch.float32, 1, True, True, True, True, True, True),     # dstate 200 (partial state group)
+    (2, 16, 256, 33, torch.float32, 1, True, True, True, True, True, True),     # dstate 256, the largest
     (2, 64, 16, 256, torch.bfloat16, 1, True, True, True, True, True, True),    # bf16 I/O
     (1, 32, 16, 70, torch.float16, 1, True, True, True, True, True, True),      # fp16 I/O
     # fast path: dstate 16, variable B/C, 16-channel groups

@@ -105,6 +105,27 @@ def test_selective_scan_fn_matches_oracle(case):
         assert_close(grads[k], gr, rtol, atol, f"d{k}")
 
 
+@pytest.mark.parametrize("shape", [(2, 64, 16, 256), (1, 16, 32, 50)], ids=["fast", "general"])
+def test_softplus_above_its_threshold(shape):
+    # step sizes well past the softplus threshold (delta + bias > 20, where
+    # softplus(x) is taken as x and its derivative as 1, forward_kernel.cu:217-221
+    # and backward_kernel.cu:512-514) mixed with ordinary ones, on the fast and
+    # the general kernels, against the float64 oracle
+    b, d, n, l = shape
+    print(f"\n[parity] softplus threshold {shape}", flush=True)
+    sys.stdout.flush()
+    x = make_inputs(b, d, n, l, seed=4321)
+    gen = torch.Generator().manual_seed(4322)
+    big = torch.rand(x["delta"].shape, generator=gen) < 0.3
+    x["delta"] = torch.where(big, 20.0 + 15.0 * torch.rand(x["delta"].shape, generator=gen), x["delta"])
+    assert bool((x["delta"] + x["delta_bias"][None, :, None] > 20).any())
+    out, grads = _run_gpu(x, torch.device("cuda:0"), True)
+    ref, rgrads = oracle_fwd_bwd(x, delta_softplus=True)
+    assert_close(out, ref, 1e-3, 1e-3, "out")
+    for k, gr in rgrads.items():
+        assert_close(grads[k], gr, 1e-3, 1e-3, f"d{k}")
+
+
 def test_reference_surface_SelectiveScanFn():
     """SelectiveScanFn.apply with the reference's 8 positional args (modules/mamba_simple.py:131-140)."""
     from mamba_amd.ops.selective_scan_interface import SelectiveScanFn

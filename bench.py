@@ -34,7 +34,8 @@ SelectiveScanFn, the residual added after each block).
       as for the scan;
   causal_lm_24x768_b16_decode_bf16   single-token decode of that model for 16
       sequences after a 128-token prompt; ``value`` is tokens per second of
-      the step replayed as one HIP graph (the eager step beside it).
+      the step replayed as one HIP graph (the eager step beside it);
+      ``..._b1_decode_bf16`` and ``..._b64_decode_bf16``: 1 and 64 sequences.
 
 ``--calibrate-copy MIB`` instead times a plain device-to-device copy of MIB
 MiB (torch's copy kernel); under ``rocprofv3 --pmc FETCH_SIZE`` /
@@ -198,6 +199,8 @@ def norm_cpu_baseline(rows, dim, dtype_name, sample_rows=None, reps=3):
 DECODE_WORKLOADS = {
     # name: (batch, prompt, d_model, layers, vocab)
     "causal_lm_24x768_b16_decode_bf16": (16, 128, 768, 24, 50280),
+    "causal_lm_24x768_b1_decode_bf16": (1, 128, 768, 24, 50280),
+    "causal_lm_24x768_b64_decode_bf16": (64, 128, 768, 24, 50280),
 }
 
 

@@ -286,20 +286,22 @@ __device__ __forceinline__ void bwd_rows_resident(const NormParams& p, float* s_
             }
         }
     }
-    // fold this wave's column sums into the workgroup's
+    // this wave's column sums into its own LDS region (plain stores: no
+    // other wave writes there)
 #pragma unroll
     for (int k = 0; k < kNSB; ++k) {
         const int64_t vi = int64_t(k) * 64 + lane;
         if (vi < nvec) {
 #pragma unroll
-            for (int e = 0; e < VE; ++e) atomicAdd(&s_dw[e * nvec + vi], acc[k][e]);
+            for (int e = 0; e < VE; ++e) s_dw[e * nvec + vi] = acc[k][e];
         }
     }
 }
 
 // Backward rows of any length: segments of kNSB vectors per lane, the
 // second pass re-reading a row longer than one segment from L2, dweight
-// column sums added into LDS per row.
+// column sums added into the wave's LDS region per row (a wave's own LDS
+// operations execute in order, so each sum is formed in row order).
 template <typename T, typename TW, int VE>
 __device__ __forceinline__ void bwd_rows_general(const NormParams& p, float* s_dw, int lane, int64_t nvec,
                                                  int64_t row0, int64_t rstride) {
@@ -356,34 +358,53 @@ __device__ __forceinline__ void bwd_rows_general(const NormParams& p, float* s_d
                     }
                     vstore<T, VE>(dxr + vi * VE, o);
 #pragma unroll
-                    for (int e = 0; e < VE; ++e) atomicAdd(&s_dw[e * nvec + vi], dy[k][e] * (s[k][e] * rstd));
+                    for (int e = 0; e < VE; ++e) s_dw[e * nvec + vi] += dy[k][e] * (s[k][e] * rstd);
                 }
             }
         }
     }
 }
 
-// Column c = vi * VE + e of the workgroup's dweight sums lives in LDS at
-// s_dw[e * nvec + vi], so the 64 lanes of one LDS add touch 64 consecutive
-// words (no bank conflicts); the workgroup writes them to its row of the
-// workspace in column order.  kResident: every row fits one register
-// segment (bwd_rows_resident), else bwd_rows_general.
+// Each wave of the workgroup (blockDim.x / 64 of them, at most kBwdWaves)
+// sums its rows' dweight terms into its own LDS region of dim floats;
+// column c = vi * VE + e lives at region[e * nvec + vi], so the 64 lanes of
+// one LDS access touch 64 consecutive words (no bank conflicts).  The
+// workgroup then writes region 0 + region 1 + ... (in wave order) to its
+// row of the workspace, so every sum has a fixed order and dweight is the
+// same bits on every run.  kResident: every row fits one register segment
+// (bwd_rows_resident), else bwd_rows_general.
 template <typename T, typename TW, int VE, bool kResident>
 __global__ __launch_bounds__(64 * kBwdWaves) void rmsnorm_bwd_kernel(const NormParams p) {
-    extern __shared__ float s_dw[];                     // (dim) column sums of this workgroup
-    for (int64_t c = threadIdx.x; c < p.dim; c += 64 * kBwdWaves) s_dw[c] = 0.f;
+    extern __shared__ float s_dw[];                     // (waves, dim) column sums of each wave
+    const int nw = int(blockDim.x >> 6);
+    for (int64_t c = threadIdx.x; c < int64_t(nw) * p.dim; c += blockDim.x) s_dw[c] = 0.f;
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
+    const int wave = int(threadIdx.x >> 6);
     const int64_t nvec = p.dim / VE;
-    const int64_t row0 = int64_t(blockIdx.x) * kBwdWaves + (threadIdx.x >> 6);
-    const int64_t rstride = int64_t(gridDim.x) * kBwdWaves;
-    if constexpr (kResident) bwd_rows_resident<T, TW, VE>(p, s_dw, lane, nvec, row0, rstride);
-    else bwd_rows_general<T, TW, VE>(p, s_dw, lane, nvec, row0, rstride);
+    const int64_t row0 = int64_t(blockIdx.x) * nw + wave;
+    const int64_t rstride = int64_t(gridDim.x) * nw;
+    float* region = s_dw + int64_t(wave) * p.dim;
+    if constexpr (kResident) bwd_rows_resident<T, TW, VE>(p, region, lane, nvec, row0, rstride);
+    else bwd_rows_general<T, TW, VE>(p, region, lane, nvec, row0, rstride);
 
     __syncthreads();
     float* part = p.part + int64_t(blockIdx.x) * p.dim;
-    for (int64_t c = threadIdx.x; c < p.dim; c += 64 * kBwdWaves) part[c] = s_dw[(c % VE) * nvec + c / VE];
+    for (int64_t c = threadIdx.x; c < p.dim; c += blockDim.x) {
+        const int64_t i = (c % VE) * nvec + c / VE;
+        float t = s_dw[i];
+        for (int w = 1; w < nw; ++w) t += s_dw[int64_t(w) * p.dim + i];
+        part[c] = t;
+    }
+}
+
+// waves per backward workgroup: kBwdWaves while their LDS regions (one row
+// of dim floats each) fit 64 KiB, fewer for longer rows
+int bwd_waves(int64_t dim) {
+    int nw = kBwdWaves;
+    while (nw > 1 && int64_t(nw) * dim * int64_t(sizeof(float)) > 65536) nw >>= 1;
+    return nw;
 }
 
 // dweight[c] = sum over the nparts rows of part, in a fixed order: wave i of
@@ -423,9 +444,10 @@ hipError_t launch_tw(const NormParams& p, bool vec, bool bwd, int64_t nparts, vo
         else hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, TW, 1, false>), grid, dim3(64 * kFwdWaves), 0, stream, p);
         return hipGetLastError();
     }
-    const size_t lds = size_t(p.dim) * sizeof(float);
+    const int nw = bwd_waves(p.dim);
+    const size_t lds = size_t(nw) * size_t(p.dim) * sizeof(float);
     if (nparts > 0) {
-        const dim3 grid{unsigned(nparts)}, block{64 * kBwdWaves};
+        const dim3 grid{unsigned(nparts)}, block{unsigned(64 * nw)};
         if (vec && p.dim <= 64 * kNSB * VE) hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, TW, VE, true>), grid, block, lds, stream, p);
         else if (vec) hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, TW, VE, false>), grid, block, lds, stream, p);
         else hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, TW, 1, false>), grid, block, lds, stream, p);

@@ -121,6 +121,31 @@ def test_rstd_and_deterministic_dweight():
     assert torch.equal(dw1, dw2), "dweight must not depend on scheduling"
 
 
+@pytest.mark.parametrize("case", [(6000, 768, torch.bfloat16), (3000, 768, torch.float32), (700, 8192, torch.bfloat16)],
+                         ids=["resident-bf16", "segments-fp32", "long-rows-2-waves"])
+def test_dweight_same_bits_every_run(case):
+    # fp32 weight (dweight fp32, so no rounding to the weight dtype can hide
+    # a different summation order): three backward runs give the same bits, on
+    # the one-segment path, the multi-segment path and rows long enough that
+    # a workgroup has 2 waves; dweight against the float64 sum
+    from mamba_amd.ops.rms_norm import rms_norm_bwd, rms_norm_fwd
+    rows, dim, dt = case
+    _say(f"dweight reproducible {case}")
+    gen = torch.Generator().manual_seed(11 + dim)
+    x = torch.randn(rows, dim, generator=gen).to(dt).to(DEV)
+    w = (0.5 * torch.randn(dim, generator=gen)).to(DEV)                   # fp32
+    out, _, rstd = rms_norm_fwd(x, w, None, eps=1e-6, want_rstd=True, want_s=False)
+    dout = torch.randn(rows, dim, generator=gen).to(dt).to(DEV)
+    runs = [rms_norm_bwd(x, w, rstd, dout) for _ in range(3)]
+    torch.cuda.synchronize()
+    for dx, dw in runs[1:]:
+        assert torch.equal(dx, runs[0][0])
+        assert torch.equal(dw, runs[0][1]), "dweight must not depend on scheduling"
+    xd, dd = x.double().cpu(), dout.double().cpu()
+    want = (dd * xd * rstd.double().cpu()[:, None]).sum(0)
+    assert_close(runs[0][1].cpu(), want, 1e-4, 1e-4 * float(want.abs().max()), "dweight")
+
+
 def test_empty_rows():
     from mamba_amd.ops.rms_norm import rms_norm_bwd, rms_norm_fwd
     _say("no rows")

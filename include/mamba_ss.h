@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 14
+#define SS_ABI_VERSION 15
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -244,12 +244,22 @@ typedef struct ss_conv1d_bwd_args {
     void* dx;                            /* overwritten, itype */
     float* dweight;                      /* accumulated into, fp32 (dim, width) contiguous */
     float* dbias;                        /* accumulated into, fp32 (dim); may be NULL iff !has_bias */
+    /* ABI v15: with a workspace (NULL: none) of at least
+     * ss_conv1d_bwd_workspace_bytes bytes, dweight / dbias are summed in a
+     * fixed order (per-workgroup partials, then a second launch adds them per
+     * channel in (batch, sequence tile) order): the same bits on every run.
+     * Without it each workgroup adds its partial with fp32 atomics. */
+    float* workspace;
+    int64_t workspace_bytes;
 } ss_conv1d_bwd_args;
 
 /* Forward: writes out.  Backward: writes dx, accumulates dweight / dbias;
    recomputes the pre-activation from x, weight and bias. */
 int ss_conv1d_fwd(const ss_conv1d_args* a, void* stream);
 int ss_conv1d_bwd(const ss_conv1d_bwd_args* a, void* stream);
+/* Workspace bytes of the fixed-order backward sums for these sizes (batch x
+ * dim x sequence tiles x 5 floats); -1 on invalid sizes. */
+int64_t ss_conv1d_bwd_workspace_bytes(const ss_conv1d_bwd_args* a);
 
 /* ------------------------------------------------------------------------
  * RMSNorm with an optional residual add, on rows of dim elements.  Replaces

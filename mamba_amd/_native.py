@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 14
+ABI_VERSION = 15
 # bytes of the fixed device scratch of ss_bwd_noalloc (SS_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -24,6 +24,7 @@ EXPORTED = (
     "ss_fwd", "ss_bwd", "ss_bwd_noalloc", "ss_conv1d_fwd", "ss_conv1d_bwd",
     "ss_rmsnorm_fwd", "ss_rmsnorm_bwd", "ss_rmsnorm_bwd_workspace_bytes",
     "ss_state_update", "ss_conv1d_update", "ss_decode_linear", "ss_decode_linear_workspace_bytes",
+    "ss_conv1d_bwd_workspace_bytes",
 )
 
 _i64, _i32, _p = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
@@ -80,6 +81,7 @@ class Conv1dBwdArgs(ctypes.Structure):
         ("dout_batch_stride", _i64), ("dout_dim_stride", _i64),
         ("dx_batch_stride", _i64), ("dx_dim_stride", _i64),
         ("dout", _p), ("dx", _p), ("dweight", _p), ("dbias", _p),
+        ("workspace", _p), ("workspace_bytes", _i64),
     ]
 
 
@@ -183,6 +185,8 @@ def load():
         lib.ss_conv1d_fwd.restype = ctypes.c_int
         lib.ss_conv1d_bwd.argtypes = [ctypes.POINTER(Conv1dBwdArgs), _p]
         lib.ss_conv1d_bwd.restype = ctypes.c_int
+        lib.ss_conv1d_bwd_workspace_bytes.argtypes = [ctypes.POINTER(Conv1dBwdArgs)]
+        lib.ss_conv1d_bwd_workspace_bytes.restype = _i64
         lib.ss_decode_linear.argtypes = [ctypes.POINTER(DecodeLinearArgs), _p]
         lib.ss_decode_linear.restype = ctypes.c_int
         lib.ss_decode_linear_workspace_bytes.argtypes = [ctypes.POINTER(DecodeLinearArgs)]

@@ -37,6 +37,7 @@ struct ConvParams {
     int64_t do_bs, do_ds, dx_bs, dx_ds;
     const void* x; const float* w; const float* bias; void* out;
     const void* dout; void* dx; float* dw; float* dbias;
+    float* part;                                 // fixed-order sums: (row, tile, 5) partials; null: atomics
 };
 
 template <typename IT>
@@ -256,6 +257,10 @@ __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < kCT / 64; ++i) s += red[i][k];
+        if (p.part) {                                   // summed later in a fixed order
+            p.part[(row_id * int64_t(gridDim.y) + blockIdx.y) * 5 + k] = s;
+            return;
+        }
         if (k < 4) {
             const int tap = k - (4 - p.width);          // right-aligned slot k is tap k - (4 - width)
             if (tap >= 0) atomicAdd(p.dw + d * p.width + tap, s);
@@ -265,12 +270,39 @@ __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
     }
 }
 
+// dweight / dbias += the backward's partials, one thread per (channel, slot
+// k): slots 0..3 the right-aligned taps, 4 the bias; summed over batch rows,
+// then sequence tiles, in that order
+__global__ __launch_bounds__(256) void conv1d_bwd_reduce(const float* __restrict__ part, int64_t batch, int64_t dim,
+                                                         int64_t ntiles, int width, float* __restrict__ dw,
+                                                         float* __restrict__ dbias) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= dim * 5) return;
+    const int64_t d = i / 5;
+    const int k = int(i % 5);
+    float s = 0.f;
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t t = 0; t < ntiles; ++t) s += part[((b * dim + d) * ntiles + t) * 5 + k];
+    if (k < 4) {
+        const int tap = k - (4 - width);
+        if (tap >= 0) dw[d * width + tap] += s;
+    } else if (dbias) {
+        dbias[d] += s;
+    }
+}
+
 template <typename IT, int VW>
 void launch_vw(const ConvParams& p, bool bwd, hipStream_t stream) {
     constexpr int V = VW ? VW : 4;
     const dim3 grid(unsigned(p.batch * p.dim), unsigned((p.seqlen + kCT * V - 1) / (kCT * V)));
-    if (bwd) hipLaunchKernelGGL((conv1d_bwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
-    else hipLaunchKernelGGL((conv1d_fwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
+    if (bwd) {
+        hipLaunchKernelGGL((conv1d_bwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
+        if (p.part)
+            hipLaunchKernelGGL(conv1d_bwd_reduce, dim3(unsigned((p.dim * 5 + 255) / 256)), dim3(256), 0, stream,
+                               p.part, p.batch, p.dim, int64_t(grid.y), int(p.width), p.dw, p.dbias);
+    } else {
+        hipLaunchKernelGGL((conv1d_fwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
+    }
 }
 
 template <typename IT>
@@ -297,6 +329,12 @@ hipError_t launch_conv(const ConvParams& p, int itype, bool bwd, hipStream_t str
 
 }  // namespace
 
+int64_t conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen) {
+    // the most sequence tiles a launch can have (4 steps per thread)
+    const int64_t ntiles = (seqlen + kCT * 4 - 1) / (kCT * 4);
+    return batch * dim * ntiles * 5 * int64_t(sizeof(float));
+}
+
 hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, hipStream_t stream) {
     ConvParams p{};
     p.batch = a->batch; p.dim = a->dim; p.seqlen = a->seqlen; p.width = int32_t(a->width);
@@ -310,6 +348,7 @@ hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, h
         p.do_bs = g->dout_batch_stride; p.do_ds = g->dout_dim_stride;
         p.dx_bs = g->dx_batch_stride; p.dx_ds = g->dx_dim_stride;
         p.dout = g->dout; p.dx = g->dx; p.dw = g->dweight; p.dbias = a->has_bias ? g->dbias : nullptr;
+        p.part = g->workspace;
     }
     // every row of every tensor the launch touches starts on an n-element
     // boundary and seqlen is a multiple of n (so each n-step vector is

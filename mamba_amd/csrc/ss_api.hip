@@ -529,6 +529,13 @@ int ss_conv1d_bwd(const ss_conv1d_bwd_args* g, void* stream) {
         return fail(SS_ERR_INVALID, "dweight / dbias is misaligned");
     if (g->dout_batch_stride < 0 || g->dout_dim_stride < 0 || g->dx_batch_stride < 0 || g->dx_dim_stride < 0)
         return fail(SS_ERR_INVALID, "negative stride");
+    if (g->workspace) {
+        if (!aligned(g->workspace, 4)) return fail(SS_ERR_INVALID, "workspace is misaligned");
+        const int64_t need = ss::conv1d_bwd_workspace_bytes(g->f.batch, g->f.dim, g->f.seqlen);
+        if (g->workspace_bytes < need)
+            return fail(SS_ERR_INVALID, "workspace_bytes=%lld below the %lld the fixed-order sums need",
+                        (long long)g->workspace_bytes, (long long)need);
+    }
     hipError_t e = ss::conv1d_launch(&g->f, g, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(SS_ERR_HIP, "conv1d backward launch failed: %s", hipGetErrorString(e));
     return ok();
@@ -684,6 +691,20 @@ int64_t ss_decode_linear_workspace_bytes(const ss_decode_linear_args* a) {
     }
     ok();
     return ss::decode_linear_split(a->batch, a->n_out, a->k_in).workspace_bytes;
+}
+
+int64_t ss_conv1d_bwd_workspace_bytes(const ss_conv1d_bwd_args* g) {
+    if (!g) {
+        fail(SS_ERR_INVALID, "null argument block");
+        return -1;
+    }
+    if (g->f.batch < 0 || g->f.dim < 0 || g->f.seqlen < 0) {
+        fail(SS_ERR_INVALID, "negative size (batch=%lld dim=%lld seqlen=%lld)", (long long)g->f.batch,
+             (long long)g->f.dim, (long long)g->f.seqlen);
+        return -1;
+    }
+    ok();
+    return ss::conv1d_bwd_workspace_bytes(g->f.batch, g->f.dim, g->f.seqlen);
 }
 
 int64_t ss_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim) {

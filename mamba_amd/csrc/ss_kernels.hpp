@@ -112,6 +112,8 @@ hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int itype, hipStream_t stream);
 // causal depthwise conv1d (+ SiLU); g == nullptr: forward, else backward
 hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, hipStream_t stream);
+// bytes of the backward's fixed-order partials (batch x dim x tiles x 5 floats)
+int64_t conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen);
 // single-token decode: selective-scan state update and conv1d state update
 hipError_t state_update_launch(const ss_state_update_args* a, hipStream_t stream);
 hipError_t conv_update_launch(const ss_conv1d_update_args* a, hipStream_t stream);

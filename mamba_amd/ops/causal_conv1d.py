@@ -12,7 +12,11 @@ applies SiLU):
 strides are free, so x may be a channel slice of a packed xz tensor),
 weight as (dim, width) or nn.Conv1d's (dim, 1, width), width 1..4, and
 returns out in x's dtype.  Gradients: dx in x's dtype, dweight / dbias in
-the parameters' dtypes (accumulated in fp32).
+the parameters' dtypes (accumulated in fp32).  Under
+``torch.use_deterministic_algorithms(True)`` the backward sums dweight and
+dbias in a fixed order (per-workgroup partials added per channel by a second
+launch), so they come out with the same bits on every run; otherwise each
+workgroup adds its partial with fp32 atomics.
 """
 import ctypes
 
@@ -68,8 +72,10 @@ def causal_conv1d_fwd(x, weight, bias=None, silu=False, out=None):
     return out
 
 
-def causal_conv1d_bwd(x, weight, bias, dout, silu=False, dx=None):
-    """Returns (dx, dweight fp32 (dim, width), dbias fp32 or None)."""
+def causal_conv1d_bwd(x, weight, bias, dout, silu=False, dx=None, deterministic=None):
+    """Returns (dx, dweight fp32 (dim, width), dbias fp32 or None).
+    ``deterministic``: sum dweight / dbias in a fixed order; None follows
+    ``torch.use_deterministic_algorithms``."""
     lib = nat.load()
     w, b = _params32(weight, bias, x.shape[1], x.device)
     _require(dout.shape == x.shape and dout.dtype == x.dtype, "dout must match x in shape and dtype")
@@ -84,8 +90,17 @@ def causal_conv1d_bwd(x, weight, bias, dout, silu=False, dx=None):
     g.dout_batch_stride, g.dout_dim_stride = dout.stride(0), dout.stride(1)
     g.dx_batch_stride, g.dx_dim_stride = dx.stride(0), dx.stride(1)
     g.dout, g.dx, g.dweight, g.dbias = _ptr(dout), _ptr(dx), _ptr(dw), _ptr(db)
+    if deterministic is None:
+        deterministic = torch.are_deterministic_algorithms_enabled()
+    ws = None
+    if deterministic:
+        nbytes = lib.ss_conv1d_bwd_workspace_bytes(ctypes.byref(g))
+        _require(nbytes >= 0, "invalid conv1d sizes")
+        ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=x.device)
+        g.workspace, g.workspace_bytes = _ptr(ws), ws.numel() * 4
     with torch.cuda.device(x.device):
         nat.check(lib.ss_conv1d_bwd(ctypes.byref(g), _stream(x.device)), "causal_conv1d_bwd")
+    del ws                  # the caching allocator keeps it until the stream's work is done
     return dx, dw, db
 
 

@@ -60,7 +60,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 14
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 15
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -484,6 +484,37 @@ def test_rmsnorm_empty_and_bwd_rejects(nat, lib):
     g = valid_norm_bwd(nat)
     g.dweight = None
     assert lib.ss_rmsnorm_bwd(ctypes.byref(g), None) == nat.SS_ERR_INVALID
+
+
+def valid_conv_bwd(nat, batch=2, dim=64, seqlen=5000):
+    g = nat.Conv1dBwdArgs()
+    g.f.batch, g.f.dim, g.f.seqlen, g.f.width = batch, dim, seqlen, 4
+    g.f.itype, g.f.has_bias, g.f.silu = nat.SS_BF16, 1, 1
+    g.f.x_batch_stride, g.f.x_dim_stride = dim * seqlen, seqlen
+    g.f.out_batch_stride, g.f.out_dim_stride = dim * seqlen, seqlen
+    g.f.w_dim_stride, g.f.w_width_stride = 4, 1
+    g.f.x, g.f.weight, g.f.bias, g.f.out = (FAKE + 65536 * i for i in range(4))
+    g.dout_batch_stride, g.dout_dim_stride = dim * seqlen, seqlen
+    g.dx_batch_stride, g.dx_dim_stride = dim * seqlen, seqlen
+    g.dout, g.dx, g.dweight, g.dbias = (FAKE + 65536 * (4 + i) for i in range(4))
+    return g
+
+
+def test_conv1d_bwd_workspace_query_and_rejects(nat, lib):
+    # 5 fp32 partials (4 right-aligned taps + bias) per (batch row, channel,
+    # sequence tile of 1024 steps: the fewest steps a workgroup takes)
+    assert lib.ss_conv1d_bwd_workspace_bytes(ctypes.byref(valid_conv_bwd(nat))) == 2 * 64 * 5 * 5 * 4
+    assert lib.ss_conv1d_bwd_workspace_bytes(ctypes.byref(valid_conv_bwd(nat, seqlen=1024))) == 2 * 64 * 5 * 4
+    assert lib.ss_conv1d_bwd_workspace_bytes(ctypes.byref(valid_conv_bwd(nat, seqlen=0))) == 0
+    assert lib.ss_conv1d_bwd_workspace_bytes(ctypes.byref(valid_conv_bwd(nat, batch=-1))) == -1
+    g = valid_conv_bwd(nat)
+    g.workspace, g.workspace_bytes = FAKE + 2, 1 << 20
+    assert lib.ss_conv1d_bwd(ctypes.byref(g), None) == nat.SS_ERR_INVALID
+    assert "misaligned" in lib.ss_last_error().decode()
+    g = valid_conv_bwd(nat)
+    g.workspace, g.workspace_bytes = FAKE, 2 * 64 * 5 * 5 * 4 - 4
+    assert lib.ss_conv1d_bwd(ctypes.byref(g), None) == nat.SS_ERR_INVALID
+    assert "workspace_bytes" in lib.ss_last_error().decode()
 
 
 def test_rmsnorm_workspace_query(lib):

@@ -16,12 +16,21 @@ backward gives the same bits on every run.  Checked, through the C ABI
 * torch.use_deterministic_algorithms(True) turns it on for autograd
   (selective_scan_fn), and for arguments the fast kernels do not take it
   raises as torch's own ops do, or warns under warn_only.
+
+The causal conv1d backward (ss_conv1d_bwd_args.workspace) likewise: three
+runs with the fixed-order dweight / dbias sums bit-identical, equal to the
+atomic sums to 1e-5 relative and to float64 autograd of the conv oracle,
+accumulating onto what dweight / dbias held; and mamba_inner_fn's gradients
+(scan and conv together) bit-identical across runs under
+torch.use_deterministic_algorithms(True).
 """
+import ctypes
 import sys
 
 import pytest
 import torch
 
+from oracle.mamba_block_ref import causal_conv1d_ref
 from oracle.selective_scan_ref import make_inputs
 from tests._util import NAMES, assert_close, oracle_fwd_bwd
 
@@ -163,3 +172,110 @@ def test_torch_deterministic_setting_drives_autograd():
             grads(xr)
     finally:
         torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
+
+
+# (batch, dim, seqlen, width, bias, dtype): several sequence tiles per row
+# (2048 steps per bf16 workgroup, 1024 fp32), a ragged last tile, width 2
+CONV_CASES = [(3, 96, 5000, 4, True, torch.bfloat16), (2, 40, 3001, 2, False, torch.float32),
+              (4, 16, 1028, 3, True, torch.float16)]
+
+
+def _conv_bwd(x, w, b, dout, det, init=None):
+    from mamba_amd import _native as nat
+    from mamba_amd.ops import causal_conv1d as cc
+    from mamba_amd.selective_scan import _ptr, _stream
+    if init is None:
+        return cc.causal_conv1d_bwd(x, w, b, dout, silu=True, deterministic=det)
+    # accumulation: the C ABI adds into dweight / dbias
+    lib = nat.load()
+    w2, b2 = cc._params32(w, b, x.shape[1], x.device)
+    dx = torch.empty_like(x)
+    dw, db = init[0].clone(), (init[1].clone() if b is not None else None)
+    g = nat.Conv1dBwdArgs()
+    g.f = cc._fill(x, w2, b2, True, None)
+    g.dout_batch_stride, g.dout_dim_stride = dout.stride(0), dout.stride(1)
+    g.dx_batch_stride, g.dx_dim_stride = dx.stride(0), dx.stride(1)
+    g.dout, g.dx, g.dweight, g.dbias = _ptr(dout), _ptr(dx), _ptr(dw), _ptr(db)
+    ws = torch.empty(lib.ss_conv1d_bwd_workspace_bytes(ctypes.byref(g)) // 4, dtype=torch.float32, device=DEV)
+    g.workspace, g.workspace_bytes = _ptr(ws), ws.numel() * 4
+    assert lib.ss_conv1d_bwd(ctypes.byref(g), _stream(DEV)) == nat.SS_OK
+    torch.cuda.synchronize()
+    return dx, dw, db
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=["bf16-w4-bias", "fp32-w2", "fp16-w3-bias"])
+def test_conv1d_backward_fixed_order_sums(case):
+    batch, dim, L, width, has_bias, dt = case
+    _say(f"conv1d backward batch {batch} dim {dim} seqlen {L} width {width} {dt}")
+    g = torch.Generator().manual_seed(dim * 7 + L)
+    x = torch.randn(batch, dim, L, generator=g).to(dt)
+    w = torch.randn(dim, width, generator=g) * 0.5
+    b = torch.randn(dim, generator=g) if has_bias else None
+    dout = torch.randn(batch, dim, L, generator=g).to(dt)
+    xd, wd, dd = x.to(DEV), w.to(DEV), dout.to(DEV)
+    bd = b.to(DEV) if b is not None else None
+    runs = [_conv_bwd(xd, wd, bd, dd, det=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    for i, what in ((0, "dx"), (1, "dweight"), (2, "dbias")):
+        if runs[0][i] is not None:
+            assert torch.equal(runs[0][i], runs[1][i]) and torch.equal(runs[0][i], runs[2][i]), f"{what} differs"
+    atomic = _conv_bwd(xd, wd, bd, dd, det=False)
+    torch.cuda.synchronize()
+    assert torch.equal(runs[0][0], atomic[0])                   # dx has no sums across workgroups
+    for i, what in ((1, "dweight"), (2, "dbias")):
+        if atomic[i] is not None:
+            assert_close(runs[0][i], atomic[i], 1e-5, 1e-5 * float(atomic[i].abs().max()), f"{what} vs atomic")
+    xr, wr = x.double(), w.double().requires_grad_(True)
+    br = b.double().requires_grad_(True) if b is not None else None
+    causal_conv1d_ref(xr, wr, br, activation="silu").backward(dout.double())
+    tol = 1e-3 if dt == torch.float32 else 2e-2
+    assert_close(runs[0][1].cpu(), wr.grad, tol, tol * max(1.0, float(wr.grad.abs().max())), "dweight vs oracle")
+    if b is not None:
+        assert_close(runs[0][2].cpu(), br.grad, tol, tol * max(1.0, float(br.grad.abs().max())), "dbias vs oracle")
+    init = (torch.randn(dim, width, device=DEV), torch.randn(dim, device=DEV))
+    _, dw, db = _conv_bwd(xd, wd, bd, dd, det=True, init=init)
+    assert torch.equal(dw, init[0] + runs[0][1])
+    if b is not None:
+        assert torch.equal(db, init[1] + runs[0][2])
+
+
+def test_mamba_inner_fn_deterministic_setting():
+    from mamba_amd.ops.selective_scan_interface import mamba_inner_fn
+    batch, d_model, dim, L, R, N, width = 2, 32, 64, 4104, 4, 16, 4
+    _say(f"mamba_inner_fn under torch.use_deterministic_algorithms, seqlen {L}")
+    g = torch.Generator().manual_seed(341)
+    p = {
+        "conv1d_weight": torch.randn(dim, 1, width, generator=g) * 0.3,
+        "conv1d_bias": torch.randn(dim, generator=g) * 0.1,
+        "x_proj_weight": torch.randn(R + 2 * N, dim, generator=g) * dim ** -0.5,
+        "delta_proj_weight": torch.rand(dim, R, generator=g) * R ** -0.5,
+        "out_proj_weight": torch.randn(d_model, dim, generator=g) * dim ** -0.5,
+        "out_proj_bias": torch.randn(d_model, generator=g) * 0.1,
+        "A": -torch.arange(1, N + 1, dtype=torch.float32).repeat(dim, 1),
+        "D": torch.ones(dim),
+        "delta_bias": torch.log(torch.expm1(torch.rand(dim, generator=g) * 0.099 + 0.001)),
+    }
+    xz = torch.randn(batch, 2 * dim, L, generator=g).to(torch.bfloat16)
+    dres = torch.randn(batch, L, d_model, generator=g).to(torch.bfloat16)
+    args = ("conv1d_weight", "conv1d_bias", "x_proj_weight", "delta_proj_weight", "out_proj_weight",
+            "out_proj_bias", "A")
+
+    def grads():
+        gp = {k: (v.to(torch.bfloat16) if k not in ("A", "D", "delta_bias") else v).to(DEV).requires_grad_(True)
+              for k, v in p.items()}
+        xzg = xz.to(DEV).requires_grad_(True)
+        out = mamba_inner_fn(xzg, *(gp[k] for k in args), D=gp["D"], delta_bias=gp["delta_bias"],
+                             delta_softplus=True)
+        out.backward(dres.to(DEV))
+        torch.cuda.synchronize()
+        return {"xz": xzg.grad.clone(), **{k: v.grad.clone() for k, v in gp.items()}}
+
+    prev = torch.are_deterministic_algorithms_enabled()
+    prev_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        a, b = grads(), grads()
+    finally:
+        torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
+    for k in a:
+        assert torch.equal(a[k], b[k]), f"d{k} differs between runs"

@@ -106,10 +106,16 @@ class MambaSimple(nn.Module):
         if self.input_proj.bias is not None:
             xz = xz + self.input_proj.bias[:, None]
         xz = xz.view(2 * self.inner_dim, batch, seqlen).permute(1, 0, 2)
-        A = -torch.exp(self.log_A.float())
-        args = (xz, self.short_conv.weight, self.short_conv.bias, self.ssm_param_proj.weight,
+        if torch.is_grad_enabled():
+            A = -torch.exp(self.log_A.float())
+            D, delta_bias = self.D.float(), self.delta_proj.bias.float()
+            conv_w, conv_b = self.short_conv.weight, self.short_conv.bias
+        else:
+            # no autograd graph: the fp32 parameters of the last call, unless one changed
+            A, D, delta_bias, conv_w, conv_b = self._decode_params()
+        args = (xz, conv_w, conv_b, self.ssm_param_proj.weight,
                 self.delta_proj.weight, self.output_proj.weight, self.output_proj.bias, A)
-        kw = dict(D=self.D.float(), delta_bias=self.delta_proj.bias.float(), delta_softplus=True)
+        kw = dict(D=D, delta_bias=delta_bias, delta_softplus=True)
         if inference_cache is not None:
             conv_state, ssm_state = inference_cache
             return mamba_inner_prefill(*args, **kw, conv_state=conv_state, ssm_state=ssm_state)
@@ -174,8 +180,9 @@ class MambaSimple(nn.Module):
 
     def _decode_params(self):
         """A = -exp(log_A), D, the delta bias and the conv weight / bias in fp32, computed
-        once and reused by every step until one of those parameters changes (their
-        version counters move on any in-place update, an optimizer step included)."""
+        once and reused by every decode step and no-grad forward until one of those
+        parameters changes (their version counters move on any in-place update, an
+        optimizer step included)."""
         params = [self.log_A, self.D, self.delta_proj.bias, self.short_conv.weight]
         if self.short_conv.bias is not None:
             params.append(self.short_conv.bias)

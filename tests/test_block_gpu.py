@@ -7,7 +7,9 @@
 * mamba_inner_fn forward and backward (all 14 differentiable inputs)
   against float64 autograd of mamba_inner_ref;
 * MambaSimple (both forward paths) and CausalLM against the oracle, with
-  the same weights.
+  the same weights;
+* a no-grad MambaSimple forward (fp32 parameters cached by version) equal bit
+  for bit to one with autograd, also after an in-place parameter update.
 
 Tolerances: fp32 rtol / atol 1e-3, bf16 / fp16 2e-2 (relative to the
 largest magnitude for the GEMM-heavy block outputs, stated per test).
@@ -168,3 +170,30 @@ def test_mamba_simple_both_paths_and_causal_lm():
         logits = lm(ids.to(DEV)).cpu()
     ref = causal_lm_ref({k: v.detach().double().cpu() for k, v in lm.state_dict().items()}, ids, num_layers=2)
     assert_close(logits, ref, 1e-3, 1e-3 * float(ref.abs().max()), "CausalLM logits")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_mamba_simple_no_grad_forward_matches(dt):
+    from mamba_amd.modules import MambaSimple
+    _say(f"MambaSimple no-grad forward with cached parameters, {dt}")
+    torch.manual_seed(12)
+    m = MambaSimple(model_dim=64, state_dim=16, conv_bias=True, device=DEV, dtype=dt)
+    hidden = torch.randn(2, 256, 64, device=DEV).to(dt)
+
+    def both():
+        with torch.no_grad():
+            a = m(hidden)
+        b = m(hidden).detach()
+        torch.cuda.synchronize()
+        return a, b
+    a, b = both()
+    assert torch.equal(a, b)
+    with torch.no_grad():            # in place: the cached fp32 copies must follow
+        m.log_A.add_(0.25)
+        m.D.mul_(0.5)
+        m.delta_proj.bias.add_(0.1)
+        m.short_conv.weight.mul_(-1.0)
+        m.short_conv.bias.add_(0.2)
+    a2, b2 = both()
+    assert torch.equal(a2, b2)
+    assert not torch.equal(a2, a)

@@ -182,22 +182,27 @@ class MambaSimple(nn.Module):
         """A = -exp(log_A), D, the delta bias and the conv weight / bias in fp32, computed
         once and reused by every decode step and no-grad forward until one of those
         parameters changes (their version counters move on any in-place update, an
-        optimizer step included)."""
+        optimizer step included).  Parameters created under torch.inference_mode
+        carry no version counter, so for them the values are computed on every call."""
         params = [self.log_A, self.D, self.delta_proj.bias, self.short_conv.weight]
         if self.short_conv.bias is not None:
             params.append(self.short_conv.bias)
+        if any(p.is_inference() for p in params):
+            return self._fp32_params()
         key = tuple((p.data_ptr(), p._version) for p in params)
         cached = getattr(self, "_decode_cache", None)
         if cached is None or cached[0] != key:
-            with torch.no_grad():
-                w = self.short_conv.weight
-                vals = (-torch.exp(self.log_A.float()), self.D.float().contiguous(),
-                        self.delta_proj.bias.float().contiguous(),
-                        w.reshape(w.shape[0], w.shape[-1]).float().contiguous(),
-                        self.short_conv.bias.float().contiguous() if self.short_conv.bias is not None else None)
-            self._decode_cache = (key, vals)
+            self._decode_cache = (key, self._fp32_params())
             cached = self._decode_cache
         return cached[1]
+
+    def _fp32_params(self):
+        with torch.no_grad():
+            w = self.short_conv.weight
+            return (-torch.exp(self.log_A.float()), self.D.float().contiguous(),
+                    self.delta_proj.bias.float().contiguous(),
+                    w.reshape(w.shape[0], w.shape[-1]).float().contiguous(),
+                    self.short_conv.bias.float().contiguous() if self.short_conv.bias is not None else None)
 
     def _forward_reference(self, hidden_states):
         # the reference's op sequence (modules/mamba_simple.py:95-149)

@@ -9,7 +9,9 @@
 * MambaSimple (both forward paths) and CausalLM against the oracle, with
   the same weights;
 * a no-grad MambaSimple forward (fp32 parameters cached by version) equal bit
-  for bit to one with autograd, also after an in-place parameter update.
+  for bit to one with autograd, also after an in-place parameter update;
+  a block built under torch.inference_mode (no version counters) forwards
+  and steps without the cache.
 
 Tolerances: fp32 rtol / atol 1e-3, bf16 / fp16 2e-2 (relative to the
 largest magnitude for the GEMM-heavy block outputs, stated per test).
@@ -197,3 +199,31 @@ def test_mamba_simple_no_grad_forward_matches(dt):
     a2, b2 = both()
     assert torch.equal(a2, b2)
     assert not torch.equal(a2, a)
+
+
+def test_mamba_simple_parameters_made_in_inference_mode():
+    # inference tensors carry no version counter: no-grad forwards and decode
+    # steps compute the fp32 parameters on every call instead of caching them
+    from mamba_amd.modules import MambaSimple
+    _say("MambaSimple built under torch.inference_mode")
+    torch.manual_seed(13)
+    with torch.inference_mode():
+        m = MambaSimple(model_dim=64, state_dim=16, conv_bias=True, device=DEV, dtype=torch.float32)
+        hidden = torch.randn(2, 128, 64, device=DEV)
+        out = m(hidden)
+        conv_state, ssm_state = m.allocate_inference_cache(2)
+        steps = [m.step(hidden[:, t], conv_state, ssm_state) for t in range(4)]
+        sd0 = {k: v.clone() for k, v in m.state_dict().items()}
+        m.log_A.add_(0.25)                      # in place, no version counter moves
+        out2 = m(hidden)
+        sd1 = {k: v.clone() for k, v in m.state_dict().items()}
+    ref = MambaSimple(model_dim=64, state_dim=16, conv_bias=True, device=DEV, dtype=torch.float32)
+    with torch.no_grad():
+        ref.load_state_dict(sd0)
+        want = ref(hidden.clone())
+        ref.load_state_dict(sd1)
+        want2 = ref(hidden.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(out, want) and torch.equal(out2, want2)
+    for t, y in enumerate(steps):
+        assert_close(y.cpu(), want[:, t].cpu(), 1e-3, 1e-3, f"step {t}")

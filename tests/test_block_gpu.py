@@ -4,6 +4,9 @@
   the conv oracle: widths 1-4, with and without bias and activation, x as a
   channel slice of a packed xz tensor, a seqlen that is not a multiple of 4
   (element path), fp32 / bf16 / fp16;
+* 40 seeded random conv1d shapes (batch, channels, seqlen from 1 to 5000,
+  width, dtype, bias, SiLU, padded channel rows, atomic or fixed-order
+  dweight / dbias sums) against float64 autograd of the conv oracle;
 * mamba_inner_fn forward and backward (all 14 differentiable inputs)
   against float64 autograd of mamba_inner_ref;
 * MambaSimple (both forward paths) and CausalLM against the oracle, with
@@ -83,6 +86,46 @@ def test_causal_conv1d(case):
     assert_close(wg.grad.cpu(), wr.grad, rtol, atol * scale, "dweight")
     if b is not None:
         assert_close(bg.grad.cpu(), br.grad, rtol, atol * max(1.0, float(br.grad.abs().max())), "dbias")
+
+
+@pytest.mark.parametrize("i", range(40))
+def test_causal_conv1d_random(i):
+    import random
+    from mamba_amd.ops.causal_conv1d import causal_conv1d_bwd, causal_conv1d_fwd
+    rnd = random.Random(5000 + i)
+    batch = rnd.choice([1, 2, 3, 5])
+    dim = rnd.choice([1, 3, 16, 40, 64, 100])
+    L = rnd.choice([1, 2, 3, 4, 5, 7, 8, 15, 16, 31, 64, 100, 255, 256, 1023, 1024, 1025, 2048, 3001, 4104,
+                    rnd.randint(1, 5000)])
+    width = rnd.choice([1, 2, 3, 4])
+    dt = rnd.choice([torch.float32, torch.bfloat16, torch.float16])
+    has_bias = rnd.random() < 0.6
+    silu = rnd.random() < 0.7
+    pad = rnd.choice([0, 0, 8, 3])
+    det = rnd.random() < 0.5
+    _say(f"conv1d random {i}: batch {batch} dim {dim} seqlen {L} width {width} {dt} bias {has_bias} "
+         f"silu {silu} pad {pad} fixed-order {det}")
+    g = torch.Generator().manual_seed(6000 + i)
+    xz = torch.randn(batch, dim + pad, L, generator=g).to(dt)
+    w = torch.randn(dim, width, generator=g) * 0.5
+    b = torch.randn(dim, generator=g) if has_bias else None
+    dout = torch.randn(batch, dim, L, generator=g).to(dt)
+    x = xz.to(DEV)[:, :dim]
+    bd = b.to(DEV) if b is not None else None
+    out = causal_conv1d_fwd(x, w.to(DEV), bd, silu)
+    dx, dw, db = causal_conv1d_bwd(x, w.to(DEV), bd, dout.to(DEV), silu, deterministic=det)
+    torch.cuda.synchronize()
+    xr = xz[:, :dim].double().requires_grad_(True)
+    wr = w.double().requires_grad_(True)
+    br = b.double().requires_grad_(True) if b is not None else None
+    ref = causal_conv1d_ref(xr, wr, br, activation="silu" if silu else None)
+    ref.backward(dout.double())
+    rtol, atol = TOL[dt]
+    assert_close(out.float().cpu(), ref.detach(), rtol, atol, "out")
+    assert_close(dx.float().cpu(), xr.grad, rtol, atol, "dx")
+    assert_close(dw.cpu(), wr.grad, rtol, atol * max(1.0, float(wr.grad.abs().max())), "dweight")
+    if b is not None:
+        assert_close(db.cpu(), br.grad, rtol, atol * max(1.0, float(br.grad.abs().max())), "dbias")
 
 
 def _block_params(d_model, dim, R, N, width, dt, seed, out_bias=True, conv_bias=True):

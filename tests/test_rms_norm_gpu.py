@@ -9,6 +9,8 @@
   twice), and the one-element-per-lane path (lengths or strides that are
   not whole 16-byte vectors); strided rows; more rows than backward
   workgroups can take at once; no rows;
+* 30 seeded random cases (rows, row length from 1 to 6000, dtypes, residual,
+  row padding) through the same checks;
 * dweight has the same bits on every run;
 * CausalLM with the residual stream fused into the norms against the
   reference's block order (every op on the GPU), forward and gradients.
@@ -100,6 +102,20 @@ def test_rms_norm_fwd_bwd(case):
     dw_want = wd.grad
     wtol = max(tol, TOL[wdt])
     assert_close(wg.grad.cpu(), dw_want, wtol, wtol * float(dw_want.abs().max()), "dweight")
+
+
+def _random_case(i):
+    import random
+    rnd = random.Random(4000 + i)
+    dt = rnd.choice([torch.float32, torch.bfloat16, torch.float16])
+    dim = rnd.choice([1, 7, 8, 64, 100, 512, 768, 1000, 1024, 2048, 2049, 4096, rnd.randint(1, 6000)])
+    rows = rnd.choice([1, 2, 17, 64, 300, rnd.randint(1, 3000)])
+    return ((rows,), dim, dt, rnd.choice([dt, torch.float32]), rnd.random() < 0.6, rnd.choice([0, 0, 8, 3]))
+
+
+@pytest.mark.parametrize("i", range(30))
+def test_rms_norm_random(i):
+    test_rms_norm_fwd_bwd(_random_case(i))
 
 
 def test_rstd_and_deterministic_dweight():

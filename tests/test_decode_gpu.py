@@ -153,6 +153,68 @@ def test_state_update_low_rank_delta(dt_, rank):
     assert_close(out.cpu().double(), want_out.double(), tol, tol, "out")
 
 
+@pytest.mark.parametrize("i", range(30))
+def test_state_update_random(i):
+    """Seeded random state updates: batch, dim, dstate (1 to 200), groups, dtype,
+    z / D / bias, dt full or as the low-rank pair (any rank), B / C as column
+    slices of the x-projection output, a strided state; against the float64
+    oracle (a low-rank dt rounded to the input type first, as the kernel does).
+    The kernel rounds its fp32 sum of the low-rank product, the oracle its
+    float64 sum: where the two fall on either side of a rounding boundary of a
+    16-bit type, dt differs by one unit in its last place (2^-8 relative for
+    bf16) and the state by as much, so the state is then held to the input
+    type's tolerance."""
+    import random
+    from mamba_amd.ops.selective_state_update import selective_state_update
+    rnd = random.Random(3000 + i)
+    batch = rnd.choice([1, 2, 5, 16, 33])
+    N = rnd.choice([1, 4, 8, 16, 16, 16, 32, 64, 200])
+    G = rnd.choice([1, 1, 2])
+    dim = G * rnd.choice([1, 7, 16, 48, 96, 200])
+    dt_ = rnd.choice([torch.float32, torch.bfloat16, torch.float16])
+    with_z, with_D, with_bias = rnd.random() < 0.7, rnd.random() < 0.7, rnd.random() < 0.7
+    rank = rnd.choice([0, 0, 1, 7, 16, 48, 64])
+    strided = rnd.random() < 0.3
+    _say(f"state update random {i}: batch {batch} dim {dim} dstate {N} groups {G} {dt_} z {with_z} D {with_D} "
+         f"bias {with_bias} rank {rank} strided {strided}")
+    gen = torch.Generator().manual_seed(3500 + i)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    x, z = r(batch, dim).to(dt_), r(batch, dim).to(dt_)
+    xdb = (0.3 * r(batch, rank + 2 * G * N)).to(dt_)       # [dt_low | B | C], B and C as column slices
+    B = xdb[:, rank:rank + G * N].reshape(batch, G, N)
+    C = xdb[:, rank + G * N:].reshape(batch, G, N)
+    A = -torch.rand(dim, N, generator=gen) * 3
+    D, bias = r(dim), r(dim) * 0.5
+    state0 = r(batch, dim, N)
+    if rank:
+        w = (r(dim, rank) / rank ** 0.5).to(dt_)
+        dt64 = (xdb[:, :rank].double() @ w.double().t()).to(dt_).double()
+    else:
+        dtv = r(batch, dim).to(dt_)
+        dt64 = dtv.double()
+    if strided:
+        big = torch.zeros(batch, dim, 2 * N, device=DEV)
+        big[..., ::2] = state0.to(DEV)
+        st = big[..., ::2]
+    else:
+        st = state0.to(DEV).clone()
+    xdb_d = xdb.to(DEV)
+    Bd = xdb_d[:, rank:rank + G * N].view(batch, G, N)
+    Cd = xdb_d[:, rank + G * N:].view(batch, G, N)
+    dt_arg = (xdb_d[:, :rank], w.to(DEV)) if rank else dtv.to(DEV)
+    out = selective_state_update(st, x.to(DEV), dt_arg, A.to(DEV), Bd, Cd, D.to(DEV) if with_D else None,
+                                 z=z.to(DEV) if with_z else None, dt_bias=bias.to(DEV) if with_bias else None,
+                                 dt_softplus=True)
+    want_out, want_st = selective_state_update_ref(state0.double(), x.double(), dt64, A.double(), B.double(),
+                                                   C.double(), D.double() if with_D else None,
+                                                   z=z.double() if with_z else None,
+                                                   dt_bias=bias.double() if with_bias else None, dt_softplus=True)
+    tol = TOL[dt_]
+    stol = 1e-4 if rank == 0 or dt_ == torch.float32 else tol
+    assert_close(st.cpu().double(), want_st, stol, stol, "state")
+    assert_close(out.cpu().double(), want_out.double(), tol, tol, "out")
+
+
 @pytest.mark.parametrize("width,bias,act,dt_", [(4, True, "silu", torch.float32), (3, False, None, torch.float32),
                                                 (1, True, "silu", torch.bfloat16), (2, True, "silu", torch.float16),
                                                 (4, False, "silu", torch.bfloat16)])

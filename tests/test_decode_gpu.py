@@ -520,8 +520,11 @@ def test_decode_linear_fused_norm(case):
     y, s = dlm.decode_linear(x, w, b, conv=(st_f, cw, cb, "silu") if cdim else None, norm=(res, nw, 1e-5))
     normed, s_r = rms_norm_fn(x, nw, res, 1e-5, prenorm=True)
     st_r = st0.clone() if cdim else None
-    # (unsplit: the fused launch does not split K, so the sums run in its order)
-    y_r = dlm.decode_linear(normed, w, b, conv=(st_r, cw, cb, "silu") if cdim else None, split=False)
+    # the fused launch (k_in up to 1024) does not split K, so the reference runs
+    # unsplit; above that the op runs the RMSNorm kernel, then decode_linear as
+    # usual (split where the library splits), and so does the reference
+    fused = k <= 1024
+    y_r = dlm.decode_linear(normed, w, b, conv=(st_r, cw, cb, "silu") if cdim else None, split=not fused)
     torch.cuda.synchronize()
     assert torch.equal(s, s_r), "residual stream"
     assert torch.equal(y, y_r), "output"
@@ -529,3 +532,20 @@ def test_decode_linear_fused_norm(case):
         assert torch.equal(st_f, st_r), "conv state"
     want = normed.float() @ w.float().t() + b.float()
     assert_close(y[:, cdim:].float().cpu(), want[:, cdim:].cpu(), 1e-2, 1e-2 * float(want.abs().max()), "vs fp32")
+
+
+@pytest.mark.parametrize("i", range(20))
+def test_decode_linear_fused_norm_random(i):
+    # seeded random shapes through the same bit-for-bit checks: batch 1 to 64,
+    # k_in a multiple of 16 up to 1024 (and above, where the RMSNorm kernel runs
+    # first), ragged output tiles, fp32 or row-dtype norm weight, with and
+    # without residual and conv channels
+    import random
+    rnd = random.Random(1700 + i)
+    batch = rnd.choice([1, 2, 5, 16, 17, 33, 64])
+    k = 16 * rnd.choice([1, 3, 8, 24, 48, 64, 80])
+    n = rnd.choice([16, 37, 80, 200, 512, 1008])
+    cdim = rnd.choice([0, 0, n, max(1, n // 2)])
+    case = (batch, k, n, rnd.random() < 0.7, rnd.choice([None, torch.float32]), cdim,
+            rnd.choice([torch.bfloat16, torch.float16]))
+    test_decode_linear_fused_norm(case)

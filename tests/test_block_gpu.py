@@ -8,7 +8,9 @@
   width, dtype, bias, SiLU, padded channel rows, atomic or fixed-order
   dweight / dbias sums) against float64 autograd of the conv oracle;
 * mamba_inner_fn forward and backward (all 14 differentiable inputs)
-  against float64 autograd of mamba_inner_ref;
+  against float64 autograd of mamba_inner_ref, also on 12 seeded random
+  shapes (d_inner not a multiple of 16, ragged seqlens, dstate other than
+  16, odd dt_rank, with and without biases);
 * MambaSimple (both forward paths) and CausalLM against the oracle, with
   the same weights;
 * a no-grad MambaSimple forward (fp32 parameters cached by version) equal bit
@@ -175,6 +177,46 @@ def test_mamba_inner_fn(dt):
     def close(a, b, what):
         assert_close(a, b, rtol, atol * max(1.0, float(b.detach().abs().max())), what)
     close(out.float().cpu(), ref, "out")
+    close(xzg.grad.float().cpu(), xzr.grad, "dxz")
+    for k in p:
+        if p[k] is not None:
+            close(gp[k].grad.float().cpu(), rp[k].grad, f"d{k}")
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_mamba_inner_fn_random(i):
+    import random
+    from mamba_amd.ops.selective_scan_interface import mamba_inner_fn
+    rnd = random.Random(2100 + i)
+    batch = rnd.choice([1, 2, 3])
+    d_model = rnd.choice([8, 16, 24, 32])
+    dim = rnd.choice([16, 24, 40, 64, 80])
+    L = rnd.choice([1, 5, 16, 33, 64, 100, 127, 200, rnd.randint(1, 300)])
+    R = rnd.choice([1, 3, 4, 8])
+    N = rnd.choice([16, 16, 4, 8, 32])
+    width = rnd.choice([2, 3, 4])
+    dt = rnd.choice([torch.float32, torch.float32, torch.bfloat16])
+    out_bias, conv_bias = rnd.random() < 0.5, rnd.random() < 0.5
+    _say(f"mamba_inner_fn random {i}: batch {batch} d_model {d_model} dim {dim} seqlen {L} rank {R} dstate {N} "
+         f"width {width} {dt} out_bias {out_bias} conv_bias {conv_bias}")
+    p = _block_params(d_model, dim, R, N, width, dt, seed=2200 + i, out_bias=out_bias, conv_bias=conv_bias)
+    g = torch.Generator().manual_seed(2300 + i)
+    xz = torch.randn(batch, 2 * dim, L, generator=g).to(dt)
+    dres = torch.randn(batch, L, d_model, generator=g).to(dt)
+    gp = {k: (v.to(DEV).requires_grad_(True) if v is not None else None) for k, v in p.items()}
+    xzg = xz.to(DEV).requires_grad_(True)
+    out = mamba_inner_fn(xzg, *(gp[k] for k in ARGS), D=gp["D"], delta_bias=gp["delta_bias"], delta_softplus=True)
+    out.backward(dres.to(DEV))
+    torch.cuda.synchronize()
+    rp = {k: (v.double().requires_grad_(True) if v is not None else None) for k, v in p.items()}
+    xzr = xz.double().requires_grad_(True)
+    ref = mamba_inner_ref(xzr, *(rp[k] for k in ARGS), D=rp["D"], delta_bias=rp["delta_bias"], delta_softplus=True)
+    ref.backward(dres.double())
+    rtol, atol = TOL[dt]
+
+    def close(a, b, what):
+        assert_close(a, b, rtol, atol * max(1.0, float(b.detach().abs().max())), what)
+    close(out.detach().float().cpu(), ref.detach(), "out")
     close(xzg.grad.float().cpu(), xzr.grad, "dxz")
     for k in p:
         if p[k] is not None:

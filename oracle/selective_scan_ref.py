@@ -1,6 +1,6 @@
 """CPU oracle for the selective scan (test infrastructure only).
 
-This module is the checker, never the product: only ``tests/``, the
+This module is test infrastructure, never the product: only ``tests/``, the
 ``__graft_entry__.smoke()`` check and the ``cpu_baseline`` leg of ``bench.py``
 may import it.  The product path (``mamba_amd``) runs on the HIP library and
 fails loudly when that library is missing.

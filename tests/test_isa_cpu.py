@@ -80,8 +80,8 @@ def test_waterfall_check_finds_a_planted_one():
     assert isa_check.waterfalls_in_main_loop(code_after) == []
 
 
-def test_checker_catches_planted_hazards():
-    """The checker itself flags a DPP read 1 wait state after the write, a
+def test_isa_check_catches_planted_hazards():
+    """isa_check itself flags a DPP read 1 wait state after the write, a
     transcendental result read at once, and a packed fp32 op."""
     bad = ["v_mul_f32_e32 v1, 0x40400000, v1",
            "s_waitcnt vmcnt(2)",

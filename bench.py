@@ -558,7 +558,7 @@ def main():
         args.warmup = 100 if scan else 5
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+        print(f"bench.py: the benchmark runs on one GPU only (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE {world}); the selective scan would shard by batch or channel "
               "with one exchange of dA / dD / delta-bias (or dB / dC) gradients, which is not built here.",
               file=sys.stderr)

@@ -840,9 +840,21 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
 
     struct Ck { float d, o, z, C; };
     // steps past a ragged sequence's end (the last segment's last chunks) are
-    // identity steps: delta' = 0, dout = 0, C = 0, loads clamped to the end
+    // identity steps: delta' = 0, dout = 0, C = 0, loads clamped to the end.
+    // Chunks wholly inside the sequence load at a fixed per-lane offset plus
+    // the chunk's uniform offset (no per-load address arithmetic).
     const int64_t L = p.seqlen;
+    const uint32_t od = uint32_t(row * p.dl_ds + r) * es, oo = uint32_t(row * q.do_ds + r) * es;
+    const uint32_t oz = uint32_t(row * p.z_ds + r) * es, oC = uint32_t(row * p.C_ns + r) * es;
     auto fetch = [&](int ck, Ck& P) {
+        if (int64_t(ck) * kT + kT <= L) {
+            const uint32_t so = uint32_t(ck * kT) * es;
+            P.d = bload<IT>(Rd, od, so);
+            P.o = bload<IT>(Ro, oo, so);
+            P.z = kZ ? bload<IT>(Rz, oz, so) : 0.f;
+            P.C = bload<IT>(RC, oC, so);
+            return;
+        }
         const int t = ck * kT + r;
         const bool in = t < L;
         const int te = in ? t : int(L) - 1;

@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // are the first two this kernel runs (the tail), made of identity steps
     const int nck = int((L + 2 * kT - 1) / (2 * kT)) * 2;   // below 2^22 (seqlen < 2^26)
     // this workgroup's chunks [k0, k1), an even number starting at an even index
-    const int k0 = seg * (nck / nseg), k1 = k0 + nck / nseg;
+    const int k0 = 2 * seg_begin(seg, nck / 2, nseg), k1 = 2 * seg_begin(seg + 1, nck / 2, nseg);
 
     // Buffer resources at the workgroup's rows; lane (row, r) owns step r of
     // channel c0 + row and, for the B / C staging, step r of state row.  The
@@ -824,8 +824,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
     const int64_t c0 = (blk % nblk) * kChPerWG;
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
-    const int nck_seg = int((p.seqlen + 2 * kT - 1) / (2 * kT)) * 2 / p.nseg;   // padded as in ss_bwd_fast
-    const int k0 = seg * nck_seg, k1 = k0 + nck_seg;
+    const int npairs = int((p.seqlen + 2 * kT - 1) / (2 * kT));   // chunk pairs, padded as in ss_bwd_fast
+    const int k0 = 2 * seg_begin(seg, npairs, p.nseg), k1 = 2 * seg_begin(seg + 1, npairs, p.nseg);
 
     constexpr int64_t es64 = sizeof(IT);
     const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
@@ -907,16 +907,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
 
 bool bwd_fast_ok(const BwdParams& q);
 
-// Segments for the backward: as for the forward (enough for 768
-// workgroups), each segment an even number of at least 16 chunks.
+// Segments for the backward (seg_count): whole chunk pairs, at least 8
+// pairs (16 chunks) each.
 int bwd_segments(const BwdParams& q) {
     if (!bwd_fast_ok(q)) return 1;
     const FwdParams& p = q.f;
-    const int64_t wgs = p.batch * (p.dim / kChPerWG);
-    const int64_t nck = (p.seqlen + 2 * kT - 1) / (2 * kT) * 2;   // padded to an even count
-    int nseg = 1;
-    while (wgs * nseg < 768 && 2 * nseg <= 64 && nck % (4 * nseg) == 0 && nck / (2 * nseg) >= 16) nseg *= 2;
-    return nseg;
+    return seg_count(p.batch * (p.dim / kChPerWG), (p.seqlen + 2 * kT - 1) / (2 * kT), 8);
 }
 
 bool bwd_fast_ok(const BwdParams& q) {

@@ -269,8 +269,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     // super-chunks, the last one partial when seqlen is not a multiple of 64
     // (below 2^20); the last segment ends with that partial one, the tail
     const int nsc_pad = int((p.seqlen + kSC - 1) / kSC);
-    const int nsc_seg = nsc_pad / nseg;
-    const int sc0 = seg * nsc_seg, sc1 = sc0 + nsc_seg;
+    const int sc0 = seg_begin(seg, nsc_pad, nseg), sc1 = seg_begin(seg + 1, nsc_pad, nseg);
     const int lt = int(p.seqlen - int64_t(nsc_pad - 1) * kSC);   // steps of the last super-chunk, 1..64
     const bool tail = seg == nseg - 1 && lt < kSC;
     const int scf = tail ? sc1 - 1 : sc1;                       // end of the full super-chunks
@@ -556,8 +555,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     const int64_t c = c0 + row;
     const int64_t g = c0 / p.dpg;
     // segments 0 .. nseg - 2 only: whole super-chunks (the tail ends the last)
-    const int nsc_seg = int((p.seqlen + kSC - 1) / kSC) / p.nseg;
-    const int sc0 = seg * nsc_seg, sc1 = sc0 + nsc_seg;
+    const int nsc_pad = int((p.seqlen + kSC - 1) / kSC);
+    const int sc0 = seg_begin(seg, nsc_pad, p.nseg), sc1 = seg_begin(seg + 1, nsc_pad, p.nseg);
 
     constexpr int64_t es64 = sizeof(IT);
     const rsrc_t Ru = make_rsrc_in(p.u, (b * p.u_bs + c0 * p.u_ds) * es64, p.u_end);
@@ -627,23 +626,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     if (r == 0) p.seg_s[si] = dsum;
 }
 
-// Segments for the forward: enough that batch x channel blocks x segments
-// reaches kSegTargetWGs workgroups (three per CU), each segment a whole
-// number of at least kSegMinSC super-chunks; 1 (serial) when the batch
-// already fills the GPU or the fast path does not apply.
+// Segments for the forward (seg_count): at least kSegMinSC super-chunks
+// each; 1 (serial) when the fast path does not apply.
 bool fwd_fast_ok(const FwdParams& p);
-constexpr int64_t kSegTargetWGs = 768;
 constexpr int kSegMinSC = 4;
-constexpr int kSegMax = 64;
 int fwd_segments(const FwdParams& p) {
     if (!fwd_fast_ok(p)) return 1;
-    const int64_t wgs = p.batch * (p.dim / kChPerWG);
-    const int64_t nsc = (p.seqlen + kSC - 1) / kSC;     // the last one partial for a ragged seqlen
-    int nseg = 1;
-    while (wgs * nseg < kSegTargetWGs && 2 * nseg <= kSegMax && nsc % (2 * nseg) == 0 &&
-           nsc / (2 * nseg) >= kSegMinSC)
-        nseg *= 2;
-    return nseg;
+    return seg_count(p.batch * (p.dim / kChPerWG), (p.seqlen + kSC - 1) / kSC, kSegMinSC);
 }
 
 bool fwd_fast_ok(const FwdParams& p) {

@@ -112,6 +112,23 @@ hipError_t launch_fwd(const FwdParams& p, int itype, hipStream_t stream);
 hipError_t launch_bwd(const BwdParams& p, int itype, hipStream_t stream);
 // causal depthwise conv1d (+ SiLU); g == nullptr: forward, else backward
 hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, hipStream_t stream);
+// Sequence segments of the fast scans.  A launch of wgs workgroups (batch x
+// channel blocks) doubles its segment count while it has fewer than
+// kSegSlots workgroups (three per CU), up to kSegMax segments of at least
+// min_units units each (super-chunks forward, chunk pairs backward); 1 when
+// the batch already fills the GPU.  Segment s covers units [seg_begin(s),
+// seg_begin(s + 1)), so any unit count splits (lengths differ by at most
+// one unit).  (Counts that fit every segment into one round, such as 6 at
+// 128 workgroups, measured the same as the doubled 8.)
+constexpr int64_t kSegSlots = 768;
+constexpr int kSegMax = 64;
+inline int seg_count(int64_t wgs, int64_t units, int min_units) {
+    int n = 1;
+    while (wgs * n < kSegSlots && 2 * n <= kSegMax && units / (2 * n) >= min_units) n *= 2;
+    return n;
+}
+__host__ __device__ inline int seg_begin(int s, int units, int nseg) { return int(int64_t(s) * units / nseg); }
+
 // bytes of the backward's fixed-order partials (batch x dim x tiles x 5 floats)
 int64_t conv1d_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen);
 // single-token decode: selective-scan state update and conv1d state update

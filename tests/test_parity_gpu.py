@@ -218,8 +218,11 @@ def test_forward_without_checkpoints(shape):
     assert torch.equal(out3, out1) and torch.equal(last3, last)
 
 
+# the last two: segment counts that do not divide the sequence's super-chunks
+# (469 into 64 segments of 7 or 8; 79 into 16 of 4 or 5)
 SEG_CASES = [(1, 64, 16, 4096, torch.float32), (2, 32, 16, 2048, torch.bfloat16),
-             (1, 1536, 16, 8192, torch.bfloat16), (1, 64, 16, 4093, torch.float32)]
+             (1, 1536, 16, 8192, torch.bfloat16), (1, 64, 16, 4093, torch.float32),
+             (1, 64, 16, 30000, torch.float32), (1, 96, 16, 5000, torch.bfloat16)]
 
 
 @pytest.mark.parametrize("shape", SEG_CASES, ids=[f"b{c[0]}-d{c[1]}-l{c[3]}-{str(c[4]).split('.')[-1]}"
@@ -277,8 +280,9 @@ def test_sequence_parallel_forward_then_backward_matches_oracle():
 
 
 @pytest.mark.parametrize("shape", [(1, 64, 16, 4096, torch.float32), (1, 1536, 16, 8192, torch.bfloat16),
-                                   (1, 64, 16, 4093, torch.float32)],
-                         ids=["b1-d64-l4096-f32", "b1-d1536-l8192-bf16", "b1-d64-l4093-f32"])
+                                   (1, 64, 16, 4093, torch.float32), (1, 64, 16, 30000, torch.float32)],
+                         ids=["b1-d64-l4096-f32", "b1-d1536-l8192-bf16", "b1-d64-l4093-f32",
+                              "b1-d64-l30000-f32-uneven"])
 def test_sequence_parallel_backward(shape):
     """Small batches: the backward's segments (adjoint carries scanned in parallel
     and joined) give the serial backward's gradients (to rounding)."""

@@ -446,8 +446,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const rsrc_t Rdu = make_rsrc_in(q.du, (b * q.du_bs + c0 * q.du_ds) * es64, q.du_end);
     const rsrc_t Rdd = make_rsrc_in(q.ddelta, (b * q.dd_bs + c0 * q.dd_ds) * es64, q.dd_end);
     const rsrc_t Rdz = kZ ? make_rsrc_in(q.dz, (b * q.dz_bs + c0 * q.dz_ds) * es64, q.dz_end) : make_rsrc_n(nullptr, 0);
-    // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain
-    const rsrc_t Rx = make_rsrc_in(p.x, (b * p.n_chunks * p.dim + c0) * kT * 4, p.x_end);
+    // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain,
+    // through a resource based at its chunk (offsets from the row's first
+    // chunk would pass 2^32 bytes once seqlen x dim reaches 2^30)
+    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
+    const int64_t x_chunk_bytes = p.dim * kT * 4;
+    auto x_rsrc = [&](int ck) { return make_rsrc_in(p.x, x_off + int64_t(ck) * x_chunk_bytes, p.x_end); };
     // dB / dC of this batch row and group, or of its slice of the workspace
     // (rows of ld floats)
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
@@ -465,7 +469,6 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const uint32_t odu = uint32_t(row * q.du_ds + r) * es, odd = uint32_t(row * q.dd_ds + r) * es;
     const uint32_t odz = uint32_t(row * q.dz_ds + r) * es;
     const uint32_t ox = uint32_t(row * kT + r) * 4u;
-    const uint32_t x_chunk_bytes = uint32_t(p.dim * kT * 4);
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -502,7 +505,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         }
         P.B = bload<IT>(RB, oB, so);
         P.C = bload<IT>(RC, oC, so);
-        const float v = bload<float>(Rx, ox, uint32_t(ck > 0 ? ck - 1 : 0) * x_chunk_bytes);
+        const float v = bload<float>(x_rsrc(ck > 0 ? ck - 1 : 0), ox, 0);
         P.x = ck > 0 ? v : 0.f;
     };
     // A chunk of the tail: loads at steps clamped to the sequence, and past
@@ -525,7 +528,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         }
         P.B = in ? bload<IT>(RB, uint32_t(row * p.B_ns + te) * es, 0) : 0.f;
         P.C = in ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
-        const float v = bload<float>(Rx, ox, uint32_t(ck > 0 ? ck - 1 : 0) * x_chunk_bytes);
+        const float v = bload<float>(x_rsrc(ck > 0 ? ck - 1 : 0), ox, 0);
         P.x = ck > 0 ? v : 0.f;
     };
     // this lane's element of the B / C tile (state row, step r) into buffer buf
@@ -918,13 +921,14 @@ int bwd_segments(const BwdParams& q) {
 bool bwd_fast_ok(const BwdParams& q) {
     const FwdParams& p = q.f;
     // every byte offset the kernel forms stays below 2^32: rows and seqlen
-    // below 2^26 elements, and the checkpoint offset (chunk x dim x 64 B)
+    // below 2^26 elements, checkpoints addressed from their own chunk (dim
+    // below 2^24)
     // (a seqlen that is not a multiple of 32 ends in identity-padded chunks)
     return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 1 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && (!p.has_z || p.y != nullptr) &&
            small_strides({p.seqlen + 2 * kT, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
                           q.do_ds, q.du_ds, q.dd_ds, q.dz_ds}) &&
-           p.seqlen * p.dim < (int64_t(1) << 30);
+           p.dim < (int64_t(1) << 24);
 }
 
 // ------------------------------------------------------- dB / dC slices --

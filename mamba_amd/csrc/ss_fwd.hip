@@ -290,18 +290,23 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const int64_t y_end = kZ ? p.y_end : 0;
     // x: (batch, chunk, dim, dstate)
     const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
-    const rsrc_t Rx = make_rsrc_in(p.x, x_off, p.x_end);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
     const uint32_t oz = uint32_t(row * p.z_ds + 4 * r) * es;
     const uint32_t oB = uint32_t(row * p.B_ns + 4 * r) * es, oC = uint32_t(row * p.C_ns + 4 * r) * es;
     const uint32_t oo = uint32_t(row * p.o_ds + 4 * r) * es, oy = uint32_t(row * p.y_ds + 4 * r) * es;
     const uint32_t ox = uint32_t(row * kT + r) * 4u;
-    const uint32_t x_chunk_bytes = uint32_t(p.dim * kT * 4);
+    const int64_t x_chunk_bytes = p.dim * kT * 4;          // below 2^30 (dim below 2^24)
     // the tail's checkpoints: a resource that ends with this batch row's
     // n_chunks chunks, so the stores of chunks past the sequence are dropped
     const int64_t x_row_end = (b + 1) * p.n_chunks * p.dim * kT * 4;
-    const rsrc_t Rx_tail = make_rsrc_in(p.x, x_off, p.x_end < x_row_end ? p.x_end : x_row_end);
+    const int64_t x_tail_end = p.x_end < x_row_end ? p.x_end : x_row_end;
+    // the checkpoints of super-chunk sc through a resource based at its first
+    // chunk: offsets from the row's first chunk would pass 2^32 bytes once
+    // seqlen x dim reaches 2^30
+    auto x_rsrc = [&](int sc, bool tail) {
+        return make_rsrc_in(p.x, x_off + int64_t(kQ * sc) * x_chunk_bytes, tail ? x_tail_end : p.x_end);
+    };
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -452,6 +457,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             }
         }
         dpp_sources_ready4(dt, dtu);
+        const rsrc_t Rx = x_rsrc(sc, kTail);
         const float* sB = s_bc + (buf * 2 + 0) * 16 * kSC;
         const float* sC = s_bc + (buf * 2 + 1) * 16 * kSC;
 
@@ -492,7 +498,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                 h = __builtin_fmaf(a[k], h, bmul<4 * q + k / 4>(f4get(dtu, k % 4), Bq[k]));
                 yp[k] = h;
             });
-            bstore<float, kStoreNT>(kTail ? Rx_tail : Rx, ox, uint32_t(kQ * sc + q) * x_chunk_bytes, h);
+            bstore<float, kStoreNT>(Rx, ox, uint32_t(q * x_chunk_bytes), h);
 #pragma unroll
             for (int m = 0; m < 4; ++m)
                 *reinterpret_cast<float4*>(yrow + r * 16 + 4 * (m ^ ((r >> 1) & 3))) =
@@ -637,12 +643,13 @@ int fwd_segments(const FwdParams& p) {
 
 bool fwd_fast_ok(const FwdParams& p) {
     // every byte offset the kernel forms stays below 2^32: rows and seqlen
-    // below 2^26 elements, and the checkpoint offset (chunk x dim x 64 B)
+    // below 2^26 elements, checkpoints addressed from each super-chunk's
+    // first chunk (dim below 2^24)
     // (a seqlen that is not a multiple of 64 ends in a partial super-chunk)
     return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 1 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 &&
            small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns}) &&
-           p.seqlen * p.dim < (int64_t(1) << 30);
+           p.dim < (int64_t(1) << 24);
 }
 
 template <typename IT>

@@ -446,12 +446,6 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const rsrc_t Rdu = make_rsrc_in(q.du, (b * q.du_bs + c0 * q.du_ds) * es64, q.du_end);
     const rsrc_t Rdd = make_rsrc_in(q.ddelta, (b * q.dd_bs + c0 * q.dd_ds) * es64, q.dd_end);
     const rsrc_t Rdz = kZ ? make_rsrc_in(q.dz, (b * q.dz_bs + c0 * q.dz_ds) * es64, q.dz_end) : make_rsrc_n(nullptr, 0);
-    // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain,
-    // through a resource based at its chunk (offsets from the row's first
-    // chunk would pass 2^32 bytes once seqlen x dim reaches 2^30)
-    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
-    const int64_t x_chunk_bytes = p.dim * kT * 4;
-    auto x_rsrc = [&](int ck) { return make_rsrc_in(p.x, x_off + int64_t(ck) * x_chunk_bytes, p.x_end); };
     // dB / dC of this batch row and group, or of its slice of the workspace
     // (rows of ld floats)
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
@@ -469,6 +463,24 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const uint32_t odu = uint32_t(row * q.du_ds + r) * es, odd = uint32_t(row * q.dd_ds + r) * es;
     const uint32_t odz = uint32_t(row * q.dz_ds + r) * es;
     const uint32_t ox = uint32_t(row * kT + r) * 4u;
+    // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain,
+    // through a resource based at a window of chunks whose offsets stay below
+    // 2^31 bytes (offsets from the row's first chunk would pass 2^32 once
+    // seqlen x dim reaches 2^30); the chunks run last to first, and a window
+    // is rebased (to end at the chunk) when a chunk leaves it, which at most
+    // rows never happens
+    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
+    const int64_t x_chunk_bytes = p.dim * kT * 4;
+    const int x_wck = int((int64_t(1) << 31) / x_chunk_bytes) > 0 ? int((int64_t(1) << 31) / x_chunk_bytes) : 1;
+    int x_w0 = k1 - x_wck > 0 ? k1 - x_wck : 0;
+    rsrc_t Rx = make_rsrc_in(p.x, x_off + int64_t(x_w0) * x_chunk_bytes, p.x_end);
+    auto x_load = [&](int ckx) {
+        if (ckx < x_w0) {
+            x_w0 = ckx - x_wck + 1 > 0 ? ckx - x_wck + 1 : 0;
+            Rx = make_rsrc_in(p.x, x_off + int64_t(x_w0) * x_chunk_bytes, p.x_end);
+        }
+        return bload<float>(Rx, ox, uint32_t(ckx - x_w0) * uint32_t(x_chunk_bytes));
+    };
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -505,7 +517,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         }
         P.B = bload<IT>(RB, oB, so);
         P.C = bload<IT>(RC, oC, so);
-        const float v = bload<float>(x_rsrc(ck > 0 ? ck - 1 : 0), ox, 0);
+        const float v = x_load(ck > 0 ? ck - 1 : 0);
         P.x = ck > 0 ? v : 0.f;
     };
     // A chunk of the tail: loads at steps clamped to the sequence, and past
@@ -528,7 +540,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         }
         P.B = in ? bload<IT>(RB, uint32_t(row * p.B_ns + te) * es, 0) : 0.f;
         P.C = in ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
-        const float v = bload<float>(x_rsrc(ck > 0 ? ck - 1 : 0), ox, 0);
+        const float v = x_load(ck > 0 ? ck - 1 : 0);
         P.x = ck > 0 ? v : 0.f;
     };
     // this lane's element of the B / C tile (state row, step r) into buffer buf

@@ -301,12 +301,15 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     // n_chunks chunks, so the stores of chunks past the sequence are dropped
     const int64_t x_row_end = (b + 1) * p.n_chunks * p.dim * kT * 4;
     const int64_t x_tail_end = p.x_end < x_row_end ? p.x_end : x_row_end;
-    // the checkpoints of super-chunk sc through a resource based at its first
-    // chunk: offsets from the row's first chunk would pass 2^32 bytes once
-    // seqlen x dim reaches 2^30
-    auto x_rsrc = [&](int sc, bool tail) {
-        return make_rsrc_in(p.x, x_off + int64_t(kQ * sc) * x_chunk_bytes, tail ? x_tail_end : p.x_end);
-    };
+    // the checkpoints through resources based at a window of super-chunks
+    // whose offsets stay below 2^31 bytes (offsets from the row's first chunk
+    // would pass 2^32 once seqlen x dim reaches 2^30); a window is rebased
+    // when a super-chunk leaves it, which at most rows never happens
+    const int x_wsc = int((int64_t(1) << 31) / (kQ * x_chunk_bytes)) > 0
+                          ? int((int64_t(1) << 31) / (kQ * x_chunk_bytes)) : 1;
+    int x_w0 = sc0;
+    rsrc_t Rx_w = make_rsrc_in(p.x, x_off + int64_t(kQ * sc0) * x_chunk_bytes, p.x_end);
+    rsrc_t Rx_wt = make_rsrc_in(p.x, x_off + int64_t(kQ * sc0) * x_chunk_bytes, x_tail_end);
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -457,7 +460,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             }
         }
         dpp_sources_ready4(dt, dtu);
-        const rsrc_t Rx = x_rsrc(sc, kTail);
+        if (sc >= x_w0 + x_wsc) {
+            x_w0 = sc;
+            Rx_w = make_rsrc_in(p.x, x_off + int64_t(kQ * sc) * x_chunk_bytes, p.x_end);
+            Rx_wt = make_rsrc_in(p.x, x_off + int64_t(kQ * sc) * x_chunk_bytes, x_tail_end);
+        }
+        const rsrc_t Rx = kTail ? Rx_wt : Rx_w;
+        const uint32_t x_so = uint32_t((sc - x_w0) * kQ) * uint32_t(x_chunk_bytes);
         const float* sB = s_bc + (buf * 2 + 0) * 16 * kSC;
         const float* sC = s_bc + (buf * 2 + 1) * 16 * kSC;
 
@@ -498,7 +507,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                 h = __builtin_fmaf(a[k], h, bmul<4 * q + k / 4>(f4get(dtu, k % 4), Bq[k]));
                 yp[k] = h;
             });
-            bstore<float, kStoreNT>(Rx, ox, uint32_t(q * x_chunk_bytes), h);
+            bstore<float, kStoreNT>(Rx, ox, x_so + uint32_t(q * x_chunk_bytes), h);
 #pragma unroll
             for (int m = 0; m < 4; ++m)
                 *reinterpret_cast<float4*>(yrow + r * 16 + 4 * (m ^ ((r >> 1) & 3))) =

@@ -634,7 +634,15 @@ def test_forward_workspace_query(nat, lib):
     a = valid_fwd(nat, batch=1, dim=64, seqlen=4096)
     assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 1 * 16 * 64 * 17 * 4       # 4 blocks: 64 / 16 = 4 sc each
     a = valid_fwd(nat, batch=1, dim=64, seqlen=100)
-    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 0                           # general kernel: serial
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 0                           # too short to split
+    # segment counts need not divide the super-chunk count (469 here)
+    a = valid_fwd(nat, batch=1, dim=1536, seqlen=30000)
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 1 * 8 * 1536 * 17 * 4
+    a = valid_fwd(nat, batch=1, dim=64, seqlen=30000)
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 1 * 64 * 64 * 17 * 4
+    # seqlen x dim above 2^30 stays on the fast path (65 blocks -> 16 segments)
+    a = valid_fwd(nat, batch=1, dim=1040, seqlen=(1 << 20) + 37)
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == 1 * 16 * 1040 * 17 * 4
     a.u = None
     assert lib.ss_fwd_workspace_bytes(ctypes.byref(a)) == -1
 

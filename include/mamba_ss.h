@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 15
+#define SS_ABI_VERSION 16
 
 /* element types of u / delta / z / out / dout / du / ddelta / dz / variable B, C */
 enum ss_dtype { SS_F32 = 0, SS_BF16 = 1, SS_F16 = 2 };
@@ -99,6 +99,16 @@ typedef struct ss_fwd_args {
        Results agree to rounding.  Calls that overlap must not share it. */
     void* workspace;
     int64_t workspace_bytes;
+    /* 0, or at most 2^31: the byte span of x that one buffer resource of the
+       fast kernels addresses (ABI v16).  The kernels address the checkpoints
+       of a batch row through a resource based at a window of chunks whose
+       offsets stay below this span, and rebase it when a chunk leaves the
+       window; 0 means 2^31, where rows below 2^31 bytes of checkpoints
+       (seqlen x dim below 2^25) use one window.  Results do not depend on
+       it: a smaller span only rebases more often (at least one chunk, or one
+       64-step super-chunk in the forward, per window).  For tests of the
+       rebasing. */
+    int64_t x_window_bytes;
 } ss_fwd_args;
 
 typedef struct ss_bwd_args {
@@ -418,7 +428,11 @@ int ss_conv1d_update(const ss_conv1d_update_args* a, void* stream);
  * must equal batch, norm->dim equal k_in (at most 1024), norm->dtype equal
  * dtype; norm->x, residual and residual_out need 16-byte aligned rows
  * (bases and row strides), weight 16-byte alignment.  The K split is not
- * used with it. */
+ * used with it.  Every output tile's workgroup reads norm->x and
+ * norm->residual while the first one writes residual_out, so residual_out
+ * must not overlap either (no in-place residual stream: SS_ERR_INVALID).
+ * In every form, y must not overlap the input rows (x, or norm's x,
+ * residual and residual_out): SS_ERR_INVALID. */
 typedef struct ss_decode_linear_args {
     int64_t batch, n_out, k_in;
     int32_t dtype;                       /* SS_BF16 or SS_F16: x, weight, y */

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "libmamba_ss.so")
 
 SS_F32, SS_BF16, SS_F16 = 0, 1, 2
 SS_OK, SS_ERR_INVALID, SS_ERR_UNSUPPORTED, SS_ERR_HIP = 0, 1, 2, 3
-ABI_VERSION = 15
+ABI_VERSION = 16
 # bytes of the fixed device scratch of ss_bwd_noalloc (SS_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -47,6 +47,7 @@ class FwdArgs(ctypes.Structure):
         ("D", _p), ("delta_bias", _p), ("z", _p), ("out", _p), ("x", _p),
         ("y", _p), ("y_batch_stride", _i64), ("y_dim_stride", _i64),
         ("last_state", _p), ("workspace", _p), ("workspace_bytes", _i64),
+        ("x_window_bytes", _i64),
     ]
 
 

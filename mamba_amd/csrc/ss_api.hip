@@ -38,6 +38,18 @@ size_t elem_size(int itype) { return itype == SS_F32 ? 4 : 2; }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Whether the byte ranges of two row arrays overlap: `rows` rows of p_cols
+// (q_cols) elements of es bytes, row strides in elements.  An absent array
+// overlaps nothing.
+bool rows_overlap(const void* p, int64_t p_stride, int64_t p_cols, const void* q, int64_t q_stride, int64_t q_cols,
+                  int64_t rows, size_t es) {
+    if (!p || !q || rows <= 0 || p_cols <= 0 || q_cols <= 0) return false;
+    const uintptr_t p0 = reinterpret_cast<uintptr_t>(p), q0 = reinterpret_cast<uintptr_t>(q);
+    const uintptr_t p1 = p0 + uintptr_t(((rows - 1) * p_stride + p_cols) * int64_t(es));
+    const uintptr_t q1 = q0 + uintptr_t(((rows - 1) * q_stride + q_cols) * int64_t(es));
+    return p0 < q1 && q0 < p1;
+}
+
 int64_t n_chunks_for(int64_t L) { return (L + ss::kChunk - 1) / ss::kChunk; }
 
 // Checks common to forward and backward.  `empty` is set when there is no
@@ -57,6 +69,8 @@ int check_fwd_common(const ss_fwd_args* a, bool* empty) {
             return fail(SS_ERR_INVALID, "dim=%lld is not a multiple of n_groups=%lld",
                         (long long)a->dim, (long long)a->n_groups);
     }
+    if (a->x_window_bytes < 0 || a->x_window_bytes > (int64_t(1) << 31))
+        return fail(SS_ERR_INVALID, "x_window_bytes=%lld outside [0, 2^31]", (long long)a->x_window_bytes);
     if (a->n_chunks != n_chunks_for(a->seqlen))
         return fail(SS_ERR_INVALID, "n_chunks=%lld, expected ceil(seqlen / %d) = %lld",
                     (long long)a->n_chunks, ss::kChunk, (long long)n_chunks_for(a->seqlen));
@@ -139,6 +153,7 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.B_end = p.var_B && N > 0 ? seq_end(p.B, B, G, L, p.B_bs, p.B_gs, es) + (N - 1) * p.B_ns * int64_t(es) : 0;
     p.C_end = p.var_C && N > 0 ? seq_end(p.C, B, G, L, p.C_bs, p.C_gs, es) + (N - 1) * p.C_ns * int64_t(es) : 0;
     p.x_end = p.x ? B * p.n_chunks * D * N * int64_t(sizeof(float)) : 0;
+    p.x_win = a->x_window_bytes > 0 ? a->x_window_bytes : (int64_t(1) << 31);
     return p;
 }
 
@@ -661,6 +676,16 @@ int ss_decode_linear(const ss_decode_linear_args* a, void* stream) {
                                   n->residual_out_row_stride >= n->dim)) &&
                                 aligned(n->weight, 16) && (!n->rstd || aligned(n->rstd, 4));
             if (!rows16) return fail(SS_ERR_INVALID, "the fused norm needs 16-byte aligned rows covering dim");
+            // every output tile's workgroup reads x and residual, and only the
+            // first writes residual_out: an in-place residual stream would let
+            // the other tiles normalise rows already updated
+            const size_t es = elem_size(n->dtype);
+            const int64_t d = n->dim;
+            if (n->residual &&
+                (rows_overlap(n->residual_out, n->residual_out_row_stride, d, n->x, n->x_row_stride, d, n->rows, es) ||
+                 rows_overlap(n->residual_out, n->residual_out_row_stride, d, n->residual, n->residual_row_stride, d,
+                              n->rows, es)))
+                return fail(SS_ERR_INVALID, "norm residual_out overlaps norm x or residual (no in-place residual)");
         }
     }
     if (a->batch == 0 || a->n_out == 0) return ok();
@@ -671,6 +696,19 @@ int ss_decode_linear(const ss_decode_linear_args* a, void* stream) {
     if ((!a->norm && !aligned(a->x, 8)) || !aligned(a->weight, 8) || !aligned(a->y, 2))
         return fail(SS_ERR_INVALID, "x / weight must be 8-byte aligned, y 2-byte aligned");
     if (a->bias && !aligned(a->bias, a->bias_dtype == SS_F32 ? 4 : 2)) return fail(SS_ERR_INVALID, "bias is misaligned");
+    {
+        // y is written while other workgroups still read the input rows
+        const size_t es = elem_size(a->dtype);
+        const ss_rmsnorm_args* n = a->norm;
+        const int64_t no = a->n_out, k = a->k_in, rows = a->batch;
+        const bool ov =
+            n ? (rows_overlap(a->y, a->y_row_stride, no, n->x, n->x_row_stride, k, rows, es) ||
+                 (n->residual && (rows_overlap(a->y, a->y_row_stride, no, n->residual, n->residual_row_stride, k, rows, es) ||
+                                  rows_overlap(a->y, a->y_row_stride, no, n->residual_out, n->residual_out_row_stride, k,
+                                               rows, es))))
+              : rows_overlap(a->y, a->y_row_stride, no, a->x, a->x_row_stride, k, rows, es);
+        if (ov) return fail(SS_ERR_INVALID, "y overlaps the input rows (x, or the norm's x / residual / residual_out)");
+    }
     if ((!a->norm && (a->x_row_stride < a->k_in || a->x_row_stride % 4)) || a->w_row_stride < a->k_in ||
         a->y_row_stride < a->n_out || a->w_row_stride % 4)
         return fail(SS_ERR_INVALID, "row strides must cover the rows, x / weight strides multiples of 4");

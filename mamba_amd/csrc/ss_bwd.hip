@@ -465,13 +465,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const uint32_t ox = uint32_t(row * kT + r) * 4u;
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain,
     // through a resource based at a window of chunks whose offsets stay below
-    // 2^31 bytes (offsets from the row's first chunk would pass 2^32 once
+    // p.x_win (2^31 bytes unless the caller set a smaller span; offsets from
+    // the row's first chunk would pass 2^32 once
     // seqlen x dim reaches 2^30); the chunks run last to first, and a window
     // is rebased (to end at the chunk) when a chunk leaves it, which at most
     // rows never happens
     const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
     const int64_t x_chunk_bytes = p.dim * kT * 4;
-    const int x_wck = int((int64_t(1) << 31) / x_chunk_bytes) > 0 ? int((int64_t(1) << 31) / x_chunk_bytes) : 1;
+    const int x_wck = int(p.x_win / x_chunk_bytes) > 0 ? int(p.x_win / x_chunk_bytes) : 1;
     int x_w0 = k1 - x_wck > 0 ? k1 - x_wck : 0;
     rsrc_t Rx = make_rsrc_in(p.x, x_off + int64_t(x_w0) * x_chunk_bytes, p.x_end);
     auto x_load = [&](int ckx) {
@@ -563,12 +564,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     };
     // (TAIL: the workspace's padded rows have slots for the steps past the
     // sequence.  In rows of seqlen floats, which only a call without
-    // workspace uses for a ragged seqlen, their sums (zero) go to steps inside
-    // it, so no address leaves the row: a chunk wholly past the sequence adds
-    // them onto the previous chunk's 16 steps, one per address (onto one
-    // address, all workgroups' adds of the chunk were serialised in the
-    // atomic unit: seqlen 2064 fp32 took 570 us against 338 us at 2048), a
-    // partial chunk onto the last step.)
+    // workspace uses for a ragged seqlen, their sums (zero, unless the state
+    // is not finite) go to steps inside it, so no address leaves the row: a
+    // chunk wholly past the sequence adds them onto the previous chunk's 16
+    // steps, clamped to the last step (onto one address for every lane, all
+    // workgroups' adds of the chunk were serialised in the atomic unit:
+    // seqlen 2064 fp32 took 570 us against 338 us at 2048), a partial chunk
+    // onto the last step.)
     auto flush_commit = [&](int ck, const float (&v)[2 * kWaves], auto TAIL) {
         const float sB = (v[0] + v[1]) + (v[2] + v[3]);
         const float sC = (v[4] + v[5]) + (v[6] + v[7]);
@@ -577,6 +579,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         if constexpr (decltype(TAIL)::value) {
             if (ck * kT >= ld) {
                 so = uint32_t((ck - 1) * kT) * 4u;
+                if ((ck - 1) * kT + ft >= L) ofl = uint32_t(fn * ld + int(L) - 1 - (ck - 1) * kT) * 4u;
             } else {
                 const int t = ck * kT + ft;
                 if (t >= ld) ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
@@ -680,12 +683,20 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                 float hprev;
                 if constexpr (k == 0) hprev = h0;
                 else hprev = hs[k - 1];
-                const float gah = ga * hprev;        // g_t a_t h_{t-1}
+                float gah = ga * hprev;              // g_t a_t h_{t-1}
+                // past the sequence (tail chunks): the state carried through the
+                // identity steps meets zero adjoints and inputs; those products
+                // are zero unless the state is not finite (0 * inf), and are
+                // dropped, so that no such NaN reaches dA or the dB / dC sums
+                // (whose past-the-end lanes go onto steps of the row)
+                const bool past = kTail && ck * kT + k >= L;
+                if constexpr (kTail) gah = past ? 0.f : gah;
                 bfmac<k>(dA_acc, dt, gah);
                 s2p[ki] = gah;                       // times A_n in the sum over states
                 s1p[ki] = gv * Bq[k];
                 dBp[ki] = bmul<k>(dtu, gv);
                 dCp[ki] = bmul<k>(dy, hs[k]);
+                if constexpr (kTail) dCp[ki] = past ? 0.f : dCp[ki];
             });
             // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
             float* trh = trw;

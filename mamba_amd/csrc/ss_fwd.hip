@@ -302,11 +302,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const int64_t x_row_end = (b + 1) * p.n_chunks * p.dim * kT * 4;
     const int64_t x_tail_end = p.x_end < x_row_end ? p.x_end : x_row_end;
     // the checkpoints through resources based at a window of super-chunks
-    // whose offsets stay below 2^31 bytes (offsets from the row's first chunk
-    // would pass 2^32 once seqlen x dim reaches 2^30); a window is rebased
-    // when a super-chunk leaves it, which at most rows never happens
-    const int x_wsc = int((int64_t(1) << 31) / (kQ * x_chunk_bytes)) > 0
-                          ? int((int64_t(1) << 31) / (kQ * x_chunk_bytes)) : 1;
+    // whose offsets stay below p.x_win (2^31 bytes unless the caller set a
+    // smaller span; offsets from the row's first chunk would pass 2^32 once
+    // seqlen x dim reaches 2^30); a window is rebased when a super-chunk
+    // leaves it, which at most rows never happens
+    const int x_wsc = int(p.x_win / (kQ * x_chunk_bytes)) > 0 ? int(p.x_win / (kQ * x_chunk_bytes)) : 1;
     int x_w0 = sc0;
     rsrc_t Rx_w = make_rsrc_in(p.x, x_off + int64_t(kQ * sc0) * x_chunk_bytes, p.x_end);
     rsrc_t Rx_wt = make_rsrc_in(p.x, x_off + int64_t(kQ * sc0) * x_chunk_bytes, x_tail_end);

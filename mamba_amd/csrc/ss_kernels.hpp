@@ -29,6 +29,9 @@ struct FwdParams {
     // store to an absent optional output (x, y: a forward that no backward
     // follows writes neither)
     int64_t u_end, dl_end, z_end, o_end, y_end, B_end, C_end, x_end;
+    // byte span of x one checkpoint resource of the fast kernels addresses
+    // (at most 2^31, so the offsets inside it stay below 2^31)
+    int64_t x_win;
     // sequence-parallel scan (fast paths): the sequence is cut into nseg
     // equal segments handled by separate workgroups; seg_h (batch, nseg,
     // dim, 16) holds each segment's end state (forward) or adjoint carry

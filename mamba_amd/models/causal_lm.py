@@ -16,6 +16,7 @@ import torch
 import torch.nn as nn
 
 from ..modules import MambaSimple, RMSNorm
+from ..ops import decode_linear as decode_linear_ops
 
 
 @dataclass
@@ -145,7 +146,10 @@ class GraphedStep:
     replays, and returns the captured logits buffer (overwritten by the next
     call).  The cache tensors are the captured ones: keep using the same
     cache object.  Nothing in a step clears memory with a memset, so the
-    graph replays correctly any number of times.
+    graph replays correctly any number of times.  The decode linear layers'
+    split workspace (tile counters and partial tiles) is the graph's own,
+    allocated before the capture, so a replay shares it with no other graph
+    and no eager call; replays of one graph must not overlap each other.
     """
 
     def __init__(self, model, inference_cache, batch_size, warmup=2):
@@ -154,16 +158,16 @@ class GraphedStep:
         saved = [(c.clone(), s.clone()) for c, s in inference_cache]
         # warm-up outside the capture (library handles, allocator pools); it
         # advances the cache, which is put back afterwards
+        self.workspace = decode_linear_ops.new_workspace(dev)
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side), torch.no_grad():
+        with torch.cuda.stream(side), torch.no_grad(), decode_linear_ops.private_workspace(self.workspace):
             for _ in range(warmup):
                 model.step(self.ids, inference_cache)
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        # captured on the warm-up stream: per-stream buffers the kernels use
-        # (the decode linear layer's split workspace) already exist there
-        with torch.cuda.graph(self.graph, stream=side), torch.no_grad():
+        with torch.cuda.graph(self.graph, stream=side), torch.no_grad(), \
+                decode_linear_ops.private_workspace(self.workspace):
             self.logits = model.step(self.ids, inference_cache)
         with torch.no_grad():
             for (c, s), (c0, s0) in zip(inference_cache, saved):

@@ -28,8 +28,13 @@ the first time that stream calls outside a graph capture, and reused by every
 later call on it, captured ones included (the kernel leaves it ready for the
 next call).  A call captured on a stream that has none yet runs without the
 split.  Calls that share a stream run in order, so they never use the
-workspace at the same time.
+workspace at the same time.  Work that may run beside that stream's own
+(a captured graph replayed on another stream) brings its own workspace:
+``private_workspace(ws)`` makes the calls of the current thread inside it
+use ``ws`` (from ``new_workspace``) instead, which is how ``GraphedStep``
+gives every captured step a workspace of its own.
 """
+import contextlib
 import ctypes
 import threading
 
@@ -44,6 +49,24 @@ _MAX_ROWS = 64
 _WS_BYTES = 1 << 20            # covers every split the library picks (at most 63 tiles x 4 slices x 1 KiB + counters)
 _workspaces = {}
 _ws_lock = threading.Lock()
+_private = threading.local()
+
+
+def new_workspace(device):
+    """A zeroed split workspace, for ``private_workspace``."""
+    return torch.zeros(_WS_BYTES, dtype=torch.uint8, device=device)
+
+
+@contextlib.contextmanager
+def private_workspace(ws):
+    """Calls of this thread inside the block use ``ws`` (on its device) as
+    their split workspace instead of the per-stream one."""
+    prev = getattr(_private, "ws", None)
+    _private.ws = ws
+    try:
+        yield ws
+    finally:
+        _private.ws = prev
 
 
 def _fits(x, weight, bias):
@@ -57,7 +80,11 @@ def _fits(x, weight, bias):
 
 def _workspace(device):
     """The split workspace of (device, current stream), or None while a graph
-    is being captured on a stream that has none yet."""
+    is being captured on a stream that has none yet; inside
+    ``private_workspace`` the one given there."""
+    ws = getattr(_private, "ws", None)
+    if ws is not None and ws.device == device:
+        return ws
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
     ws = _workspaces.get(key)

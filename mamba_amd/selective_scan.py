@@ -280,18 +280,26 @@ def workspace_bytes(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplu
     return int(n)
 
 
-def _set_deterministic(lib, b, flag):
+def _set_deterministic(lib, b, flag, workspace="auto"):
     """Sets b.deterministic: the flag, or with None torch.use_deterministic_algorithms.
     An explicit request the kernels cannot honour raises (from the library);
     one that comes from torch's setting raises as torch's own ops do, or
-    warns and runs with atomic sums under warn_only."""
+    warns and runs with atomic sums under warn_only.  The deterministic sums
+    need a workspace: a call made with ``workspace=None`` cannot have them."""
     if flag is not None:
         b.deterministic = int(bool(flag))
         return
     b.deterministic = int(torch.are_deterministic_algorithms_enabled())
-    if b.deterministic and lib.ss_bwd_workspace_bytes(ctypes.byref(b)) < 0:
+    if not b.deterministic:
+        return
+    msg = None
+    if lib.ss_bwd_workspace_bytes(ctypes.byref(b)) < 0:
         msg = ("selective_scan.backward has no deterministic implementation for these arguments: "
                + lib.ss_last_error().decode())
+    elif workspace is None:
+        msg = ("selective_scan.backward: the deterministic sums need a workspace, and this call passes "
+               "workspace=None")
+    if msg is not None:
         if not torch.is_deterministic_algorithms_warn_only_enabled():
             raise RuntimeError(msg)
         import warnings
@@ -318,7 +326,7 @@ def backward_into(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
     lib = nat.load()
     b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                        du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
-    _set_deterministic(lib, b, deterministic)
+    _set_deterministic(lib, b, deterministic, workspace)
     if isinstance(workspace, str):
         _require(workspace == "auto", f"workspace must be 'auto', None or a tensor, got {workspace!r}")
         n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))
@@ -344,7 +352,7 @@ def prepare_backward(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softpl
     lib = nat.load()
     b = _bwd_into_args(u, delta, A, B, C, D, delta_bias, dout, x, use_delta_softplus,
                        du, ddelta, dA, dB, dC, dD, ddelta_bias, z, y, dz)
-    _set_deterministic(lib, b, deterministic)
+    _set_deterministic(lib, b, deterministic, workspace)
     if isinstance(workspace, str):
         _require(workspace == "auto", f"workspace must be 'auto', None or a tensor, got {workspace!r}")
         n = lib.ss_bwd_workspace_bytes(ctypes.byref(b))

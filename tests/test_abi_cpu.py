@@ -60,7 +60,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_version_and_constants(lib, nat):
-    assert lib.ss_abi_version() == nat.ABI_VERSION == 15
+    assert lib.ss_abi_version() == nat.ABI_VERSION == 16
     assert lib.ss_chunk_size() == 16
     assert lib.ss_max_dstate() == 256
     assert lib.ss_last_error() == b""
@@ -156,6 +156,11 @@ def test_valid_blocks_pass(nat, lib):
         assert bwd_rc(lib, valid_bwd(nat, itype=itype))[0] == nat.SS_OK
     assert fwd_rc(lib, valid_fwd(nat, dstate=256))[0] == nat.SS_OK
     assert fwd_rc(lib, valid_fwd(nat, dstate=1))[0] == nat.SS_OK
+    # checkpoint windows: 0 (the default span) up to 2^31 bytes
+    for window in (1, 64 << 10, 1 << 31):
+        a = valid_fwd(nat)
+        a.x_window_bytes = window
+        assert fwd_rc(lib, a)[0] == nat.SS_OK
 
 
 def test_empty_problem_needs_no_pointers(nat, lib):
@@ -182,6 +187,9 @@ FWD_BREAKS = [
     ("misaligned delta", lambda a: setattr(a, "delta", FAKE + 2), "INVALID", "delta is misaligned"),
     ("misaligned A", lambda a: setattr(a, "A", FAKE + 1), "INVALID", "A is misaligned"),
     ("negative stride", lambda a: setattr(a, "B_dstate_stride", -1), "INVALID", "negative stride"),
+    ("negative checkpoint window", lambda a: setattr(a, "x_window_bytes", -1), "INVALID", "x_window_bytes"),
+    ("checkpoint window past 2^31", lambda a: setattr(a, "x_window_bytes", (1 << 31) + 1), "INVALID",
+     "x_window_bytes"),
     ("huge grid", lambda a: (setattr(a, "batch", 1 << 40), setattr(a, "n_chunks", a.n_chunks)), "UNSUPPORTED",
      "too large"),
 ]
@@ -563,8 +571,9 @@ def valid_linear(nat, batch=16, n_out=3072, k_in=768):
 
 @pytest.mark.parametrize("case", ["conv_itype", "conv_batch", "conv_dim", "conv_width", "conv_null_state",
                                   "norm_rows", "norm_dim", "norm_k_in", "norm_dtype", "norm_w_dtype",
-                                  "norm_misaligned", "norm_stride", "norm_neg_eps", "ws_misaligned", "ws_neg",
-                                  "k_in", "null_y"])
+                                  "norm_misaligned", "norm_stride", "norm_neg_eps", "norm_inplace_residual",
+                                  "norm_residual_out_over_x", "norm_y_over_residual", "y_over_x", "ws_misaligned",
+                                  "ws_neg", "k_in", "null_y"])
 def test_decode_linear_rejects(nat, lib, case):
     # every check runs before any device work, so these calls need no GPU
     a = valid_linear(nat)
@@ -605,6 +614,12 @@ def test_decode_linear_rejects(nat, lib, case):
             n.x_row_stride = 772                       # rows not 16-byte aligned
         elif case == "norm_neg_eps":
             n.eps = -1.0
+        elif case == "norm_inplace_residual":
+            n.residual_out = n.residual                # the residual stream updated in place
+        elif case == "norm_residual_out_over_x":
+            n.residual_out = n.x + 16 * 768 * 2 - 16   # the last 16 bytes of x
+        elif case == "norm_y_over_residual":
+            a.y = n.residual + 4096
     elif case == "ws_misaligned":
         a.workspace, a.workspace_bytes = FAKE + 4, 1 << 20
     elif case == "ws_neg":
@@ -613,9 +628,14 @@ def test_decode_linear_rejects(nat, lib, case):
         a.k_in = 24
     elif case == "null_y":
         a.y = None
+    elif case == "y_over_x":
+        a.y = a.x + 768 * 2 * 15                       # y's first row is x's last
     rc = lib.ss_decode_linear(ctypes.byref(a), None)
     assert rc in (nat.SS_ERR_INVALID, nat.SS_ERR_UNSUPPORTED), case
-    assert lib.ss_last_error().decode()
+    err = lib.ss_last_error().decode()
+    assert err
+    if "over" in case or "inplace" in case:
+        assert rc == nat.SS_ERR_INVALID and "overlaps" in err, (case, err)
 
 
 def test_rmsnorm_python_boundary_refuses_cpu_tensors():
@@ -687,3 +707,34 @@ def test_deterministic_workspace_query(nat, lib):
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == -1
     assert "deterministic" in lib.ss_last_error().decode()
     assert lib.ss_bwd_noalloc(ctypes.byref(b), None) == nat.SS_ERR_UNSUPPORTED
+
+
+def test_deterministic_setting_without_workspace(nat, lib):
+    """torch.use_deterministic_algorithms with a call that passes no
+    workspace: raises as torch's own ops do, or under warn_only warns and
+    runs with atomic sums; an explicit flag is passed through untouched (the
+    library refuses it), and a call with a workspace keeps the fixed order."""
+    import warnings
+
+    import torch
+    from mamba_amd import selective_scan as ss
+    was, was_warn = torch.are_deterministic_algorithms_enabled(), torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        b = valid_bwd(nat)
+        with pytest.raises(RuntimeError, match="need a workspace"):
+            ss._set_deterministic(lib, b, None, None)
+        b = valid_bwd(nat)
+        ss._set_deterministic(lib, b, None, "auto")
+        assert b.deterministic == 1
+        torch.use_deterministic_algorithms(True, warn_only=True)
+        b = valid_bwd(nat)
+        with warnings.catch_warnings(record=True) as w:
+            warnings.simplefilter("always")
+            ss._set_deterministic(lib, b, None, None)
+        assert b.deterministic == 0 and any("need a workspace" in str(x.message) for x in w)
+        b = valid_bwd(nat)
+        ss._set_deterministic(lib, b, True, None)
+        assert b.deterministic == 1
+    finally:
+        torch.use_deterministic_algorithms(was, warn_only=was_warn)

@@ -123,3 +123,34 @@ def test_outputs_stay_in_their_arrays(case):
     for k in ("dA", "dB", "dC", "dD", "ddelta_bias"):      # atomic sums: the order may differ
         w = want[k].float()
         assert_close(got[k].float().cpu(), w.cpu(), 1e-5, 1e-5 * max(1.0, float(w.abs().max())), k)
+
+
+def test_ragged_tail_sums_stay_in_their_state_rows():
+    # seqlen 333 (333 % 32 = 13) without workspace: dB / dC rows of seqlen
+    # floats, a partial last chunk (steps 320..332) and a chunk wholly past
+    # the sequence (336..351), whose sums go onto steps of the row.  An
+    # infinite u at the last step makes the state infinite there, so the
+    # identity steps past the sequence produce 0 * inf = NaN partial sums;
+    # they must stay on the row's last step and never reach the first steps
+    # of the next state row.
+    from mamba_amd import selective_scan as ss
+    batch, dim, L = 1, 16, 333
+    _say(f"batch {batch} dim {dim} seqlen {L} float32 workspace None, inf at the last step")
+    x = make_inputs(batch, dim, 16, L, seed=333)
+    x = {k: v.to(DEV) for k, v in x.items()}
+    x["u"][:, :, L - 1] = float("inf")
+    out, y = torch.empty_like(x["u"]), torch.empty_like(x["u"])
+    xck = torch.empty((batch, ss.n_chunks(L), dim, 16), device=DEV)
+    ss.forward_into(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["delta_bias"], True, out, xck,
+                    z=x["z"], y=y, workspace=None)
+    du, dd, dz = torch.empty_like(out), torch.empty_like(out), torch.empty_like(out)
+    dA = torch.empty(x["A"].shape, device=DEV)
+    dB, dC = torch.empty(x["B"].shape, device=DEV), torch.empty(x["C"].shape, device=DEV)
+    dD, db = torch.empty(dim, device=DEV), torch.empty(dim, device=DEV)
+    ss.backward_into(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["delta_bias"], x["dout"], xck, True,
+                     du, dd, dA, dB, dC, dD, db, z=x["z"], y=y, dz=dz, workspace=None, zero_grads=True,
+                     deterministic=False)
+    torch.cuda.synchronize()
+    assert not torch.isfinite(xck[0, -1]).all(), "the state at the end should be infinite"
+    for name, t in (("dB", dB), ("dC", dC)):
+        assert torch.isfinite(t[..., :L - 1]).all(), f"{name}: a non-finite sum landed before the last step"

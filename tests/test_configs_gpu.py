@@ -12,21 +12,24 @@
   kernels run in sequence segments: 128 channel blocks).
 * CausalLM 24 x 768, vocab 50280, bf16, eval (models/causal_lm.py:53-59):
   logits of token ids (16, 2048) on rows 0 and 15 against the float64
-  oracle (causal_lm_ref); on one sequence of 32768 the sequence-segmented
-  scan against the serial scan at full length, and the first 2048
-  positions against the oracle (causality: they depend on no later token).
+  oracle (causal_lm_ref), held to the reference op order's own bf16 error
+  on the same rows (use_fast_path=False everywhere, run on the same GPU);
+  on one sequence of 32768, the first 2048 positions the same way
+  (causality: they depend on no later token) and the sequence-segmented
+  scan against the serial scan at full length, whose difference must stay
+  below that reference-order error.
 
 Tolerances, elementwise |got - want| <= atol + rtol |want|:
 * fp32: rtol 1e-3, atol 1e-3;
-* bf16: rtol 2e-2 with an absolute floor stated per test, plus, for the
-  stacks whose worst element is loose, a bound on the rms of the error.
-  The bf16 paths round every intermediate (projections, conv, delta, the
-  scan's I/O) to bf16 (unit roundoff 2^-9), so the floor follows the scale
-  of the tensor.  Measured on the CPU with the oracle itself run in bf16
-  against float64: block outputs (max |out| 0.18) err <= 1.1e-3; 24-layer
-  logits (rms 28) err rms 0.25 (0.9 % of the logits' rms), max 2.9 (0.10
-  rms).  The rms bound (2 % of the tensor's rms) is the tight one there;
-  the elementwise floor (0.15 rms) only catches gross errors.
+* bf16 block: rtol 2e-2 with an absolute floor stated per test;
+* bf16 gradients and LM logits: rtol 2e-2 plus twice the largest error of
+  the reference op order run in bf16 on the same GPU, and the rms of the
+  error (for the logits also its 50 / 90 / 99 / 99.9 % quantiles) bounded
+  by a small multiple of the reference order's.  The bf16 paths round
+  every intermediate (projections, conv, delta, the scan's I/O) to bf16
+  (unit roundoff 2^-9); through 24 layers the logits (rms 28) carry errors
+  of rms ~0.25 and up to ~3 against float64 either way, so the reference
+  order's own error is the yardstick rather than a fixed floor.
 """
 import math
 import sys
@@ -170,60 +173,120 @@ def _lm_ref(sd, ids):
     return causal_lm_ref(sd, ids, num_layers=24, scan=c_oracle.scan)
 
 
+def _set_fast(lm, fast):
+    """The fast path (fused kernels) or the reference's own op sequence
+    (PyTorch ops around SelectiveScanFn, RMSNorm in PyTorch) in every module."""
+    from mamba_amd.modules import MambaSimple, RMSNorm
+    for mod in lm.modules():
+        if isinstance(mod, (MambaSimple, RMSNorm)):
+            mod.use_fast_path = fast
+
+
+QUANTILES = (0.5, 0.9, 0.99, 0.999)
+
+
+def _quantiles(e):
+    """QUANTILES of the elements of e (all of them: a partial sort)."""
+    import numpy as np
+    a = e.numpy()
+    k = [int(q * (a.size - 1)) for q in QUANTILES]
+    return np.partition(a, k)[k]
+
+
+def _hold_to_reference_order(got, ref, want, what):
+    """The fast path's logits against the float64 oracle, held to the error
+    of the reference op order run in bf16 on the same GPU (the block-gradient
+    test's yardstick): every element within 2e-2 |want| + twice the
+    reference order's largest error; the rms of the error and its 50 %, 90 %,
+    99 % and 99.9 % quantiles each at most 1.1 x the reference order's (a
+    fault that moves a small share of the logits shows in the upper
+    quantiles well before it reaches the elementwise bound).  Measured: the
+    two paths' error statistics agree to within 1 % (the logits' error is
+    mostly the bf16 rounding both paths share at the LM head).  Returns the
+    reference order's error and its quantiles."""
+    got, ref, want = got.double(), ref.double(), want.double()
+    ef, er = (got - want).abs().flatten(), (ref - want).abs().flatten()
+    qf, qr = _quantiles(ef), _quantiles(er)
+    bound = 2e-2 * want.abs().flatten() + 2 * float(er.max())
+    ratio = float((ef / bound).max())
+    _say(f"{what}: logits rms {_rms(want):.3g}; err rms fast {_rms(ef):.3g}, reference order {_rms(er):.3g}; "
+         f"max fast {float(ef.max()):.3g}, reference order {float(er.max()):.3g}; quantiles "
+         + ", ".join(f"{q}: {float(a):.3g}/{float(b):.3g}" for q, a, b in zip(QUANTILES, qf, qr))
+         + f"; worst element / bound {ratio:.3f}")
+    assert ratio <= 1, f"{what}: an element outside 2e-2 |want| + 2 x the reference order's largest error"
+    assert _rms(ef) <= 1.1 * _rms(er), f"{what}: rms of the error above 1.1 x the reference order's"
+    for q, a, b in zip(QUANTILES, qf, qr):
+        assert float(a) <= 1.1 * float(b), f"{what}: {q} quantile of the error above 1.1 x the reference order's"
+    return er, qr
+
+
 @pytest.mark.timeout(900)
 def test_causal_lm_24x768_b16_l2048_bf16_logits_vs_oracle():
-    """Floor: 0.15 x the rms of the reference logits (rms about 28); rms of
-    the error within 2e-2 of the logits' rms."""
+    """Rows 0 and 15 of the fast path's logits against the float64 oracle,
+    held to the reference op order's own bf16 error on the same rows."""
     _say("CausalLM 24 x 768, vocab 50280, (16, 2048) bf16 eval: rows 0 and 15 vs float64 oracle")
     lm = _lm(47)
     ids = torch.randint(0, 50280, (16, 2048), generator=torch.Generator().manual_seed(48))
     with torch.no_grad():
         logits = lm(ids.to(DEV))
         rows = {r: logits[r:r + 1].float().cpu() for r in (0, 15)}
-    del logits
+        del logits
+        _set_fast(lm, False)
+        ref = lm(ids[[0, 15]].to(DEV)).float().cpu()
+        _set_fast(lm, True)
     sd = _sd64(lm)
-    for r, got in rows.items():
+    for i, (r, got) in enumerate(rows.items()):
         want = _lm_ref(sd, ids[r:r + 1])
-        atol = 0.15 * _rms(want)
-        _say(f"row {r}: logits rms {_rms(want):.3g}, err rms {_rms(got.double() - want):.3g}, "
-             f"worst ratio {_worst(got, want, 2e-2, atol):.3f}")
-        assert _rms(got.double() - want) <= 2e-2 * _rms(want), f"logits row {r}: rms of the error"
-        assert_close(got, want, 2e-2, atol, f"logits row {r}")
+        _hold_to_reference_order(got, ref[i:i + 1], want, f"logits row {r}")
 
 
 @pytest.mark.timeout(900)
 def test_causal_lm_24x768_b1_l32768_bf16_segmented_vs_serial_and_oracle(monkeypatch):
     """One sequence of 32768: the scans run in sequence segments (96 channel
-    blocks fill an eighth of the GPU).  Their logits against the serial scan
-    at full length (same elementwise tolerance as against the oracle), and
-    the first 2048 positions against the float64 oracle."""
+    blocks fill an eighth of the GPU).  The first 2048 positions against the
+    float64 oracle (causality: they depend on no later token), held to the
+    reference op order's bf16 error on the same positions.  Every position
+    against the serial scan at full length: their difference (the segment
+    joins' rounding, carried through 24 layers by the occasional bf16
+    rounding flip) must stay well inside that reference-order error: its
+    rms at most half the reference order's, at most 1e-5 of the logits
+    beyond the reference order's 99.9 % quantile and at most 1e-6 of them
+    beyond its largest error.  (A single flip can move a logit by a few
+    units, so the largest difference alone is no yardstick: measured, rms
+    0.05 against 0.24, largest 4 against 2.2, 1.6e-7 of the logits beyond
+    the 99.9 % quantile and 6e-8 beyond the largest error.)"""
     from mamba_amd import selective_scan as ssmod
-    _say("CausalLM 24 x 768, (1, 32768) bf16 eval: segmented vs serial scan, prefix vs oracle")
+    _say("CausalLM 24 x 768, (1, 32768) bf16 eval: prefix vs oracle, segmented vs serial scan")
     lm = _lm(49)
     ids = torch.randint(0, 50280, (1, 32768), generator=torch.Generator().manual_seed(50))
     idg = ids.to(DEV)
     with torch.no_grad():
         seg = lm(idg)
         prefix = seg[:, :2048].float().cpu()
+        _set_fast(lm, False)
+        ref = lm(idg[:, :2048]).float().cpu()
+        _set_fast(lm, True)
+    want = _lm_ref(_sd64(lm), ids[:, :2048])
+    er, qr = _hold_to_reference_order(prefix, ref, want, "logits of the first 2048 positions")
+    q999, emax = float(qr[QUANTILES.index(0.999)]), float(er.max())
+    with torch.no_grad():
         orig = ssmod.forward_into
         monkeypatch.setattr(ssmod, "forward_into", lambda *a, **k: orig(*a, **{**k, "workspace": None}))
         ser = lm(idg)
         monkeypatch.setattr(ssmod, "forward_into", orig)
-        worst, rms_sum, n = 0.0, 0.0, 0
-        for lo in range(0, 32768, 2048):                 # elementwise, 2048 positions at a time
-            a, b = seg[:, lo:lo + 2048].float(), ser[:, lo:lo + 2048].float()
-            rms_sum += float(b.pow(2).sum())
-            n += b.numel()
-        atol = 0.15 * math.sqrt(rms_sum / n)
-        for lo in range(0, 32768, 2048):
-            a, b = seg[:, lo:lo + 2048].float(), ser[:, lo:lo + 2048].float()
-            worst = max(worst, float(((a - b).abs() / (atol + 2e-2 * b.abs())).max()))
-            assert_close(a, b, 2e-2, atol, f"segmented vs serial logits, positions {lo}..{lo + 2047}")
-    _say(f"segmented vs serial: worst ratio {worst:.3f}")
-    del seg, ser
-    want = _lm_ref(_sd64(lm), ids[:, :2048])
-    atol = 0.15 * _rms(want)
-    _say(f"prefix vs oracle: err rms {_rms(prefix.double() - want):.3g} of logits rms {_rms(want):.3g}, "
-         f"worst ratio {_worst(prefix, want, 2e-2, atol):.3f}")
-    assert _rms(prefix.double() - want) <= 2e-2 * _rms(want), "prefix logits: rms of the error"
-    assert_close(prefix, want, 2e-2, atol, "logits of the first 2048 positions")
+        dmax, dsq, n, over_q, over_max = 0.0, 0.0, 0, 0, 0
+        for lo in range(0, 32768, 2048):                 # 2048 positions at a time
+            d = (seg[:, lo:lo + 2048].float() - ser[:, lo:lo + 2048].float()).abs()
+            dmax = max(dmax, float(d.max()))
+            dsq += float(d.double().pow(2).sum())
+            n += d.numel()
+            over_q += int((d > q999).sum())
+            over_max += int((d > emax).sum())
+        del seg, ser
+    drms = math.sqrt(dsq / n)
+    _say(f"segmented vs serial over 32768 positions: rms {drms:.3g}, max {dmax:.3g}; beyond the reference "
+         f"order's 99.9 % quantile ({q999:.3g}): {over_q / n:.2e} of the logits, beyond its largest error "
+         f"({emax:.3g}): {over_max / n:.2e}; reference order rms {_rms(er):.3g}")
+    assert drms <= 0.5 * _rms(er), "segmented vs serial: rms of the difference above half the reference order's"
+    assert over_q <= 1e-5 * n, "segmented vs serial: too many logits beyond the reference order's 99.9 % quantile"
+    assert over_max <= 1e-6 * n, "segmented vs serial: too many logits beyond the reference order's largest error"

@@ -95,8 +95,13 @@ typedef struct ss_fwd_args {
     /* ss_fwd only, optional device scratch of ss_fwd_workspace_bytes() bytes,
        16-byte aligned.  With it, a forward with too few (batch, channel)
        rows to fill the GPU (small batch, long sequence) scans segments of
-       the sequence in parallel and joins them; NULL gives the serial scan.
-       Results agree to rounding.  Calls that overlap must not share it. */
+       the sequence in parallel and joins them, and a dstate of 16 S (32,
+       48, ..., 256; variable B and C) runs the dstate-16 fast kernels once
+       per 16-state slice, carrying y from slice to slice in an fp32
+       accumulator of batch x dim x seqlen floats (ABI v16); NULL (or less
+       than that) gives the serial scan and, for dstate 16 S, the general
+       kernels.  Results agree to rounding.  Calls that overlap must not
+       share it. */
     void* workspace;
     int64_t workspace_bytes;
     /* 0, or at most 2^31: the byte span of x that one buffer resource of the
@@ -130,9 +135,13 @@ typedef struct ss_bwd_args {
        16-byte aligned, contents ignored (the call clears what it uses).  With
        it, the dB / dC sums over channels are spread over several copies and
        added up at the end, instead of every channel block adding into the
-       same dB / dC addresses; NULL gives the same results, more slowly when
-       many channel blocks share a group.  Calls that overlap in time must not
-       share a workspace. */
+       same dB / dC addresses; for a dstate of 16 S (32, 48, ..., 256; variable
+       B and C, not deterministic) it also holds two fp32 accumulators of
+       batch x dim x seqlen floats, with which the backward runs the dstate-16
+       fast kernel once per 16-state slice (ABI v16).  NULL (or less than
+       ss_bwd_workspace_bytes()) gives the same results, more slowly when many
+       channel blocks share a group, and on the general kernels for dstate
+       16 S.  Calls that overlap in time must not share a workspace. */
     void* workspace;
     int64_t workspace_bytes;
     /* nonzero: dA, dB, dC, dD and ddelta_bias are cleared by the call before
@@ -190,10 +199,13 @@ int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a);
 int64_t ss_fwd_workspace_bytes(const ss_fwd_args* a);
 
 /* Base name of the kernel that ss_fwd / ss_bwd would launch for these
-   arguments ("ss_fwd_fast", "ss_fwd_kernel", "ss_bwd_fast", "ss_bwd_kernel"),
-   "" when there is no work, NULL (with ss_last_error set) when the arguments
-   fail the checks.  No device work; for profiling and tests.  No counterpart
-   in the reference, which has one kernel per direction. */
+   arguments, given the workspace that ss_fwd_workspace_bytes /
+   ss_bwd_workspace_bytes ask for ("ss_fwd_fast", "ss_fwd_kernel",
+   "ss_bwd_fast", "ss_bwd_kernel"; for dstate 16 S the fast kernel runs once
+   per 16-state slice), "" when there is no work, NULL (with ss_last_error
+   set) when the arguments fail the checks.  No device work; for profiling
+   and tests.  No counterpart in the reference, which has one kernel per
+   direction. */
 const char* ss_fwd_kernel_name(const ss_fwd_args* a);
 const char* ss_bwd_kernel_name(const ss_bwd_args* a);
 

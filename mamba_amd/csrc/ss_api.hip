@@ -154,8 +154,51 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.C_end = p.var_C && N > 0 ? seq_end(p.C, B, G, L, p.C_bs, p.C_gs, es) + (N - 1) * p.C_ns * int64_t(es) : 0;
     p.x_end = p.x ? B * p.n_chunks * D * N * int64_t(sizeof(float)) : 0;
     p.x_win = a->x_window_bytes > 0 ? a->x_window_bytes : (int64_t(1) << 31);
+    p.xN = N;
+    p.acc = nullptr;
+    p.acc_in_end = p.acc_out_end = 0;
     return p;
 }
+
+// ---- state slices: dstate 16 S on the dstate-16 fast kernels --------------
+// A call with dstate 16 S (S from 2 to 16) runs the fast kernels S times,
+// once per slice of 16 states: A, B, C, x and last_state (and dA, dB, dC)
+// are based at the slice's first state, x and last_state keep the call's
+// dstate as their row length (so every kernel, fast or general, reads and
+// writes the same checkpoints), and the sums over states that the slices
+// share (y forward; sum_n g B and sum_n A g a h backward) accumulate in fp32
+// in the workspace from pass to pass.  The last pass adds D and produces the
+// outputs.
+
+// The forward parameters of slice s.
+ss::FwdParams slice_fwd(const ss::FwdParams& p, int s, size_t es) {
+    ss::FwdParams q = p;
+    const int64_t n0 = int64_t(ss::kT) * s;
+    q.dstate = ss::kT;
+    q.A = p.A + n0 * p.A_ns;
+    q.B = static_cast<const char*>(p.B) + n0 * p.B_ns * int64_t(es);
+    q.C = static_cast<const char*>(p.C) + n0 * p.C_ns * int64_t(es);
+    q.B_end = p.B_end - n0 * p.B_ns * int64_t(es);
+    q.C_end = p.C_end - n0 * p.C_ns * int64_t(es);
+    if (p.x) {
+        q.x = p.x + n0;
+        q.x_end = p.x_end - n0 * int64_t(sizeof(float));
+    }
+    if (p.last_state) q.last_state = p.last_state + n0;
+    return q;
+}
+
+// Slices of the forward for p (1: dstate 16, or the fast kernels do not
+// apply: the call runs as it is).
+int fwd_slices(const ss::FwdParams& p) {
+    if (p.dstate <= ss::kT || p.dstate % ss::kT != 0 || !p.var_B || !p.var_C) return 1;
+    ss::FwdParams q = p;
+    q.dstate = ss::kT;
+    return ss::fwd_fast_ok(q) ? int(p.dstate / ss::kT) : 1;
+}
+
+// Bytes of the forward's y accumulator (batch, dim, seqlen) fp32.
+int64_t fwd_acc_bytes(const ss::FwdParams& p) { return p.batch * p.dim * p.seqlen * int64_t(sizeof(float)); }
 
 int check_fwd(const ss_fwd_args* a, bool* empty) {
     int rc = check_fwd_common(a, empty);
@@ -233,8 +276,23 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     p.dB_n = f.is_var_B ? f.batch * G * f.dstate * f.seqlen : f.dim * f.dstate;
     p.dC_n = f.is_var_C ? f.batch * G * f.dstate * f.seqlen : f.dim * f.dstate;
     p.dD_n = f.dim;
+    p.dA_N = f.dstate;
+    p.bc_N = f.dstate;
     return p;
 }
+
+// Slices of the backward for p (1 as for fwd_slices; not with deterministic
+// sums; the two accumulators below 2^31 bytes, addressed from one base).
+int bwd_slices(const ss::BwdParams& p) {
+    if (p.det || fwd_slices(p.f) <= 1) return 1;
+    ss::BwdParams q = p;
+    q.f.dstate = ss::kT;
+    if (!ss::bwd_fast_ok(q) || p.f.batch * p.f.dim * p.f.seqlen >= (int64_t(1) << 29)) return 1;
+    return int(p.f.dstate / ss::kT);
+}
+
+// Bytes of the backward's two accumulators (sum_n g B, sum_n A g a h).
+int64_t bwd_acc_bytes(const ss::BwdParams& p) { return 2 * fwd_acc_bytes(p.f); }
 
 // Workspace layout for p: slices and bytes (0 when the fast backward does
 // not use one: other kernel, or one slice over 64-byte aligned dB / dC rows).
@@ -335,10 +393,78 @@ int bwd_empty(const ss_bwd_args* a, void* stream) {
 
 // The backward of checked arguments with scratch ws of ws_bytes bytes (NULL:
 // none; the kernels then run without dB / dC slices and sequence segments).
+// The backward as S passes of the dstate-16 fast kernel, one per 16-state
+// slice (see slice_fwd).  Workspace: what one pass needs (dB / dC slices,
+// segment carries), then the two accumulators.  The gradients are cleared
+// once up front (zero_grads); each pass then clears its workspace slices and
+// adds its slice's dA / dB / dC; dD and ddelta_bias, and du / ddelta / dz,
+// come from the last pass, which has the sums over all states.
+int bwd_run_slices(const ss_bwd_args* a, ss::BwdParams p, int S, void* ws, int slices, int nseg,
+                   int64_t slice_bytes, int64_t pass_bytes, hipStream_t st) {
+    const size_t es = elem_size(a->f.itype);
+    const int64_t L = p.f.seqlen;
+    hipError_t e = hipSuccess;
+    if (p.zero_grads) {
+        e = ss::launch_bwd_zero_only(p, st);
+        if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
+    }
+    float* acc = reinterpret_cast<float*>(static_cast<char*>(ws) + pass_bytes);
+    for (int s = 0; s < S; ++s) {
+        ss::BwdParams q = p;
+        const int64_t n0 = int64_t(ss::kT) * s;
+        q.f = slice_fwd(p.f, s, es);
+        q.zero_grads = 0;
+        q.dA = p.dA + n0;
+        // dB / dC rows of this slice: (batch, group) blocks of dstate rows of
+        // seqlen floats, the slice's 16 from row n0
+        q.dB = p.dB + n0 * L;
+        q.dC = p.dC + n0 * L;
+        q.dB_end = p.dB_end - n0 * L * int64_t(sizeof(float));
+        q.dC_end = p.dC_end - n0 * L * int64_t(sizeof(float));
+        if (slice_bytes > 0) {
+            q.ws = static_cast<float*>(ws);
+            q.ws_slices = slices;
+            q.ws_stride = slice_bytes / int64_t(sizeof(float)) / (2 * slices);
+            q.ws_end = slice_bytes;
+            q.bc_ld = ss::bwd_ws_ld(L);
+            q.bc_N = ss::kT;
+        }
+        if (nseg > 1) {
+            q.f.nseg = nseg;
+            q.f.seg_h = reinterpret_cast<float*>(static_cast<char*>(ws) + slice_bytes);
+            q.f.seg_s = q.f.seg_h + q.f.batch * nseg * q.f.dim * 16;
+        }
+        q.f.acc = acc;
+        q.f.acc_in_end = s > 0 ? bwd_acc_bytes(p) : 0;
+        q.f.acc_out_end = s < S - 1 ? bwd_acc_bytes(p) : 0;
+        if (s < S - 1) {           // the per-step outputs, dD and ddelta_bias belong to the last pass
+            q.du_end = q.dd_end = q.dz_end = 0;
+            q.f.y_end = 0;
+            q.dD = nullptr;
+            q.ddelta_bias = nullptr;
+        }
+        e = ss::launch_bwd(q, a->f.itype, st);
+        if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
+    }
+    return ok();
+}
+
 int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
     ss::BwdParams p = make_bwd_params(a);
     int rc = check_det(p);
     if (rc != SS_OK) return rc;
+    if (ws && !aligned(ws, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
+    const int S = bwd_slices(p);
+    if (S > 1) {
+        ss::BwdParams q0 = p;
+        q0.f = slice_fwd(p.f, 0, elem_size(a->f.itype));
+        int slices = 1, nseg = 1;
+        int64_t slice_bytes = 0;
+        const int64_t pass_bytes = ws_bytes_for(q0, &slices, &nseg, &slice_bytes);
+        if (ws && ws_bytes >= pass_bytes + bwd_acc_bytes(p))
+            return bwd_run_slices(a, p, S, ws, slices, nseg, slice_bytes, pass_bytes, static_cast<hipStream_t>(stream));
+        // without that much workspace: the general kernel, as below
+    }
     int slices = 1, nseg = 1;
     int64_t slice_bytes = 0;
     const int64_t need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
@@ -435,16 +561,43 @@ int ss_fwd(const ss_fwd_args* a, void* stream) {
     if (rc != SS_OK) return rc;
     if (empty) return ok();
     ss::FwdParams p = make_fwd_params(a);
-    if (a->workspace) {
-        if (!aligned(a->workspace, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
-        const int nseg = ss::fwd_segments(p);
-        if (nseg > 1 && a->workspace_bytes >= ss::fwd_seg_bytes(p, nseg)) {
-            p.nseg = nseg;
-            p.seg_h = static_cast<float*>(a->workspace);
-            p.seg_s = p.seg_h + p.batch * nseg * p.dim * 16;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (a->workspace && !aligned(a->workspace, 16)) return fail(SS_ERR_INVALID, "workspace is misaligned");
+    const int slices = fwd_slices(p);
+    const size_t es = elem_size(a->itype);
+    // the sequence segments of each pass (the same for every slice), then,
+    // for state slices, the y accumulator
+    const ss::FwdParams q0 = slices > 1 ? slice_fwd(p, 0, es) : p;
+    const int nseg = ss::fwd_segments(q0);
+    const int64_t seg_bytes = nseg > 1 ? ss::fwd_seg_bytes(q0, nseg) : 0;
+    const int64_t have = a->workspace ? a->workspace_bytes : 0;
+    auto attach_segs = [&](ss::FwdParams& q) {
+        if (nseg > 1 && have >= seg_bytes) {
+            q.nseg = nseg;
+            q.seg_h = static_cast<float*>(a->workspace);
+            q.seg_s = q.seg_h + q.batch * nseg * q.dim * 16;
         }
+    };
+    if (slices > 1 && have >= seg_bytes + fwd_acc_bytes(p)) {
+        float* acc = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + seg_bytes);
+        for (int s = 0; s < slices; ++s) {
+            ss::FwdParams q = slice_fwd(p, s, es);
+            attach_segs(q);
+            q.acc = acc;
+            q.acc_in_end = s > 0 ? fwd_acc_bytes(p) : 0;
+            q.acc_out_end = s < slices - 1 ? fwd_acc_bytes(p) : 0;
+            if (s < slices - 1) {      // out, y and D belong to the last pass
+                q.D = nullptr;
+                q.o_end = 0;
+                q.y_end = 0;
+            }
+            hipError_t e = ss::launch_fwd(q, a->itype, st);
+            if (e != hipSuccess) return fail(SS_ERR_HIP, "forward launch failed: %s", hipGetErrorString(e));
+        }
+        return ok();
     }
-    hipError_t e = ss::launch_fwd(p, a->itype, static_cast<hipStream_t>(stream));
+    if (slices <= 1) attach_segs(p);
+    hipError_t e = ss::launch_fwd(p, a->itype, st);
     if (e != hipSuccess) return fail(SS_ERR_HIP, "forward launch failed: %s", hipGetErrorString(e));
     return ok();
 }
@@ -455,7 +608,10 @@ int64_t ss_fwd_workspace_bytes(const ss_fwd_args* a) {
     ok();
     if (empty) return 0;
     const ss::FwdParams p = make_fwd_params(a);
-    return ss::fwd_seg_bytes(p, ss::fwd_segments(p));
+    const int slices = fwd_slices(p);
+    const ss::FwdParams q0 = slices > 1 ? slice_fwd(p, 0, elem_size(a->itype)) : p;
+    const int nseg = ss::fwd_segments(q0);
+    return (nseg > 1 ? ss::fwd_seg_bytes(q0, nseg) : 0) + (slices > 1 ? fwd_acc_bytes(p) : 0);
 }
 
 int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a) {
@@ -467,6 +623,11 @@ int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a) {
     ok();
     int slices = 1, nseg = 1;
     int64_t slice_bytes = 0;
+    if (bwd_slices(p) > 1) {
+        ss::BwdParams q0 = p;
+        q0.f = slice_fwd(p.f, 0, elem_size(a->f.itype));
+        return ws_bytes_for(q0, &slices, &nseg, &slice_bytes) + bwd_acc_bytes(p);
+    }
     return ws_bytes_for(p, &slices, &nseg, &slice_bytes);
 }
 
@@ -474,14 +635,18 @@ const char* ss_fwd_kernel_name(const ss_fwd_args* a) {
     bool empty = false;
     if (check_fwd(a, &empty) != SS_OK) return nullptr;
     ok();
-    return empty ? "" : ss::fwd_kernel_name(make_fwd_params(a));
+    if (empty) return "";
+    const ss::FwdParams p = make_fwd_params(a);
+    return fwd_slices(p) > 1 ? "ss_fwd_fast" : ss::fwd_kernel_name(p);
 }
 
 const char* ss_bwd_kernel_name(const ss_bwd_args* a) {
     bool empty = false;
     if (check_bwd(a, &empty) != SS_OK) return nullptr;
     ok();
-    return empty ? "" : ss::bwd_kernel_name(make_bwd_params(a));
+    if (empty) return "";
+    const ss::BwdParams p = make_bwd_params(a);
+    return bwd_slices(p) > 1 ? "ss_bwd_fast" : ss::bwd_kernel_name(p);
 }
 
 int ss_bwd(const ss_bwd_args* a, void* stream) {

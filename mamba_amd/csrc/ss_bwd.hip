@@ -398,7 +398,12 @@ __device__ __forceinline__ int wg_slot(int t, int n) { return t * 16 + (n ^ t); 
 
 // kDet: deterministic sums (plain stores of the partials, summed in a fixed
 // order afterwards) instead of atomic adds.
-template <typename IT, bool kZ, bool kDet>
+// kAcc: one pass of a state-sliced backward (dstate 16 S, one pass per
+// 16-state slice): the sums over states of each step (sum_n g B, sum_n A g a h)
+// are added to those of the earlier slices (p.acc, fp32) and, but in the last
+// pass, stored back there; the per-step outputs computed from them are only
+// kept in the last pass (the host sets the other passes' extents to 0).
+template <typename IT, bool kZ, bool kDet, bool kAcc>
 // 3 workgroups per CU (12 waves): at most 168 VGPRs and 54,613 B of LDS.
 __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kT];              // [buf][B, C][n][t]
@@ -450,11 +455,15 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // (rows of ld floats)
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
     const int64_t ld = q.bc_ld;
-    const int64_t bc_off = (b * G + g) * int64_t(kT) * ld * 4;
-    const rsrc_t RdB = q.ws ? make_rsrc_in(q.ws, 2 * slice * q.ws_stride * 4 + bc_off, q.ws_end)
-                            : make_rsrc_in(q.dB, bc_off, q.dB_end);
-    const rsrc_t RdC = q.ws ? make_rsrc_in(q.ws, (2 * slice + 1) * q.ws_stride * 4 + bc_off, q.ws_end)
-                            : make_rsrc_in(q.dC, bc_off, q.dC_end);
+    const int64_t bc_off = (b * G + g) * (kAcc ? q.bc_N : int64_t(kT)) * ld * 4;
+    // (keep = false: a resource of zero bytes at the same place, through which
+    // every add is dropped)
+    auto bc_rsrc = [&](int which, bool keep) {
+        return q.ws ? make_rsrc_in(q.ws, (2 * slice + which) * q.ws_stride * 4 + bc_off, keep ? q.ws_end : 0)
+                    : make_rsrc_in(which ? q.dC : q.dB, bc_off, keep ? (which ? q.dC_end : q.dB_end) : 0);
+    };
+    const rsrc_t RdB = bc_rsrc(0, true);
+    const rsrc_t RdC = bc_rsrc(1, true);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + r) * es, od = uint32_t(row * p.dl_ds + r) * es;
     const uint32_t oo = uint32_t(row * q.do_ds + r) * es;
@@ -462,7 +471,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const uint32_t oB = uint32_t(row * p.B_ns + r) * es, oC = uint32_t(row * p.C_ns + r) * es;
     const uint32_t odu = uint32_t(row * q.du_ds + r) * es, odd = uint32_t(row * q.dd_ds + r) * es;
     const uint32_t odz = uint32_t(row * q.dz_ds + r) * es;
-    const uint32_t ox = uint32_t(row * kT + r) * 4u;
+    // x: (batch, chunk, dim, xN), 16 unless the call is state-sliced
+    const int64_t xN = kAcc ? p.xN : kT;
+    const uint32_t ox = uint32_t(row * xN + r) * 4u;
     // x: (batch, chunk, dim, dstate); the checkpoint of this lane's chain,
     // through a resource based at a window of chunks whose offsets stay below
     // p.x_win (2^31 bytes unless the caller set a smaller span; offsets from
@@ -470,8 +481,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     // seqlen x dim reaches 2^30); the chunks run last to first, and a window
     // is rebased (to end at the chunk) when a chunk leaves it, which at most
     // rows never happens
-    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
-    const int64_t x_chunk_bytes = p.dim * kT * 4;
+    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * xN * 4;
+    const int64_t x_chunk_bytes = p.dim * xN * 4;
     const int x_wck = int(p.x_win / x_chunk_bytes) > 0 ? int(p.x_win / x_chunk_bytes) : 1;
     int x_w0 = k1 - x_wck > 0 ? k1 - x_wck : 0;
     rsrc_t Rx = make_rsrc_in(p.x, x_off + int64_t(x_w0) * x_chunk_bytes, p.x_end);
@@ -502,6 +513,18 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     float Aw[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) Aw[i] = p.A[c * p.A_ds + (2 * i + tnh) * p.A_ns];
+
+    // state slices (kAcc): the earlier slices' sums over states of this row's
+    // steps, fp32 (batch, dim, seqlen), sum_n g B at p.acc and sum_n A g a h
+    // a further batch x dim x seqlen floats on (below 2^31 bytes, checked by
+    // the host); read at the start of the step's chunk (a chunk's work
+    // covers their latency), stored back (but in the last pass) with its
+    // outputs
+    const int64_t acc_off = (b * p.dim + c0) * L * 4;
+    const uint32_t acc2 = uint32_t(p.batch * p.dim * L * 4);
+    const uint32_t oacc = uint32_t(row * L + r) * 4u;
+    const rsrc_t Rai = kAcc ? make_rsrc_in(p.acc, acc_off, p.acc_in_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t Rao = kAcc ? make_rsrc_in(p.acc, acc_off, p.acc_out_end) : make_rsrc_n(nullptr, 0);
 
     struct Chunk { float u, d, o, z, y, B, C, x; };
     auto fetch = [&](int ck, Chunk& P) {     // 0 <= ck < nck
@@ -564,33 +587,31 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     };
     // (TAIL: the workspace's padded rows have slots for the steps past the
     // sequence.  In rows of seqlen floats, which only a call without
-    // workspace uses for a ragged seqlen, their sums (zero, unless the state
-    // is not finite) go to steps inside it, so no address leaves the row: a
-    // chunk wholly past the sequence adds them onto the previous chunk's 16
-    // steps, clamped to the last step (onto one address for every lane, all
-    // workgroups' adds of the chunk were serialised in the atomic unit:
-    // seqlen 2064 fp32 took 570 us against 338 us at 2048), a partial chunk
-    // onto the last step.)
+    // workspace uses for a ragged seqlen, a partial chunk adds the sums of
+    // its steps past the sequence onto the last step, so no address leaves
+    // the row, and a chunk wholly past the sequence adds nothing (its adds go
+    // through a resource of zero bytes).  Those sums are zero unless the
+    // state is not finite (0 * inf past the end: the last step's own sum is
+    // then not finite either), so no other step of dB / dC sees them.)
     auto flush_commit = [&](int ck, const float (&v)[2 * kWaves], auto TAIL) {
         const float sB = (v[0] + v[1]) + (v[2] + v[3]);
         const float sC = (v[4] + v[5]) + (v[6] + v[7]);
         uint32_t so = uint32_t(ck * kT) * 4u;
         uint32_t ofl = ofl0;
-        if constexpr (decltype(TAIL)::value) {
-            if (ck * kT >= ld) {
-                so = uint32_t((ck - 1) * kT) * 4u;
-                if ((ck - 1) * kT + ft >= L) ofl = uint32_t(fn * ld + int(L) - 1 - (ck - 1) * kT) * 4u;
-            } else {
-                const int t = ck * kT + ft;
-                if (t >= ld) ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
-            }
+        constexpr bool kTailc = decltype(TAIL)::value;
+        const bool keep = !kTailc || ck * kT < ld;
+        if constexpr (kTailc) {
+            const int t = ck * kT + ft;
+            if (t >= ld) ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
         }
+        const rsrc_t RB_ = kTailc ? bc_rsrc(0, keep) : RdB;
+        const rsrc_t RC_ = kTailc ? bc_rsrc(1, keep) : RdC;
         if constexpr (kDet) {
-            bstore<float>(RdB, ofl, so, sB);
-            bstore<float>(RdC, ofl, so, sC);
+            bstore<float>(RB_, ofl, so, sB);
+            bstore<float>(RC_, ofl, so, sC);
         } else {
-            batomic_add(RdB, ofl, so, sB);
-            batomic_add(RdC, ofl, so, sC);
+            batomic_add(RB_, ofl, so, sB);
+            batomic_add(RC_, ofl, so, sC);
         }
     };
     auto flush = [&](int ck, int buf) {
@@ -623,6 +644,18 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         lds_barrier();   // B / C tile of ck staged; dB / dC partials of ck + 1 complete
         const Chunk cur = cur_in;
         fetch(ck > k0 + 1 ? ck - 2 : k0, cur_in);
+        // the earlier slices' sums of this chunk's steps (state slices; the
+        // steps past the sequence, in the tail, read 0 through a clamped step)
+        float acc1 = 0.f, acc2v = 0.f;
+        if constexpr (kAcc) {
+            const int t = ck * kT + r;
+            const bool tin = !kTail || t < L;
+            const uint32_t oa = kTail ? uint32_t(row * L + (tin ? t : int(L) - 1)) * 4u : oacc;
+            const uint32_t sa = kTail ? 0u : uint32_t(ck * kT) * 4u;
+            const float v1 = bload<float>(Rai, oa, sa), v2 = bload<float>(Rai, oa, sa + acc2);
+            acc1 = tin ? v1 : 0.f;
+            acc2v = tin ? v2 : 0.f;
+        }
 
         // B / C of this lane's state for the 16 steps of the chunk
         float Bq[kT], Cq[kT];
@@ -683,20 +716,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                 float hprev;
                 if constexpr (k == 0) hprev = h0;
                 else hprev = hs[k - 1];
-                float gah = ga * hprev;              // g_t a_t h_{t-1}
-                // past the sequence (tail chunks): the state carried through the
-                // identity steps meets zero adjoints and inputs; those products
-                // are zero unless the state is not finite (0 * inf), and are
-                // dropped, so that no such NaN reaches dA or the dB / dC sums
-                // (whose past-the-end lanes go onto steps of the row)
-                const bool past = kTail && ck * kT + k >= L;
-                if constexpr (kTail) gah = past ? 0.f : gah;
+                const float gah = ga * hprev;        // g_t a_t h_{t-1}
                 bfmac<k>(dA_acc, dt, gah);
                 s2p[ki] = gah;                       // times A_n in the sum over states
                 s1p[ki] = gv * Bq[k];
                 dBp[ki] = bmul<k>(dtu, gv);
                 dCp[ki] = bmul<k>(dy, hs[k]);
-                if constexpr (kTail) dCp[ki] = past ? 0.f : dCp[ki];
             });
             // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
             float* trh = trw;
@@ -741,15 +766,23 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         float t1a, t2a, t1b, t2b;
         half_sum(tv1, t1a, t2a);
         half_sum(tv0, t1b, t2b);
-        const float s1r = tnh ? t1a : t1b;
-        const float s2r = tnh ? t2a : t2b;
+        float s1r = tnh ? t1a : t1b;
+        float s2r = tnh ? t2a : t2b;
+        const bool in = !kTail || ck * kT + r < L;
+        if constexpr (kAcc) {
+            s1r += acc1;
+            s2r += acc2v;
+            if (in) {
+                bstore<float>(Rao, oacc, uint32_t(ck * kT) * 4u, s1r);
+                bstore<float>(Rao, oacc, uint32_t(ck * kT) * 4u + acc2, s2r);
+            }
+        }
 
         // ---- per-step outputs of step 16 ck + r
         const float du = Dv * dy + dt * s1r;
         const float ddt = uu * s1r + s2r;
         const float dd = softplus ? ddt * sigmoidf_(pre) : ddt;
         const uint32_t so = uint32_t(ck * kT) * es;
-        const bool in = !kTail || ck * kT + r < L;
         if (in) {
             bstore<IT>(Rdu, odu, so, du);
             bstore<IT>(Rdd, odd, so, dd);
@@ -801,7 +834,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             if (q.dD) atomicAdd(q.dD + c, dD_acc);
             if (q.ddelta_bias) atomicAdd(q.ddelta_bias + c, db_acc);
         }
-        atomicAdd(q.dA + c * kT + r, dA_acc);
+        atomicAdd(q.dA + c * (kAcc ? q.dA_N : int64_t(kT)) + r, dA_acc);
     }
 }
 
@@ -951,7 +984,7 @@ bool bwd_fast_ok(const BwdParams& q) {
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && (!p.has_z || p.y != nullptr) &&
            small_strides({p.seqlen + 2 * kT, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
                           q.do_ds, q.du_ds, q.dd_ds, q.dz_ds}) &&
-           p.dim < (int64_t(1) << 24);
+           p.dim * p.xN < (int64_t(1) << 28);
 }
 
 // ------------------------------------------------------- dB / dC slices --
@@ -1007,15 +1040,19 @@ __global__ __launch_bounds__(256) void ss_ws_reduce(const float4* __restrict__ w
 }
 
 // As ss_ws_reduce for slices whose rows are padded to ld floats (or dB / dC
-// not 16-byte aligned): element t < seqlen of row i of dB / dC is the sum of
-// the slices' element i * ld + t, in slice order, then added to what dB / dC
-// held unless overwrite.  A workgroup per row.
+// not 16-byte aligned): element t < seqlen of row i of the slices (16 state
+// rows per batch row and group) is the sum of the slices' element i * ld + t,
+// in slice order, then added to what dB / dC held unless overwrite, at row
+// (i / 16) * N + i % 16 of dB / dC (N state rows per batch row and group; a
+// pass of a state-sliced backward passes dB / dC based at its slice's first
+// state).  A workgroup per row.
 __global__ __launch_bounds__(256) void ss_ws_reduce_rows(const float* __restrict__ ws, int slices, int64_t stride,
                                                          int64_t rows, int64_t L, int64_t ld, float* __restrict__ dB,
-                                                         float* __restrict__ dC, int overwrite) {
+                                                         float* __restrict__ dC, int overwrite, int64_t N) {
     for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const int64_t orow = (row / kT) * N + row % kT;
         for (int64_t t = threadIdx.x; t < L; t += blockDim.x) {
-            const int64_t w = row * ld + t, o = row * L + t;
+            const int64_t w = row * ld + t, o = orow * L + t;
             float sb = ws[w], sc = ws[stride + w];
             for (int k = 1; k < slices; ++k) {
                 sb += ws[2 * k * stride + w];
@@ -1091,7 +1128,7 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     if (fast) {
         // the slice sum as whole float4 rows: rows of seqlen floats, 16-byte
         // aligned dB / dC
-        const bool flat = p.bc_ld == p.f.seqlen && (reinterpret_cast<uintptr_t>(p.dB) & 15) == 0 &&
+        const bool flat = p.bc_ld == p.f.seqlen && p.f.xN == kT && (reinterpret_cast<uintptr_t>(p.dB) & 15) == 0 &&
                           (reinterpret_cast<uintptr_t>(p.dC) & 15) == 0;
         const int64_t n4 = sliced && flat ? p.ws_stride / 4 : 0;
         const unsigned rgrid = unsigned(n4 > 0 ? (n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048 : 1);
@@ -1103,11 +1140,14 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
         }
         const dim3 sgrid(unsigned(nblk * p.f.batch * nseg));
         if (p.det) {
-            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, true>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, true>), sgrid, block, 0, stream, p);
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, true, false>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, true, false>), sgrid, block, 0, stream, p);
+        } else if (p.f.acc) {
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false, true>), sgrid, block, 0, stream, p);
         } else {
-            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false>), sgrid, block, 0, stream, p);
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false, false>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false, false>), sgrid, block, 0, stream, p);
         }
         if (p.det) {
             const int64_t n = p.f.dim * (kT + 2);
@@ -1124,7 +1164,7 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
             const int64_t rows = p.f.batch * (p.f.dim / p.f.dpg) * kT;
             hipLaunchKernelGGL(ss_ws_reduce_rows, dim3(unsigned(rows < 2048 ? rows : 2048)), dim3(256), 0, stream,
                                p.ws, int(p.ws_slices), p.ws_stride, rows, p.f.seqlen, p.bc_ld, p.dB, p.dC,
-                               int(p.zero_grads));
+                               int(p.zero_grads), p.f.xN);
         }
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_bwd_kernel<IT, 1, true>), grid, block, 0, stream, p);

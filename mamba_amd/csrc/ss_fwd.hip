@@ -243,7 +243,11 @@ __device__ __forceinline__ int bc64_slot(int n, int gi) { return n * kSC + 4 * (
 // reading steps 16q..16q+15 with ds_read_b128 cover all 64 banks once.
 __device__ __forceinline__ int ct_slot4(int t, int i) { return t * 16 + 4 * (i ^ ((t >> 2) & 3)); }
 
-template <typename IT, bool kZ>
+// kAcc: one pass of a state-sliced scan (dstate 16 S, one pass per 16-state
+// slice): y is added to the sums over the earlier slices (p.acc, fp32) and,
+// but in the last pass, stored back there instead of becoming out / y (whose
+// extents the host sets to 0 then; D is applied in the last pass only).
+template <typename IT, bool kZ, bool kAcc>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B [n][64 steps], C [64 steps][n]]
     __shared__ __attribute__((aligned(16))) float s_yp[kWaves * kRows * kYRow];    // [wave][row][n][16 steps]
@@ -288,18 +292,20 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     // forward that no backward follows writes neither.
     const int64_t o_off = (b * p.o_bs + c0 * p.o_ds) * es64, y_off = (b * p.y_bs + c0 * p.y_ds) * es64;
     const int64_t y_end = kZ ? p.y_end : 0;
-    // x: (batch, chunk, dim, dstate)
-    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * kT * 4;
+    // x: (batch, chunk, dim, xN), this pass's 16 states at p.x (xN is 16
+    // unless the call is state-sliced)
+    const int64_t xN = kAcc ? p.xN : kT;
+    const int64_t x_off = (b * p.n_chunks * p.dim + c0) * xN * 4;
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
     const uint32_t oz = uint32_t(row * p.z_ds + 4 * r) * es;
     const uint32_t oB = uint32_t(row * p.B_ns + 4 * r) * es, oC = uint32_t(row * p.C_ns + 4 * r) * es;
     const uint32_t oo = uint32_t(row * p.o_ds + 4 * r) * es, oy = uint32_t(row * p.y_ds + 4 * r) * es;
-    const uint32_t ox = uint32_t(row * kT + r) * 4u;
-    const int64_t x_chunk_bytes = p.dim * kT * 4;          // below 2^30 (dim below 2^24)
+    const uint32_t ox = uint32_t(row * xN + r) * 4u;
+    const int64_t x_chunk_bytes = p.dim * xN * 4;          // below 2^34 (dim below 2^24, xN at most 256)
     // the tail's checkpoints: a resource that ends with this batch row's
     // n_chunks chunks, so the stores of chunks past the sequence are dropped
-    const int64_t x_row_end = (b + 1) * p.n_chunks * p.dim * kT * 4;
+    const int64_t x_row_end = ((b + 1) * p.n_chunks * p.dim * xN - (xN - kT)) * 4;
     const int64_t x_tail_end = p.x_end < x_row_end ? p.x_end : x_row_end;
     // the checkpoints through resources based at a window of super-chunks
     // whose offsets stay below p.x_win (2^31 bytes unless the caller set a
@@ -376,9 +382,29 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     }
     float4 pu = make_float4(0.f, 0.f, 0.f, 0.f), pz = pu;   // u, z of the previous super-chunk
 
-    // out / y of super-chunk sc (its 64 sums are in yo)
-    auto finish_super = [&](int sc) {
+    // state slices (kAcc): this row's sums over the earlier slices, fp32
+    // (batch, dim, seqlen) at p.acc; lane r's steps 4r..4r+3 of a super-chunk
+    // are loaded right after the previous super-chunk's outputs, a
+    // super-chunk ahead of their own
+    const int64_t acc_off = (b * p.dim + c0) * p.seqlen * 4;
+    const uint32_t oacc = uint32_t(row * p.seqlen + 4 * r) * 4u;
+    float4 pacc = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto acc_load = [&](int sc) {
+        if constexpr (kAcc)
+            pacc = bload4<float>(make_rsrc_in(p.acc, acc_off, p.acc_in_end), oacc, uint32_t(sc * kSC) * 4u);
+    };
+
+    // out / y of super-chunk sc (its 64 sums are in yo); `real` false: the
+    // placeholder call of a segment's first super-chunk, whose out / y stores
+    // the real call rewrites later and whose accumulator store is dropped (a
+    // middle pass reads the accumulator in place, right after this call)
+    auto finish_super = [&](int sc, bool real) {
         float4 y = *reinterpret_cast<const float4*>(yo + 4 * r);
+        if constexpr (kAcc) {
+            y.x += pacc.x; y.y += pacc.y; y.z += pacc.z; y.w += pacc.w;
+            bstore4<float, kStoreNT>(
+                make_rsrc_in(p.acc, acc_off + int64_t(sc) * kSC * 4, real ? p.acc_out_end : 0), oacc, y);
+        }
         y.x = __builtin_fmaf(Dv, pu.x, y.x);
         y.y = __builtin_fmaf(Dv, pu.y, y.y);
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
@@ -395,6 +421,14 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     // as finish_super for the tail super-chunk: element stores of its lt steps
     auto finish_super_tail = [&](int sc) {
         float4 y = *reinterpret_cast<const float4*>(yo + 4 * r);
+        if constexpr (kAcc) {
+            y.x += pacc.x; y.y += pacc.y; y.z += pacc.z; y.w += pacc.w;
+            const rsrc_t Ra = make_rsrc_in(p.acc, acc_off + int64_t(sc) * kSC * 4, p.acc_out_end);
+            const float av[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * r + i < lt) bstore<float, kStoreNT>(Ra, oacc + uint32_t(i) * 4u, 0, av[i]);
+        }
         y.x = __builtin_fmaf(Dv, pu.x, y.x);
         y.y = __builtin_fmaf(Dv, pu.y, y.y);
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
@@ -494,9 +528,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             yo[((q + kQ - 1) % kQ) * kT + r] = dot16(ys, cT);
             if constexpr (q == 0) {
                 if constexpr (kTail) {
-                    if (sc > sc0) finish_super(sc - 1);
+                    if (sc > sc0) finish_super(sc - 1, true);
+                    acc_load(sc);
                 } else {
-                    finish_super(sc > sc0 ? sc - 1 : sc0);   // (at sc0 a placeholder, rewritten later)
+                    finish_super(sc > sc0 ? sc - 1 : sc0, sc > sc0);   // (at sc0 a placeholder, rewritten later)
+                    acc_load(sc);
                 }
                 pu = cu;     // this super-chunk's u, z wait for its outputs
                 pz = cz;
@@ -539,9 +575,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         read_tile(ys);
         yo[(kQ - 1) * kT + r] = dot16(ys, cT);
         if (tail) finish_super_tail(sc1 - 1);
-        else finish_super(sc1 - 1);
+        else finish_super(sc1 - 1, true);
     }
-    if (p.last_state && seg == nseg - 1) p.last_state[(b * p.dim + c) * kT + r] = h;
+    if (p.last_state && seg == nseg - 1) p.last_state[(b * p.dim + c) * xN + r] = h;
 }
 
 // Pass A of the sequence-parallel forward: workgroup (b, seg, 16 channels)
@@ -653,12 +689,12 @@ int fwd_segments(const FwdParams& p) {
 bool fwd_fast_ok(const FwdParams& p) {
     // every byte offset the kernel forms stays below 2^32: rows and seqlen
     // below 2^26 elements, checkpoints addressed from each super-chunk's
-    // first chunk (dim below 2^24)
+    // first chunk (dim x the checkpoints' states per channel below 2^28)
     // (a seqlen that is not a multiple of 64 ends in a partial super-chunk)
     return p.dstate == 16 && p.var_B && p.var_C && p.seqlen >= 1 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 &&
            small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns}) &&
-           p.dim < (int64_t(1) << 24);
+           p.dim * p.xN < (int64_t(1) << 28);
 }
 
 template <typename IT>
@@ -677,8 +713,13 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
             if (e != hipSuccess) return e;
         }
         const dim3 sgrid(unsigned(nblk * p.batch * nseg));
-        if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true>), sgrid, block, 0, stream, p);
-        else hipLaunchKernelGGL((ss_fwd_fast<IT, false>), sgrid, block, 0, stream, p);
+        if (p.acc) {
+            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, true>), sgrid, block, 0, stream, p);
+        } else {
+            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, false>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, false>), sgrid, block, 0, stream, p);
+        }
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, false>), grid, block, 0, stream, p);

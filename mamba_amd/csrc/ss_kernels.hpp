@@ -32,6 +32,17 @@ struct FwdParams {
     // byte span of x one checkpoint resource of the fast kernels addresses
     // (at most 2^31, so the offsets inside it stay below 2^31)
     int64_t x_win;
+    // states per channel of x and last_state (the call's dstate): the fast
+    // kernels scan 16 states; for dstate 16 S they run once per 16-state
+    // slice, with x, last_state, A, B and C based at the slice
+    int64_t xN;
+    // state slices (fast kernels, S > 1): the sums over states that the
+    // slices share, accumulated in fp32 from pass to pass.  Forward: y
+    // (batch, dim, seqlen); backward: sum_n g B, then sum_n A g a h (two such
+    // arrays).  The extents are 0 where a pass does not read (the first) or
+    // write (the last) them.
+    float* acc;
+    int64_t acc_in_end, acc_out_end;
     // sequence-parallel scan (fast paths): the sequence is cut into nseg
     // equal segments handled by separate workgroups; seg_h (batch, nseg,
     // dim, 16) holds each segment's end state (forward) or adjoint carry
@@ -43,6 +54,8 @@ struct FwdParams {
 };
 // segments the forward uses for p (1: serial), and the workspace they need
 int fwd_segments(const FwdParams& p);
+// the fast forward applies to p
+bool fwd_fast_ok(const FwdParams& p);
 inline int64_t fwd_seg_bytes(const FwdParams& p, int nseg) {
     return nseg > 1 ? p.batch * nseg * p.dim * 17 * int64_t(sizeof(float)) : 0;
 }
@@ -81,7 +94,14 @@ struct BwdParams {
     // passes sum both, so the results are the same bits on every run
     int32_t det;
     float* det_par;
+    // state slices: row length of dA (the call's dstate) and state rows per
+    // (batch, group) of the dB / dC rows the fast kernel adds into (dstate for
+    // dB / dC themselves, 16 in the workspace's slices)
+    int64_t dA_N, bc_N;
 };
+// state slices the fast kernels run in for p (dstate 16 S: S; 1 where they
+// do not apply or dstate is 16)
+int state_slices(const FwdParams& p);
 
 // dB / dC slices the fast backward uses for p (1: add into dB / dC directly;
 // with p.det one per channel block of a group)

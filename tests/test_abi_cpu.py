@@ -377,8 +377,19 @@ def test_kernel_name_query(nat, lib):
     assert fname(valid_fwd(nat, seqlen=7)) == "ss_fwd_fast"
     assert bname(valid_bwd(nat, seqlen=100)) == "ss_bwd_fast"
     assert bname(valid_bwd(nat, seqlen=1)) == "ss_bwd_fast"
-    # another dstate, or constant B / C, takes the general kernels
-    assert fname(valid_fwd(nat, seqlen=128, dstate=32)) == "ss_fwd_kernel"
+    # dstate 16 S (32, 64, ..., 256): the fast kernels once per 16-state slice
+    # (with the workspace ss_*_workspace_bytes asks for); other dstates, or
+    # constant B / C, take the general kernels
+    for n in (32, 48, 64, 256):
+        assert fname(valid_fwd(nat, seqlen=128, dstate=n)) == "ss_fwd_fast"
+        assert bname(valid_bwd(nat, seqlen=128, dstate=n)) == "ss_bwd_fast"
+    for n in (8, 24, 200):
+        assert fname(valid_fwd(nat, seqlen=128, dstate=n)) == "ss_fwd_kernel"
+        assert bname(valid_bwd(nat, seqlen=128, dstate=n)) == "ss_bwd_kernel"
+    a = valid_fwd(nat, seqlen=128, dstate=32)
+    a.is_var_B = 0
+    a.B_batch_stride, a.B_group_stride, a.B_dstate_stride = 0, 32, 1
+    assert fname(a) == "ss_fwd_kernel"
     # no work, and invalid arguments
     assert fname(valid_fwd(nat, batch=0)) == ""
     bad = valid_fwd(nat)
@@ -395,8 +406,16 @@ def test_workspace_query(nat, lib):
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, batch=2, dim=1536, seqlen=128))) == 0
     b = valid_bwd(nat, batch=2, dim=3072, seqlen=128)
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == 2 * 2 * (2 * 16 * 128) * 4
-    # the general kernel (dstate 32) uses none; invalid arguments give -1
-    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, dim=1536, seqlen=100, dstate=32))) == 0
+    # dstate 32: two passes of the fast kernel, each with the one padded dB / dC
+    # slice of a ragged seqlen (2 x (2 x 16 x 128) floats), then the two fp32
+    # accumulators of the sums over states (2 x batch x dim x seqlen floats)
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, dim=1536, seqlen=100, dstate=32))) == (
+        2 * (2 * 16 * 128) * 4 + 2 * 2 * 1536 * 100 * 4)
+    # the forward's accumulator is one such array
+    assert lib.ss_fwd_workspace_bytes(ctypes.byref(valid_fwd(nat, dim=1536, seqlen=100, dstate=32))) == (
+        2 * 1536 * 100 * 4)
+    # the general kernel (dstate 24) uses none; invalid arguments give -1
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(valid_bwd(nat, dim=1536, seqlen=100, dstate=24))) == 0
     bad = valid_bwd(nat)
     bad.dout = None
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(bad)) == -1

@@ -13,6 +13,10 @@ on; ``cpu_baseline`` times the C restatement of the reference's algorithm
 (oracle/ss_oracle.c, float64) on the same workload (or its first batch rows)
 on this host's cores.
 
+``--workload ss_fwd_bwd_b4_d5120_n16_l8192_bf16`` is the bf16 scan (batch 4,
+dim 5120, seqlen 8192); ``ss_fwd_bwd_b8_d1536_n32_l2048_f32`` the fp32 one at
+dstate 32 (the fast kernels once per 16-state slice).
+
 Other workloads (``--workload``; one JSON line each, reported against the
 reference's own op order run on the same GPU, not against the CPU):
   mamba_block_b8_l2048_d1024_bf16   MambaSimple block (d_model 1024, d_inner
@@ -61,6 +65,7 @@ WORKLOADS = {
     # name: (batch, dim, dstate, seqlen, dtype, seed)
     "ss_fwd_bwd_b8_d1536_n16_l2048_f32": (8, 1536, 16, 2048, "float32", 1001),
     "ss_fwd_bwd_b4_d5120_n16_l8192_bf16": (4, 5120, 16, 8192, "bfloat16", 1002),
+    "ss_fwd_bwd_b8_d1536_n32_l2048_f32": (8, 1536, 32, 2048, "float32", 1006),
 }
 DEFAULT = "ss_fwd_bwd_b8_d1536_n16_l2048_f32"
 MODEL_WORKLOADS = {
@@ -634,9 +639,15 @@ def main():
         ws = ss.workspace_bytes(u, dl, A, B, C, D, bias, dout, xck, True, du, dd, dA, dB, dC, dD, db,
                                 z=z, y=y, dz=dz)
         fname, bname = f"{fname}<{tname}, z>", f"{bname}<{tname}, z>"
+        # dstate 16 S: the fast kernels once per 16-state slice, with two fp32
+        # accumulators of batch x dim x seqlen floats in the workspace
+        passes = dstate // 16 if dstate > 16 and dstate % 16 == 0 else 1
+        acc = 2 * batch * dim * seqlen * 4 if passes > 1 else 0
+        if passes > 1:
+            fname, bname = f"{fname} x {passes} state slices", f"{bname} x {passes} state slices"
         # zero_grads: a fill launch clears the accumulators (and any dB / dC
         # slices) before the scan; with slices, a last launch sums them
-        bname = f"ss_zero_segs + {bname}" + (" + ss_ws_reduce" if ws > 0 else "")
+        bname = f"ss_zero_segs + {bname}" + (" + ss_ws_reduce" if ws - acc > 0 else "")
         kernel_ms = {}
         # the set-up above leaves the GPU idle and its clocks drop: warm the
         # prepared launches up as long as the steps, then time each kernel

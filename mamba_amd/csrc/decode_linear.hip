@@ -8,16 +8,16 @@
 // for it and take several times the weight's streaming time.
 //
 // A workgroup computes a 16 (n) x 16 (b) tile of Y, or one slice of K of
-// it, with NW waves that take every NW-th K step; each K step is one or two
-// v_mfma_f32_16x16x16_bf16 (or f16) with the W tile (16 n x 16 k) as A and
-// the X tile (16 k x 16 b) as B:
-//   A: lane l holds W[n0 + (l & 15)][4 (l >> 4) .. + 3] of a 16-wide k set
-//   B: lane l holds X[b0 + (l & 15)][the same k set]
+// it, with NW waves that take every NW-th K step; each K step is one MFMA
+// with the W tile (16 n x KS k) as A and the X tile (KS k x 16 b) as B.
+// With 16-byte aligned rows and k_in a multiple of 32 a K step covers 32 k
+// on gfx950's v_mfma_f32_16x16x32_bf16 (or f16):
+//   A: lane l holds W[n0 + (l & 15)][8 (l >> 4) .. + 7] (one 16-byte load)
+//   B: lane l holds X[b0 + (l & 15)][the same 8 k]
 //   D: lane l holds Y[b0 + (l & 15)][n0 + 4 (l >> 4) + v], v = 0..3
-// With 16-byte aligned rows and k_in a multiple of 32 a lane loads 8
-// elements (16 bytes) of its W row and X row per K step of 32: elements 0-3
-// feed one MFMA and 4-7 the next (each MFMA sums over its own k set, the
-// same for A and B); otherwise 4 elements (8 bytes) per K step of 16.  The
+// otherwise 16 k on v_mfma_f32_16x16x16_bf16 (or f16), with lane l holding
+// W[n0 + (l & 15)][4 (l >> 4) .. + 3] and the same k of its X row (an
+// 8-byte load each).  The
 // wave count grows with the steps a workgroup has (4, 8 or 16) so that a
 // wave requests all its steps before it uses any.  The partial tiles of the
 // waves are summed through LDS.
@@ -61,7 +61,10 @@ namespace ss {
 namespace {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
@@ -71,6 +74,18 @@ __device__ __forceinline__ f32x4 mfma16(s16x4 a, s16x4 b, f32x4 c) {
     } else {
         return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h16x4, a), __builtin_bit_cast(h16x4, b), c,
                                                      0, 0, 0);
+    }
+}
+
+// 16 x 16 x 32 product (gfx950): 8 k per lane
+template <typename T>
+__device__ __forceinline__ f32x4 mfma32(s16x8 a, s16x8 b, f32x4 c) {
+    if constexpr (__is_same(T, bf16_t)) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b16x8, a), __builtin_bit_cast(b16x8, b), c,
+                                                       0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, a), __builtin_bit_cast(h16x8, b), c,
+                                                      0, 0, 0);
     }
 }
 
@@ -251,8 +266,7 @@ __global__ __launch_bounds__(64 * NW) void decode_linear_kernel(const ss_decode_
             const rowvec<KV> z = {};
             const rowvec<KV> av_ = (live && nv) ? av[u] : z, xv_ = (live && bv) ? xv[u] : z;
             if constexpr (KV == 8) {
-                acc = mfma16<T>(av_.lo, xv_.lo, acc);
-                acc = mfma16<T>(av_.hi, xv_.hi, acc);
+                acc = mfma32<T>(av_, xv_, acc);
             } else {
                 acc = mfma16<T>(av_, xv_, acc);
             }

@@ -456,14 +456,10 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const int64_t slice = (c0 / kChPerWG) % q.ws_slices;
     const int64_t ld = q.bc_ld;
     const int64_t bc_off = (b * G + g) * (kAcc ? q.bc_N : int64_t(kT)) * ld * 4;
-    // (keep = false: a resource of zero bytes at the same place, through which
-    // every add is dropped)
-    auto bc_rsrc = [&](int which, bool keep) {
-        return q.ws ? make_rsrc_in(q.ws, (2 * slice + which) * q.ws_stride * 4 + bc_off, keep ? q.ws_end : 0)
-                    : make_rsrc_in(which ? q.dC : q.dB, bc_off, keep ? (which ? q.dC_end : q.dB_end) : 0);
-    };
-    const rsrc_t RdB = bc_rsrc(0, true);
-    const rsrc_t RdC = bc_rsrc(1, true);
+    const rsrc_t RdB = q.ws ? make_rsrc_in(q.ws, 2 * slice * q.ws_stride * 4 + bc_off, q.ws_end)
+                            : make_rsrc_in(q.dB, bc_off, q.dB_end);
+    const rsrc_t RdC = q.ws ? make_rsrc_in(q.ws, (2 * slice + 1) * q.ws_stride * 4 + bc_off, q.ws_end)
+                            : make_rsrc_in(q.dC, bc_off, q.dC_end);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + r) * es, od = uint32_t(row * p.dl_ds + r) * es;
     const uint32_t oo = uint32_t(row * q.do_ds + r) * es;
@@ -585,33 +581,39 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             v[kWaves + ww] = s_wg[((buf * 2 + 1) * kWaves + ww) * kT * 16 + wg_slot(ft, fn)];
         }
     };
-    // (TAIL: the workspace's padded rows have slots for the steps past the
-    // sequence.  In rows of seqlen floats, which only a call without
-    // workspace uses for a ragged seqlen, a partial chunk adds the sums of
-    // its steps past the sequence onto the last step, so no address leaves
-    // the row, and a chunk wholly past the sequence adds nothing (its adds go
-    // through a resource of zero bytes).  Those sums are zero unless the
-    // state is not finite (0 * inf past the end: the last step's own sum is
-    // then not finite either), so no other step of dB / dC sees them.)
+    // (TAIL: the sums of steps past the sequence are zero, but for a state
+    // that is not finite (0 * inf), so they are replaced by exact zeros.  The
+    // workspace's padded rows have slots for those steps.  In rows of seqlen
+    // floats, which only a call without workspace uses for a ragged seqlen,
+    // their zeros go elsewhere: a partial chunk's onto the last step; a chunk
+    // wholly past the sequence adds them onto the previous chunk's 16 steps,
+    // one per address (onto one address, all workgroups' adds of the chunk
+    // were serialised in the atomic unit: seqlen 2064 fp32 took 570 us
+    // against 338 us at 2048), where the ones past the sequence land on the
+    // first steps of the next state row, or past dB / dC's end, where the
+    // resource drops them.  Adding an exact zero changes no value.)
     auto flush_commit = [&](int ck, const float (&v)[2 * kWaves], auto TAIL) {
-        const float sB = (v[0] + v[1]) + (v[2] + v[3]);
-        const float sC = (v[4] + v[5]) + (v[6] + v[7]);
+        float sB = (v[0] + v[1]) + (v[2] + v[3]);
+        float sC = (v[4] + v[5]) + (v[6] + v[7]);
         uint32_t so = uint32_t(ck * kT) * 4u;
         uint32_t ofl = ofl0;
-        constexpr bool kTailc = decltype(TAIL)::value;
-        const bool keep = !kTailc || ck * kT < ld;
-        if constexpr (kTailc) {
+        if constexpr (decltype(TAIL)::value) {
             const int t = ck * kT + ft;
-            if (t >= ld) ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
+            const bool past = t >= L;
+            sB = past ? 0.f : sB;
+            sC = past ? 0.f : sC;
+            if (ck * kT >= ld) {
+                so = uint32_t((ck - 1) * kT) * 4u;
+            } else if (t >= ld) {
+                ofl = uint32_t(fn * ld + int(L) - 1 - ck * kT) * 4u;
+            }
         }
-        const rsrc_t RB_ = kTailc ? bc_rsrc(0, keep) : RdB;
-        const rsrc_t RC_ = kTailc ? bc_rsrc(1, keep) : RdC;
         if constexpr (kDet) {
-            bstore<float>(RB_, ofl, so, sB);
-            bstore<float>(RC_, ofl, so, sC);
+            bstore<float>(RdB, ofl, so, sB);
+            bstore<float>(RdC, ofl, so, sC);
         } else {
-            batomic_add(RB_, ofl, so, sB);
-            batomic_add(RC_, ofl, so, sC);
+            batomic_add(RdB, ofl, so, sB);
+            batomic_add(RdC, ofl, so, sC);
         }
     };
     auto flush = [&](int ck, int buf) {

@@ -99,7 +99,9 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
-    const bool pad_states = (N % 16) != 0;
+    // lanes past dstate: the last group's past dstate % 16, or whole groups
+    // when dstate is below 16 SPL (48 on SPL 4)
+    const bool pad_states = N < 16 * SPL;
 
     float A2[SPL], Av[SPL], Bc[SPL], Cc[SPL];
     float gcar[SPL], acar[SPL], dA_acc[SPL], dBc_acc[SPL], dCc_acc[SPL];

@@ -74,9 +74,10 @@ __global__ __launch_bounds__(kThreads) void ss_fwd_kernel(const FwdParams p) {
         float u, dl, z;
         float B[kT], C[kT];
     };
-    // Padding states (n >= dstate, only when dstate % 16 != 0) read a valid
-    // row and get C = 0, so their h never reaches y or x.
-    const bool pad_states = (N % 16) != 0;
+    // Padding states (n >= dstate: the last group's lanes past dstate % 16,
+    // or a whole group when dstate is below 16 SPL, e.g. 48 on SPL 4) read a
+    // valid row and get C = 0, so their h never reaches y or x.
+    const bool pad_states = N < 16 * SPL;
     auto load_bc = [&](int64_t t0, int s, float (&Bo)[kT], float (&Co)[kT]) {
         const int n = 16 * s + r;
         const bool nv = n < N;

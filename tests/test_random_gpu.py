@@ -9,7 +9,10 @@ output and gradient is compared elementwise with ``oracle/ss_oracle.c`` on
 the same (already rounded) inputs: fp32 rtol / atol 1e-3, bf16 / fp16
 2e-2.  The draw covers both the fast kernels (dstate 16, variable B and C,
 16-channel groups) and the general ones, ragged and tiny seqlens, and the
-sequence-segmented paths (small batch x dim with long sequences).
+sequence-segmented paths (small batch x dim with long sequences).  A second
+draw holds dstate 32 to 128 (multiples of 16) with variable B and C and
+16-channel groups: with a workspace those run as one fast-kernel pass per
+16-state slice, without one on the general kernels.
 """
 import random
 import sys
@@ -57,12 +60,37 @@ def _seq_view(t, pad):
     return v
 
 
+def _draw_slices(i):
+    rnd = random.Random(9500 + i)
+    n_groups = rnd.choice([1, 1, 2])
+    return dict(batch=rnd.choice([1, 2, 3]), dim=n_groups * rnd.choice([16, 32]),
+                dstate=rnd.choice([32, 32, 48, 64, 64, 128]),
+                seqlen=rnd.choice([1, 17, 63, 64, 65, 500, 2047, 2049, rnd.randint(1, 3000)]),
+                dtype=rnd.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16]),
+                n_groups=n_groups, var_B=True, var_C=True, has_z=rnd.random() < 0.8,
+                has_D=rnd.random() < 0.8, has_bias=rnd.random() < 0.8, softplus=rnd.random() < 0.8,
+                pad=rnd.choice([0, 0, 1, 8]), workspace=rnd.choice(["auto", "auto", "auto", None]),
+                seed=9600 + i)
+
+
 @pytest.mark.parametrize("i", range(N_CASES))
 def test_random_shape_against_c_oracle(i):
-    from mamba_amd import selective_scan as ss
     c = _draw(i)
     print(f"\n[random] case {i}: {c}", flush=True)
     sys.stdout.flush()
+    _run_case(c)
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_state_slices_against_c_oracle(i):
+    c = _draw_slices(i)
+    print(f"\n[random slices] case {i}: {c}", flush=True)
+    sys.stdout.flush()
+    _run_case(c)
+
+
+def _run_case(c):
+    from mamba_amd import selective_scan as ss
     x = make_inputs(c["batch"], c["dim"], c["dstate"], c["seqlen"], seed=c["seed"], dtype=c["dtype"],
                     n_groups=c["n_groups"], var_B=c["var_B"], var_C=c["var_C"], has_z=c["has_z"],
                     has_D=c["has_D"], has_delta_bias=c["has_bias"])

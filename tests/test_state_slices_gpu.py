@@ -17,6 +17,12 @@ The checkpoints keep the (batch, chunk, dim, dstate) layout on every path,
 so a forward on the slices followed by a backward on the general kernel
 (no workspace), and the reverse, give the same results: checked against
 the oracle too.
+
+The general kernels' padding lanes (states past dstate in the last group
+of 16, or whole groups when dstate is below 16 x the template's group
+count: 48, 80, 96, 144, 200) are checked against the oracle at 24 channels
+(not a multiple of 16, so only the general kernels apply), with variable
+and constant B / C.
 """
 import sys
 
@@ -116,6 +122,41 @@ def test_paths_share_the_checkpoints(fwd_fast, bwd_fast):
     t = {k: v.to(DEV) for k, v in x.items()}
     out, y, xck = _fwd(t, fwd_fast)
     got = _bwd(t, y, xck, bwd_fast)
+    torch.cuda.synchronize()
+    rout, _, rg = _oracle(x, True)
+    assert_close(out.cpu(), rout, 1e-3, 1e-3, "out")
+    for k, v in got.items():
+        assert_close(v.cpu(), rg[k], 1e-3, 1e-3, k)
+
+
+# (dstate, var_B, var_C, seqlen): the general kernels run states in groups of
+# 16 per lane row, SPL = 1, 2, 4, 8 or 16 groups; a dstate below 16 SPL
+# leaves padding lanes, in the last group (40: 8 of them) or as whole groups
+# (48 on SPL 4, 80 and 96 on SPL 8, 144 on SPL 16).  Padding lanes must add
+# nothing to y, du or ddelta.
+PAD_CASES = [
+    (40, True, True, 77),
+    (48, True, True, 77),
+    (48, False, True, 50),
+    (48, True, False, 50),
+    (80, True, True, 33),
+    (96, True, True, 40),
+    (144, True, True, 20),
+    (200, True, True, 20),
+]
+
+
+@pytest.mark.parametrize("case", PAD_CASES, ids=[f"n{c[0]}-{'vB' if c[1] else 'cB'}-{'vC' if c[2] else 'cC'}-l{c[3]}"
+                                                 for c in PAD_CASES])
+def test_general_kernels_with_padding_state_groups(case):
+    n, var_B, var_C, l = case
+    b, d = 2, 24
+    print(f"\n[slices] general kernels dstate {n} var_B {var_B} var_C {var_C} seqlen {l}", flush=True)
+    sys.stdout.flush()
+    x = make_inputs(b, d, n, l, seed=300 + n + l, var_B=var_B, var_C=var_C)
+    t = {k: v.to(DEV) for k, v in x.items()}
+    out, y, xck = _fwd(t, False)
+    got = _bwd(t, y, xck, False)
     torch.cuda.synchronize()
     rout, _, rg = _oracle(x, True)
     assert_close(out.cpu(), rout, 1e-3, 1e-3, "out")

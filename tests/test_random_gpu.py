@@ -12,7 +12,10 @@ the same (already rounded) inputs: fp32 rtol / atol 1e-3, bf16 / fp16
 sequence-segmented paths (small batch x dim with long sequences).  A second
 draw holds dstate 32 to 128 (multiples of 16) with variable B and C and
 16-channel groups: with a workspace those run as one fast-kernel pass per
-16-state slice, without one on the general kernels.
+16-state slice, without one on the general kernels.  A third draws any
+dstate from 1 to 256, any channel count per group, constant or variable B
+and C, and in about a third of the cases gradient accumulators that hold
+seeded values (no zero_grads: the backward must add to them).
 """
 import random
 import sys
@@ -73,6 +76,19 @@ def _draw_slices(i):
                 seed=9600 + i)
 
 
+def _draw_general(i):
+    rnd = random.Random(9800 + i)
+    n_groups = rnd.choice([1, 1, 2, 3])
+    var_B, var_C = rnd.random() < 0.6, rnd.random() < 0.6
+    return dict(batch=rnd.choice([1, 2, 3]), dim=n_groups * rnd.randint(1, 24), dstate=rnd.randint(1, 256),
+                seqlen=rnd.choice([1, 16, 33, rnd.randint(1, 600)]),
+                dtype=rnd.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16]),
+                n_groups=n_groups, var_B=var_B, var_C=var_C, has_z=rnd.random() < 0.7,
+                has_D=rnd.random() < 0.7, has_bias=rnd.random() < 0.7, softplus=rnd.random() < 0.8,
+                pad=rnd.choice([0, 1, 5]), workspace=rnd.choice(["auto", None]), seed=9900 + i,
+                accumulate=rnd.random() < 0.3)
+
+
 @pytest.mark.parametrize("i", range(N_CASES))
 def test_random_shape_against_c_oracle(i):
     c = _draw(i)
@@ -85,6 +101,14 @@ def test_random_shape_against_c_oracle(i):
 def test_random_state_slices_against_c_oracle(i):
     c = _draw_slices(i)
     print(f"\n[random slices] case {i}: {c}", flush=True)
+    sys.stdout.flush()
+    _run_case(c)
+
+
+@pytest.mark.parametrize("i", range(32))
+def test_random_general_shapes_against_c_oracle(i):
+    c = _draw_general(i)
+    print(f"\n[random general] case {i}: {c}", flush=True)
     sys.stdout.flush()
     _run_case(c)
 
@@ -114,13 +138,22 @@ def _run_case(c):
     ss.forward_into(u, dl, A, B, C, D, bias, c["softplus"], out, xck, z=z, y=y, workspace=ws)
     du, dd = (_seq_view(torch.empty(batch, dim, L, dtype=dt, device=DEV), pad) for _ in range(2))
     dz = _seq_view(torch.empty(batch, dim, L, dtype=dt, device=DEV), pad) if z is not None else None
-    dA = torch.empty(A.shape, dtype=torch.float32, device=DEV)
-    dB = torch.empty(B.shape, dtype=torch.float32, device=DEV)
-    dC = torch.empty(C.shape, dtype=torch.float32, device=DEV)
-    dD = torch.empty(D.shape, dtype=torch.float32, device=DEV) if D is not None else None
-    db = torch.empty(bias.shape, dtype=torch.float32, device=DEV) if bias is not None else None
+    acc = c.get("accumulate", False)
+    gen = torch.Generator().manual_seed(c["seed"] + 1)
+    start = {}
+
+    def grad_buf(shape):
+        if not acc:
+            return torch.empty(shape, dtype=torch.float32, device=DEV)
+        v = torch.randn(shape, generator=gen)
+        start[len(start)] = v
+        return v.to(DEV)
+
+    dA, dB, dC = grad_buf(A.shape), grad_buf(B.shape), grad_buf(C.shape)
+    dD = grad_buf(D.shape) if D is not None else None
+    db = grad_buf(bias.shape) if bias is not None else None
     ss.backward_into(u, dl, A, B, C, D, bias, dout, xck, c["softplus"], du, dd, dA, dB, dC, dD, db,
-                     z=z, y=y, dz=dz, workspace=ws, zero_grads=True)
+                     z=z, y=y, dz=dz, workspace=ws, zero_grads=not acc, deterministic=c.get("det"))
     torch.cuda.synchronize()
 
     args = dict(D=x["D"], z=x["z"], delta_bias=x["delta_bias"], delta_softplus=c["softplus"])
@@ -129,6 +162,11 @@ def _run_case(c):
     tol = TOL[dt]
     assert_close(out.float().cpu(), rout, tol, tol, "out")
     got = dict(du=du, ddelta=dd, dA=dA, dB=dB, dC=dC, dD=dD, ddelta_bias=db, dz=dz)
+    if acc:
+        # without zero_grads the backward adds to what the accumulators held
+        base = dict(zip([k for k in ("dA", "dB", "dC", "dD", "ddelta_bias") if got[k] is not None],
+                        start.values()))
+        rg = {k: (v + base[k] if k in base else v) for k, v in rg.items() if v is not None}
     for k, v in got.items():
         if v is None:
             continue

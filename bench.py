@@ -11,7 +11,9 @@ scratch) divided by the measured time per step, in GB/s.  ``roofline``
 describes the dominant kernel, timed with HIP events on the stream it runs
 on; ``cpu_baseline`` times the C restatement of the reference's algorithm
 (oracle/ss_oracle.c, float64) on the same workload (or its first batch rows)
-on this host's cores.
+on this host's cores, and, as ``cpu_baseline.selective_scan_ref``, the
+PyTorch oracle on a 96-channel sample of it (its per-step autograd
+backward does not scale to the full workload).
 
 ``--workload ss_fwd_bwd_b4_d5120_n16_l8192_bf16`` is the bf16 scan (batch 4,
 dim 5120, seqlen 8192); ``ss_fwd_bwd_b8_d1536_n32_l2048_f32`` the fp32 one at
@@ -511,6 +513,59 @@ def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
     }
 
 
+def cpu_ref_sample(dtype_name, seqlen, dstate, batch=1, dim=96, reps=3):
+    """Times the PyTorch oracle ``selective_scan_ref`` (a per-step loop in
+    fp32 with autograd for the backward) on this host's cores, forward
+    (no_grad) and forward + backward, on a bounded sample: `batch` rows of
+    `dim` channels at the workload's dstate and the given seqlen (its backward
+    through the per-step graph grows faster than the sample: 96 channels of
+    2048 steps take seconds, 1536 channels far more than a bench run may
+    spend, and so do longer sequences).  Median of
+    `reps` after one warm-up; GB/s by the same byte formula as ``value``."""
+    import torch
+    from oracle.selective_scan_ref import selective_scan_ref
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    x = synthetic_inputs(batch, dim, dstate, seqlen, seed=1001, dtype=torch.float32)
+    names = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
+    g = {k: x[k].clone().requires_grad_(True) for k in names}
+    args = lambda: (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"])
+
+    def fwd():
+        with torch.no_grad():
+            selective_scan_ref(*args(), z=g["z"], delta_bias=g["delta_bias"], delta_softplus=True)
+
+    def fwd_bwd():
+        out = selective_scan_ref(*args(), z=g["z"], delta_bias=g["delta_bias"], delta_softplus=True)
+        torch.autograd.grad(out, [g[k] for k in names], x["dout"])
+
+    times = {}
+    for name, fn in (("fwd", fwd), ("fwd_bwd", fwd_bwd)):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        times[name] = sorted(ts)[len(ts) // 2]
+    s = 2 if dtype_name != "float32" else 4
+    fwd_b, bwd_b = algorithmic_bytes(batch, dim, dstate, seqlen, s)
+    print(f"[bench] cpu selective_scan_ref: batch {batch} x dim {dim}: fwd {times['fwd']:.3f} s, "
+          f"fwd+bwd {times['fwd_bwd']:.3f} s on {threads} threads", file=sys.stderr, flush=True)
+    return {
+        "value": round((fwd_b + bwd_b) / times["fwd_bwd"] / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "fwd_s": round(times["fwd"], 4),
+        "fwd_bwd_s": round(times["fwd_bwd"], 4),
+        "sample": f"oracle/selective_scan_ref.py (the PyTorch oracle, fp32, autograd backward) on batch {batch} "
+                  f"x dim {dim} x seqlen {seqlen} x dstate {dstate}: median of {reps} after one warm-up; "
+                  f"same byte formula as value",
+    }
+
+
 def time_copy(mib, reps=5):
     """Copies `mib` MiB device to device `reps` times; (bytes copied, ms per copy)."""
     import torch
@@ -717,6 +772,8 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(dtype_name, batch, dim, seqlen, dstate)
         line["cpu_baseline"]["gpu_speedup"] = round(gbs / line["cpu_baseline"]["value"], 1)
+        # the PyTorch oracle beside it, on a bounded sample
+        line["cpu_baseline"]["selective_scan_ref"] = cpu_ref_sample(dtype_name, min(seqlen, 2048), dstate)
     print(json.dumps(line), flush=True)
 
 

@@ -15,7 +15,8 @@ draw holds dstate 32 to 128 (multiples of 16) with variable B and C and
 16-state slice, without one on the general kernels.  A third draws any
 dstate from 1 to 256, any channel count per group, constant or variable B
 and C, and in about a third of the cases gradient accumulators that hold
-seeded values (no zero_grads: the backward must add to them).
+seeded values (no zero_grads: the backward must add to them).  A fourth
+holds dstate 16 with B and C both constant, which the fast kernels take.
 """
 import random
 import sys
@@ -101,6 +102,25 @@ def test_random_shape_against_c_oracle(i):
 def test_random_state_slices_against_c_oracle(i):
     c = _draw_slices(i)
     print(f"\n[random slices] case {i}: {c}", flush=True)
+    sys.stdout.flush()
+    _run_case(c)
+
+
+def _draw_const_bc(i):
+    rnd = random.Random(9700 + i)
+    return dict(batch=rnd.choice([1, 2, 3]), dim=rnd.choice([16, 32, 48, 64]), dstate=16,
+                seqlen=rnd.choice([1, 15, 17, 63, 64, 100, 2047, 2049, rnd.randint(1, 3000)]),
+                dtype=rnd.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16]),
+                n_groups=1, var_B=False, var_C=False, has_z=rnd.random() < 0.8,
+                has_D=rnd.random() < 0.8, has_bias=rnd.random() < 0.8, softplus=rnd.random() < 0.8,
+                pad=rnd.choice([0, 0, 1, 8]), workspace=rnd.choice(["auto", None]), seed=9750 + i,
+                accumulate=rnd.random() < 0.3)
+
+
+@pytest.mark.parametrize("i", range(20))
+def test_random_constant_bc_against_c_oracle(i):
+    c = _draw_const_bc(i)
+    print(f"\n[random constant B / C] case {i}: {c}", flush=True)
     sys.stdout.flush()
     _run_case(c)
 

@@ -313,8 +313,8 @@ int64_t ws_bytes_for(const ss::BwdParams& p, int* slices, int* nseg, int64_t* sl
     *slice_bytes = 0;
     const bool fast = ss::bwd_fast_ok(p);
     const int64_t stride = p.f.batch * (p.f.dim / p.f.dpg) * p.f.dstate * ss::bwd_ws_ld(p.f.seqlen);
-    // (dB / dC slices only for variable B / C)
-    if (fast && p.f.var_B && (p.det || *slices > 1 || p.f.seqlen % 32 != 0)) {
+    // (dB / dC slices only with B and C both variable)
+    if (fast && p.f.var_B && p.f.var_C && (p.det || *slices > 1 || p.f.seqlen % 32 != 0)) {
         *slice_bytes = int64_t(2) * *slices * stride * int64_t(sizeof(float));
     } else {
         *slices = 1;

@@ -405,13 +405,13 @@ __device__ __forceinline__ int wg_slot(int t, int n) { return t * 16 + (n ^ t); 
 // are added to those of the earlier slices (p.acc, fp32) and, but in the last
 // pass, stored back there; the per-step outputs computed from them are only
 // kept in the last pass (the host sets the other passes' extents to 0).
-// kVBC: B and C vary per step (B / C tile through LDS, dB / dC per (state,
+// kVB / kVC: B / C vary per step (tile through LDS, dB / dC per (state,
 // step) summed over the workgroup's channels and added to global memory);
-// false: both constant, (dim, dstate) fp32, held in registers, and dB / dC
-// per (channel, state) accumulated in each lane over the chunks and added
-// once at the end, so the kernel has no B / C tile, no dB / dC flush and no
-// barrier.
-template <typename IT, bool kZ, bool kDet, bool kAcc, bool kVBC>
+// false: constant, (dim, dstate) fp32, held in registers, with dB / dC per
+// (channel, state) accumulated in each lane over the chunks and added once
+// at the end.  With both constant the kernel has no B / C tile, no dB / dC
+// flush and no barrier.
+template <typename IT, bool kZ, bool kDet, bool kAcc, bool kVB, bool kVC>
 // 3 workgroups per CU (12 waves): at most 168 VGPRs and about 53 KB of LDS
 // (3 x 53,248 B share a CU; at 54,272 B only 2 do, measured).
 __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
@@ -455,8 +455,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const rsrc_t Ro = make_rsrc_in(q.dout, (b * q.do_bs + c0 * q.do_ds) * es64, q.do_end);
     const rsrc_t Rz = kZ ? make_rsrc_in(p.z, (b * p.z_bs + c0 * p.z_ds) * es64, p.z_end) : make_rsrc_n(nullptr, 0);
     const rsrc_t Ry = kZ ? make_rsrc_in(p.y, (b * p.y_bs + c0 * p.y_ds) * es64, p.y_end) : make_rsrc_n(nullptr, 0);
-    const rsrc_t RB = kVBC ? make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end) : make_rsrc_n(nullptr, 0);
-    const rsrc_t RC = kVBC ? make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t RB = kVB ? make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t RC = kVC ? make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end) : make_rsrc_n(nullptr, 0);
     const rsrc_t Rdu = make_rsrc_in(q.du, (b * q.du_bs + c0 * q.du_ds) * es64, q.du_end);
     const rsrc_t Rdd = make_rsrc_in(q.ddelta, (b * q.dd_bs + c0 * q.dd_ds) * es64, q.dd_end);
     const rsrc_t Rdz = kZ ? make_rsrc_in(q.dz, (b * q.dz_bs + c0 * q.dz_ds) * es64, q.dz_end) : make_rsrc_n(nullptr, 0);
@@ -504,8 +504,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
     const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
     // constant B / C: this lane's B[c][r], C[c][r], and its dB, dC sums
-    const float bconst = kVBC ? 0.f : static_cast<const float*>(p.B)[c * p.B_gs + r * p.B_ns];
-    const float cconst = kVBC ? 0.f : static_cast<const float*>(p.C)[c * p.C_gs + r * p.C_ns];
+    const float bconst = kVB ? 0.f : static_cast<const float*>(p.B)[c * p.B_gs + r * p.B_ns];
+    const float cconst = kVC ? 0.f : static_cast<const float*>(p.C)[c * p.C_gs + r * p.C_ns];
     float dBc = 0.f, dCc = 0.f;
 
     // (s1, s2) summed over the row's 16 states, 8 steps (half a chunk) at a
@@ -548,8 +548,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             P.z = 0.f;
             P.y = 0.f;
         }
-        P.B = kVBC ? bload<IT>(RB, oB, so) : 0.f;
-        P.C = kVBC ? bload<IT>(RC, oC, so) : 0.f;
+        P.B = kVB ? bload<IT>(RB, oB, so) : 0.f;
+        P.C = kVC ? bload<IT>(RC, oC, so) : 0.f;
         const float v = x_load(ck > 0 ? ck - 1 : 0);
         P.x = ck > 0 ? v : 0.f;
     };
@@ -571,16 +571,15 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             P.z = 0.f;
             P.y = 0.f;
         }
-        P.B = (kVBC && in) ? bload<IT>(RB, uint32_t(row * p.B_ns + te) * es, 0) : 0.f;
-        P.C = (kVBC && in) ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
+        P.B = (kVB && in) ? bload<IT>(RB, uint32_t(row * p.B_ns + te) * es, 0) : 0.f;
+        P.C = (kVC && in) ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
         const float v = x_load(ck > 0 ? ck - 1 : 0);
         P.x = ck > 0 ? v : 0.f;
     };
     // this lane's element of the B / C tile (state row, step r) into buffer buf
     auto stage = [&](const Chunk& P, int buf) {
-        if constexpr (!kVBC) return;
-        s_bc[(buf * 2 + 0) * 16 * kT + bc_slot(row, r)] = P.B;
-        s_bc[(buf * 2 + 1) * 16 * kT + bc_slot(row, r)] = P.C;
+        if constexpr (kVB) s_bc[(buf * 2 + 0) * 16 * kT + bc_slot(row, r)] = P.B;
+        if constexpr (kVC) s_bc[(buf * 2 + 1) * 16 * kT + bc_slot(row, r)] = P.C;
     };
     // dB / dC of chunk ck from wave-partial buffer buf: thread (n, t) sums the
     // 4 waves and adds once into global memory (16 consecutive steps per state)
@@ -626,12 +625,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
             bstore<float>(RdB, ofl, so, sB);
             bstore<float>(RdC, ofl, so, sC);
         } else {
-            batomic_add(RdB, ofl, so, sB);
-            batomic_add(RdC, ofl, so, sC);
+            if constexpr (kVB) batomic_add(RdB, ofl, so, sB);
+            if constexpr (kVC) batomic_add(RdC, ofl, so, sC);
         }
     };
     auto flush = [&](int ck, int buf) {
-        if constexpr (!kVBC) return;
+        if constexpr (!kVB && !kVC) return;
         float v[2 * kWaves];
         flush_read(buf, v);
         flush_commit(ck, v, std::false_type{});
@@ -660,7 +659,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         const int ck = __builtin_amdgcn_readfirstlane(ck_in);
         // B / C tile of ck staged; dB / dC partials of ck + 1 complete (the
         // transposition area is per row)
-        if constexpr (kVBC) lds_barrier();
+        if constexpr (kVB || kVC) lds_barrier();
         const Chunk cur = cur_in;
         fetch(ck > k0 + 1 ? ck - 2 : k0, cur_in);
         // the earlier slices' sums of this chunk's steps (state slices; the
@@ -682,18 +681,21 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         const float* sC = s_bc + (buf * 2 + 1) * 16 * kT;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if constexpr (kVBC) {
+            if constexpr (kVB) {
                 const float4 vb = *reinterpret_cast<const float4*>(sB + bc_slot(r, 4 * i));
-                const float4 vc = *reinterpret_cast<const float4*>(sC + bc_slot(r, 4 * i));
                 Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
-                Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
             } else {
                 Bq[4 * i] = Bq[4 * i + 1] = Bq[4 * i + 2] = Bq[4 * i + 3] = bconst;
+            }
+            if constexpr (kVC) {
+                const float4 vc = *reinterpret_cast<const float4*>(sC + bc_slot(r, 4 * i));
+                Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
+            } else {
                 Cq[4 * i] = Cq[4 * i + 1] = Cq[4 * i + 2] = Cq[4 * i + 3] = cconst;
             }
         }
         float fv[2 * kWaves];
-        if constexpr (kVBC) flush_read(buf ^ 1, fv);
+        if constexpr (kVB || kVC) flush_read(buf ^ 1, fv);
 
         const float uu = cur.u, pre = cur.d + bias, dout = cur.o, zz = cur.z, yv = cur.y, h0 = cur.x;
         float dt = softplus ? softplus20(pre) : pre;
@@ -712,7 +714,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         });
         // the LDS reads issued above have had the decay factors to land
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (kVBC) flush_commit(ck + 1 < k1 ? ck + 1 : k1 - 1, fv, TAIL);
+        if constexpr (kVB || kVC) flush_commit(ck + 1 < k1 ? ck + 1 : k1 - 1, fv, TAIL);
         float hcur = h0;
         static_for<kT>([&](auto K) {
             constexpr int k = decltype(K)::value;
@@ -744,16 +746,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                 bfmac<k>(dA_acc, dt, gah);
                 s2p[ki] = gah;                       // times A_n in the sum over states
                 s1p[ki] = gv * Bq[k];
-                if constexpr (kVBC) {
-                    dBp[ki] = bmul<k>(dtu, gv);
-                    dCp[ki] = bmul<k>(dy, hs[k]);
-                } else if (!kTail || ck * kT + k < L) {
-                    // constant B / C: this lane's dB, dC over the steps (a
-                    // step past the sequence adds nothing, also for a state
-                    // that is not finite)
-                    bfmac<k>(dBc, dtu, gv);
-                    bfmac<k>(dCc, dy, hs[k]);
-                }
+                // constant B / C: this lane's dB, dC over the steps (a step
+                // past the sequence adds nothing, also for a state that is
+                // not finite)
+                if constexpr (kVB) dBp[ki] = bmul<k>(dtu, gv);
+                else if (!kTail || ck * kT + k < L) bfmac<k>(dBc, dtu, gv);
+                if constexpr (kVC) dCp[ki] = bmul<k>(dy, hs[k]);
+                else if (!kTail || ck * kT + k < L) bfmac<k>(dCc, dy, hs[k]);
             });
             // (s1, s2) of steps 4kg..4kg+3 as two float4 (steps 2m, 2m+1 of the half)
             float* trh = trw;
@@ -763,10 +762,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
                 make_float4(s1p[2], s2p[2], s1p[3], s2p[3]);
             // dB / dC of steps 4kg..4kg+3 summed over the wave's rows: row j
             // holds step 4kg + j
-            if constexpr (kVBC) {
-                wgB[wg_slot(4 * kg + j, r)] = rows4_sum(dBp[0], dBp[1], dBp[2], dBp[3]);
-                wgC[wg_slot(4 * kg + j, r)] = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
-            }
+            if constexpr (kVB) wgB[wg_slot(4 * kg + j, r)] = rows4_sum(dBp[0], dBp[1], dBp[2], dBp[3]);
+            if constexpr (kVC) wgC[wg_slot(4 * kg + j, r)] = rows4_sum(dCp[0], dCp[1], dCp[2], dCp[3]);
             if constexpr ((kg & 1) == 0) {           // half hh is written: read it back
                 float2 (&tv)[8] = hh ? tv1 : tv0;
 #pragma unroll
@@ -849,13 +846,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
         chunk(ck, PA, PB, std::integral_constant<int, 1>{}, std::false_type{});
         chunk(ck - 1, PB, PA, std::integral_constant<int, 0>{}, std::false_type{});
     }
-    if constexpr (kVBC) {
+    if constexpr (kVB || kVC) {
         lds_barrier();
         flush(k0, 0);
-    } else {
-        atomicAdd(q.dB + c * kT + r, dBc);
-        atomicAdd(q.dC + c * kT + r, dCc);
     }
+    if constexpr (!kVB) atomicAdd(q.dB + c * kT + r, dBc);
+    if constexpr (!kVC) atomicAdd(q.dC + c * kT + r, dCc);
 
     // ---- per-channel and per-(channel, state) sums over time and batch
     dD_acc = row_allsum(dD_acc);
@@ -1020,8 +1016,8 @@ bool bwd_fast_ok(const BwdParams& q) {
     // below 2^26 elements, checkpoints addressed from their own chunk (dim
     // below 2^24)
     // (a seqlen that is not a multiple of 32 ends in identity-padded chunks)
-    // (B and C both variable, or both constant without deterministic sums)
-    return p.dstate == 16 && ((p.var_B && p.var_C) || (!p.var_B && !p.var_C && !q.det)) && p.seqlen >= 1 &&
+    // (deterministic sums only with B and C both variable)
+    return p.dstate == 16 && ((p.var_B && p.var_C) || !q.det) && p.seqlen >= 1 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 && (!p.has_z || p.y != nullptr) &&
            small_strides({p.seqlen + 2 * kT, p.u_ds, p.dl_ds, p.z_ds, p.y_ds, p.B_ns, p.C_ns,
                           q.do_ds, q.du_ds, q.dd_ds, q.dz_ds}) &&
@@ -1143,7 +1139,7 @@ static hipError_t launch_zero(const BwdParams& p, bool sliced, hipStream_t strea
 hipError_t launch_bwd_zero_only(const BwdParams& p, hipStream_t stream) { return launch_zero(p, false, stream); }
 
 int bwd_ws_slices(const BwdParams& p) {
-    if (!bwd_fast_ok(p) || !p.f.var_B) return 1;   // (constant B / C: dB / dC per channel, no slices)
+    if (!bwd_fast_ok(p) || !p.f.var_B || !p.f.var_C) return 1;   // (slices only with B and C both variable)
     if (p.det) return int(p.f.dpg / kChPerWG);   // one slice per channel block of a group
     // at most 96 channel blocks per slice: each workgroup adds once per
     // (state, step) and chunk, so the contention of up to 96 adders per
@@ -1153,6 +1149,16 @@ int bwd_ws_slices(const BwdParams& p) {
     const int64_t blocks = p.f.dpg / kChPerWG;
     const int64_t k = (blocks + 95) / 96;
     return int(k < 1 ? 1 : (k > 16 ? 16 : k));
+}
+
+// the fast backward for the combination of variable / constant B and C
+template <typename IT, bool kZ>
+static void launch_bwd_bc(const BwdParams& p, dim3 grid, dim3 block, hipStream_t stream) {
+    const FwdParams& f = p.f;
+    if (f.var_B && f.var_C) hipLaunchKernelGGL((ss_bwd_fast<IT, kZ, false, false, true, true>), grid, block, 0, stream, p);
+    else if (f.var_B) hipLaunchKernelGGL((ss_bwd_fast<IT, kZ, false, false, true, false>), grid, block, 0, stream, p);
+    else if (f.var_C) hipLaunchKernelGGL((ss_bwd_fast<IT, kZ, false, false, false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((ss_bwd_fast<IT, kZ, false, false, false, false>), grid, block, 0, stream, p);
 }
 
 template <typename IT>
@@ -1181,17 +1187,15 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
         }
         const dim3 sgrid(unsigned(nblk * p.f.batch * nseg));
         if (p.det) {
-            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, true, false, true>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, true, false, true>), sgrid, block, 0, stream, p);
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, true, false, true, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, true, false, true, true>), sgrid, block, 0, stream, p);
         } else if (p.f.acc) {
-            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false, true, true>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false, true, true>), sgrid, block, 0, stream, p);
-        } else if (vbc) {
-            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false, false, true>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false, false, true>), sgrid, block, 0, stream, p);
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false, true, true, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false, true, true, true>), sgrid, block, 0, stream, p);
+        } else if (p.f.has_z) {
+            launch_bwd_bc<IT, true>(p, sgrid, block, stream);
         } else {
-            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, false, false, false>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, false, false, false>), sgrid, block, 0, stream, p);
+            launch_bwd_bc<IT, false>(p, sgrid, block, stream);
         }
         if (p.det) {
             const int64_t n = p.f.dim * (kT + 2);

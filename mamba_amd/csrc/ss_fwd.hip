@@ -248,11 +248,11 @@ __device__ __forceinline__ int ct_slot4(int t, int i) { return t * 16 + 4 * (i ^
 // slice): y is added to the sums over the earlier slices (p.acc, fp32) and,
 // but in the last pass, stored back there instead of becoming out / y (whose
 // extents the host sets to 0 then; D is applied in the last pass only).
-// kVBC: B and C vary per step (both staged per super-chunk through LDS);
-// false: both constant, (dim, dstate) fp32, held in registers for the whole
-// launch (each lane its channel's B of its state and the 16 C of its
-// channel), so the kernel has no B / C tile and no barrier.
-template <typename IT, bool kZ, bool kAcc, bool kVBC>
+// kVB / kVC: B / C vary per step (staged per super-chunk through LDS);
+// false: constant, (dim, dstate) fp32, held in registers for the whole
+// launch (each lane its channel's B of its state; the 16 C of its channel).
+// With both constant the kernel has no B / C tile and no barrier.
+template <typename IT, bool kZ, bool kAcc, bool kVB, bool kVC>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B [n][64 steps], C [64 steps][n]]
     __shared__ __attribute__((aligned(16))) float s_yp[kWaves * kRows * kYRow];    // [wave][row][n][16 steps]
@@ -289,8 +289,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const rsrc_t Ru = make_rsrc_in(p.u, (b * p.u_bs + c0 * p.u_ds) * es64, p.u_end);
     const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
     const rsrc_t Rz = kZ ? make_rsrc_in(p.z, (b * p.z_bs + c0 * p.z_ds) * es64, p.z_end) : make_rsrc_n(nullptr, 0);
-    const rsrc_t RB = kVBC ? make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end) : make_rsrc_n(nullptr, 0);
-    const rsrc_t RC = kVBC ? make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t RB = kVB ? make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end) : make_rsrc_n(nullptr, 0);
+    const rsrc_t RC = kVC ? make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end) : make_rsrc_n(nullptr, 0);
     // out / y are written with 16-byte stores, which take their advance in the
     // resource base and no uniform offset (see bstore4).  Without a y (or x)
     // buffer the stores go through a zero-byte resource and are dropped: a
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
     // constant B: this lane's B[c][r]
-    const float bconst = kVBC ? 0.f : static_cast<const float*>(p.B)[c * p.B_gs + r * p.B_ns];
+    const float bconst = kVB ? 0.f : static_cast<const float*>(p.B)[c * p.B_gs + r * p.B_ns];
 
     struct Super { float4 u, d, z, B, C; };
     auto fetch = [&](int sc, Super& S) {       // 0 <= sc < nsc
@@ -335,8 +335,8 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         S.u = bload4<IT>(Ru, ou, so);
         S.d = bload4<IT>(Rd, od, so);
         S.z = kZ ? bload4<IT>(Rz, oz, so) : make_float4(0.f, 0.f, 0.f, 0.f);
-        S.B = kVBC ? bload4<IT>(RB, oB, so) : make_float4(0.f, 0.f, 0.f, 0.f);
-        S.C = kVBC ? bload4<IT>(RC, oC, so) : make_float4(0.f, 0.f, 0.f, 0.f);
+        S.B = kVB ? bload4<IT>(RB, oB, so) : make_float4(0.f, 0.f, 0.f, 0.f);
+        S.C = kVC ? bload4<IT>(RC, oC, so) : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     // the tail super-chunk sc: element loads at offsets clamped to its lt
     // steps, zero past them
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             const int tc = t < lt ? t : lt - 1;
 #pragma unroll
             for (int k = 0; k < 5; ++k) {
-                const float x = ((k == 2 && !kZ) || (k >= 3 && !kVBC)) ? 0.f
+                const float x = ((k == 2 && !kZ) || (k == 3 && !kVB) || (k == 4 && !kVC)) ? 0.f
                                                                        : bload<IT>(R[k], uint32_t(rs[k] + tc) * es, so);
                 v[k][i] = t < lt ? x : 0.f;
             }
@@ -363,15 +363,16 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
         S.C = make_float4(v[4][0], v[4][1], v[4][2], v[4][3]);
     };
     auto stage = [&](const Super& S, int buf) {
-        if constexpr (!kVBC) return;
-        *reinterpret_cast<float4*>(s_bc + (buf * 2 + 0) * 16 * kSC + bc64_slot(row, r)) = S.B;
-        // C transposed: step 4r + i, state row
-        float* ct = s_bc + (buf * 2 + 1) * 16 * kSC;
-        const int ci = 4 * ((row >> 2) ^ (r & 3)) + (row & 3);
-        ct[(4 * r + 0) * 16 + ci] = S.C.x;
-        ct[(4 * r + 1) * 16 + ci] = S.C.y;
-        ct[(4 * r + 2) * 16 + ci] = S.C.z;
-        ct[(4 * r + 3) * 16 + ci] = S.C.w;
+        if constexpr (kVB) *reinterpret_cast<float4*>(s_bc + (buf * 2 + 0) * 16 * kSC + bc64_slot(row, r)) = S.B;
+        if constexpr (kVC) {
+            // C transposed: step 4r + i, state row
+            float* ct = s_bc + (buf * 2 + 1) * 16 * kSC;
+            const int ci = 4 * ((row >> 2) ^ (r & 3)) + (row & 3);
+            ct[(4 * r + 0) * 16 + ci] = S.C.x;
+            ct[(4 * r + 1) * 16 + ci] = S.C.y;
+            ct[(4 * r + 2) * 16 + ci] = S.C.z;
+            ct[(4 * r + 3) * 16 + ci] = S.C.w;
+        }
     };
     // this row's product tile: lane n writes its steps 4m..4m+3 as a float4
     // at n * 16 + 4 * (m ^ ((n >> 1) & 3)); lane r reads step r of state n at
@@ -477,7 +478,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     // of this lane's channel, for every step)
     float cT[kT];
 #pragma unroll
-    for (int n = 0; n < kT; ++n) cT[n] = kVBC ? 0.f : static_cast<const float*>(p.C)[c * p.C_gs + n * p.C_ns];
+    for (int n = 0; n < kT; ++n) cT[n] = kVC ? 0.f : static_cast<const float*>(p.C)[c * p.C_gs + n * p.C_ns];
 
     Super S;
     // one super-chunk: the full ones prefetch the next and stage its B / C
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
     auto super_chunk = [&](int sc, auto TAIL) {
         constexpr bool kTail = decltype(TAIL)::value;
         const int buf = (sc - sc0) & 1;
-        if constexpr (kVBC) lds_barrier();   // B / C tile of sc staged (the other LDS areas are per row)
+        if constexpr (kVB || kVC) lds_barrier();   // B / C tile of sc staged (the other LDS areas are per row)
         const float4 cu = S.u, cd = S.d, cz = S.z;
         if constexpr (!kTail) fetch(sc + 1 < scf ? sc + 1 : scf - 1, S);
 
@@ -520,7 +521,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
             float Bq[kT];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if constexpr (kVBC) {
+                if constexpr (kVB) {
                     const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
                     Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
                 } else {
@@ -565,7 +566,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                     make_float4(yp[4 * m], yp[4 * m + 1], yp[4 * m + 2], yp[4 * m + 3]);
             // C of step r of this chunk, for its sum one chunk later (read
             // now: this buffer is not restaged before the next barrier)
-            if constexpr (kVBC) {
+            if constexpr (kVC) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float4 vc = *reinterpret_cast<const float4*>(sC + ct_slot4(16 * q + r, i));
@@ -709,11 +710,19 @@ bool fwd_fast_ok(const FwdParams& p) {
     // below 2^26 elements, checkpoints addressed from each super-chunk's
     // first chunk (dim x the checkpoints' states per channel below 2^28)
     // (a seqlen that is not a multiple of 64 ends in a partial super-chunk)
-    // (B and C both variable, or both constant)
-    return p.dstate == 16 && p.var_B == p.var_C && p.seqlen >= 1 &&
+    return p.dstate == 16 && p.seqlen >= 1 &&
            p.dim % kChPerWG == 0 && p.dpg % kChPerWG == 0 &&
            small_strides({p.seqlen, p.u_ds, p.dl_ds, p.z_ds, p.o_ds, p.y_ds, p.B_ns, p.C_ns}) &&
            p.dim * p.xN < (int64_t(1) << 28);
+}
+
+// the fast forward for the combination of variable / constant B and C
+template <typename IT, bool kZ>
+static void launch_fwd_bc(const FwdParams& p, dim3 grid, dim3 block, hipStream_t stream) {
+    if (p.var_B && p.var_C) hipLaunchKernelGGL((ss_fwd_fast<IT, kZ, false, true, true>), grid, block, 0, stream, p);
+    else if (p.var_B) hipLaunchKernelGGL((ss_fwd_fast<IT, kZ, false, true, false>), grid, block, 0, stream, p);
+    else if (p.var_C) hipLaunchKernelGGL((ss_fwd_fast<IT, kZ, false, false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((ss_fwd_fast<IT, kZ, false, false, false>), grid, block, 0, stream, p);
 }
 
 template <typename IT>
@@ -733,14 +742,12 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
         }
         const dim3 sgrid(unsigned(nblk * p.batch * nseg));
         if (p.acc) {
-            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, true, true>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, true, true>), sgrid, block, 0, stream, p);
-        } else if (vbc) {
-            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, false, true>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, false, true>), sgrid, block, 0, stream, p);
+            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, true, true, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, true, true, true>), sgrid, block, 0, stream, p);
+        } else if (p.has_z) {
+            launch_fwd_bc<IT, true>(p, sgrid, block, stream);
         } else {
-            if (p.has_z) hipLaunchKernelGGL((ss_fwd_fast<IT, true, false, false>), sgrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_fwd_fast<IT, false, false, false>), sgrid, block, 0, stream, p);
+            launch_fwd_bc<IT, false>(p, sgrid, block, stream);
         }
     } else if (spl <= 1) {
         if (vbc) hipLaunchKernelGGL((ss_fwd_kernel<IT, 1, true>), grid, block, 0, stream, p);

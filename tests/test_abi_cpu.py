@@ -390,8 +390,8 @@ def test_kernel_name_query(nat, lib):
     a.is_var_B = 0
     a.B_batch_stride, a.B_group_stride, a.B_dstate_stride = 0, 32, 1
     assert fname(a) == "ss_fwd_kernel"
-    # dstate 16 with B and C both constant ((dim, dstate) fp32): the fast
-    # kernels; one of them constant: the general ones
+    # dstate 16 with B and C, or one of them, constant ((dim, dstate) fp32):
+    # the fast kernels
     def const_bc(x, both=True):
         x.is_var_B = 0
         x.B_batch_stride, x.B_group_stride, x.B_dstate_stride = 0, 16, 1
@@ -400,13 +400,13 @@ def test_kernel_name_query(nat, lib):
             x.C_batch_stride, x.C_group_stride, x.C_dstate_stride = 0, 16, 1
         return x
     assert fname(const_bc(valid_fwd(nat, seqlen=100))) == "ss_fwd_fast"
-    assert fname(const_bc(valid_fwd(nat, seqlen=100), both=False)) == "ss_fwd_kernel"
+    assert fname(const_bc(valid_fwd(nat, seqlen=100), both=False)) == "ss_fwd_fast"
     b = valid_bwd(nat, seqlen=100)
     const_bc(b.f)
     assert bname(b) == "ss_bwd_fast"
     b = valid_bwd(nat, seqlen=100)
     const_bc(b.f, both=False)
-    assert bname(b) == "ss_bwd_kernel"
+    assert bname(b) == "ss_bwd_fast"
     # no work, and invalid arguments
     assert fname(valid_fwd(nat, batch=0)) == ""
     bad = valid_fwd(nat)

@@ -16,7 +16,8 @@ draw holds dstate 32 to 128 (multiples of 16) with variable B and C and
 dstate from 1 to 256, any channel count per group, constant or variable B
 and C, and in about a third of the cases gradient accumulators that hold
 seeded values (no zero_grads: the backward must add to them).  A fourth
-holds dstate 16 with B and C both constant, which the fast kernels take.
+holds dstate 16 with B and C, or one of them, constant, which the fast
+kernels take.
 """
 import random
 import sys
@@ -108,16 +109,19 @@ def test_random_state_slices_against_c_oracle(i):
 
 def _draw_const_bc(i):
     rnd = random.Random(9700 + i)
-    return dict(batch=rnd.choice([1, 2, 3]), dim=rnd.choice([16, 32, 48, 64]), dstate=16,
+    var_B, var_C = rnd.choice([(False, False), (False, False), (True, False), (False, True)])
+    dim = rnd.choice([16, 32, 48, 64])
+    n_groups = rnd.choice([1, 2]) if (var_B or var_C) and dim % 32 == 0 else 1
+    return dict(batch=rnd.choice([1, 2, 3]), dim=dim, dstate=16,
                 seqlen=rnd.choice([1, 15, 17, 63, 64, 100, 2047, 2049, rnd.randint(1, 3000)]),
                 dtype=rnd.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16]),
-                n_groups=1, var_B=False, var_C=False, has_z=rnd.random() < 0.8,
+                n_groups=n_groups, var_B=var_B, var_C=var_C, has_z=rnd.random() < 0.8,
                 has_D=rnd.random() < 0.8, has_bias=rnd.random() < 0.8, softplus=rnd.random() < 0.8,
                 pad=rnd.choice([0, 0, 1, 8]), workspace=rnd.choice(["auto", None]), seed=9750 + i,
                 accumulate=rnd.random() < 0.3)
 
 
-@pytest.mark.parametrize("i", range(20))
+@pytest.mark.parametrize("i", range(32))
 def test_random_constant_bc_against_c_oracle(i):
     c = _draw_const_bc(i)
     print(f"\n[random constant B / C] case {i}: {c}", flush=True)

@@ -897,8 +897,9 @@ __global__ __launch_bounds__(256) void ss_det_param_reduce(const float* __restri
 // step first, with the fast backward's lane layout and arithmetic but
 // nothing else (no recomputed state, no gradients), and writes the carry it
 // leaves at the segment's first step, g_t a_t, to seg_h and the segment's
-// sum of delta' to seg_s.
-template <typename IT, bool kZ>
+// sum of delta' to seg_s.  kVC false: C constant ((dim, dstate) fp32, in a
+// register; no tile, no barrier).
+template <typename IT, bool kZ, bool kVC>
 __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams q) {
     __shared__ __attribute__((aligned(16))) float s_c[2 * 16 * kT];                  // [buf][n][t]
     const FwdParams& p = q.f;
@@ -925,12 +926,13 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
     const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
     const rsrc_t Ro = make_rsrc_in(q.dout, (b * q.do_bs + c0 * q.do_ds) * es64, q.do_end);
     const rsrc_t Rz = kZ ? make_rsrc_in(p.z, (b * p.z_bs + c0 * p.z_ds) * es64, p.z_end) : make_rsrc_n(nullptr, 0);
-    const rsrc_t RC = make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end);
+    const rsrc_t RC = kVC ? make_rsrc_in(p.C, (b * p.C_bs + g * p.C_gs) * es64, p.C_end) : make_rsrc_n(nullptr, 0);
     constexpr uint32_t es = sizeof(IT);
 
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
     const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
+    const float cconst = kVC ? 0.f : static_cast<const float*>(p.C)[c * p.C_gs + r * p.C_ns];
 
     struct Ck { float d, o, z, C; };
     // steps past a ragged sequence's end (the last segment's last chunks) are
@@ -946,7 +948,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
             P.d = bload<IT>(Rd, od, so);
             P.o = bload<IT>(Ro, oo, so);
             P.z = kZ ? bload<IT>(Rz, oz, so) : 0.f;
-            P.C = bload<IT>(RC, oC, so);
+            P.C = kVC ? bload<IT>(RC, oC, so) : 0.f;
             return;
         }
         const int t = ck * kT + r;
@@ -955,9 +957,11 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
         P.d = in ? bload<IT>(Rd, uint32_t(row * p.dl_ds + te) * es, 0) : (softplus ? -INFINITY : -bias);
         P.o = in ? bload<IT>(Ro, uint32_t(row * q.do_ds + te) * es, 0) : 0.f;
         P.z = kZ && in ? bload<IT>(Rz, uint32_t(row * p.z_ds + te) * es, 0) : 0.f;
-        P.C = in ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
+        P.C = (kVC && in) ? bload<IT>(RC, uint32_t(row * p.C_ns + te) * es, 0) : 0.f;
     };
-    auto stage = [&](const Ck& P, int buf) { s_c[buf * 16 * kT + bc_slot(row, r)] = P.C; };
+    auto stage = [&](const Ck& P, int buf) {
+        if constexpr (kVC) s_c[buf * 16 * kT + bc_slot(row, r)] = P.C;
+    };
 
     float ga = 0.f, dsum = 0.f;
     Ck P;
@@ -965,15 +969,20 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
     stage(P, 0);
     for (int ck = k1 - 1; ck >= k0; --ck) {
         const int buf = (k1 - 1 - ck) & 1;
-        lds_barrier();   // C tile of ck staged
+        if constexpr (kVC) lds_barrier();   // C tile of ck staged
         const Ck cur = P;
         fetch(ck > k0 ? ck - 1 : k0, P);
         float Cq[kT];
         const float* sC = s_c + buf * 16 * kT;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 vc = *reinterpret_cast<const float4*>(sC + bc_slot(r, 4 * i));
-            Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
+            if constexpr (kVC) {
+                const float4 vc = *reinterpret_cast<const float4*>(sC + bc_slot(r, 4 * i));
+                Cq[4 * i] = vc.x; Cq[4 * i + 1] = vc.y; Cq[4 * i + 2] = vc.z; Cq[4 * i + 3] = vc.w;
+            } else {
+                // (past a ragged end the steps are identity steps with dout 0)
+                Cq[4 * i] = Cq[4 * i + 1] = Cq[4 * i + 2] = Cq[4 * i + 3] = cconst;
+            }
         }
         const float pre = cur.d + bias;
         float dt = softplus ? softplus20(pre) : pre;
@@ -1004,8 +1013,7 @@ bool bwd_fast_ok(const BwdParams& q);
 // Segments for the backward (seg_count): whole chunk pairs, at least 8
 // pairs (16 chunks) each.
 int bwd_segments(const BwdParams& q) {
-    // (the segments' carry pass reads variable C only)
-    if (!bwd_fast_ok(q) || !q.f.var_B || !q.f.var_C) return 1;
+    if (!bwd_fast_ok(q)) return 1;
     const FwdParams& p = q.f;
     return seg_count(p.batch * (p.dim / kChPerWG), (p.seqlen + 2 * kT - 1) / (2 * kT), 8);
 }
@@ -1182,8 +1190,13 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
         const int nseg = p.f.nseg > 1 ? p.f.nseg : 1;
         if (nseg > 1) {
             const dim3 agrid(unsigned(nblk * p.f.batch * (nseg - 1)));
-            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_seg_carry<IT, true>), agrid, block, 0, stream, p);
-            else hipLaunchKernelGGL((ss_bwd_seg_carry<IT, false>), agrid, block, 0, stream, p);
+            if (p.f.var_C) {
+                if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_seg_carry<IT, true, true>), agrid, block, 0, stream, p);
+                else hipLaunchKernelGGL((ss_bwd_seg_carry<IT, false, true>), agrid, block, 0, stream, p);
+            } else {
+                if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_seg_carry<IT, true, false>), agrid, block, 0, stream, p);
+                else hipLaunchKernelGGL((ss_bwd_seg_carry<IT, false, false>), agrid, block, 0, stream, p);
+            }
         }
         const dim3 sgrid(unsigned(nblk * p.f.batch * nseg));
         if (p.det) {

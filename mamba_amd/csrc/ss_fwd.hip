@@ -604,7 +604,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 // arithmetic, but only the state recurrence (no C, no outputs), and writes
 // the state after the segment's last step to seg_h and the segment's sum of
 // delta' to seg_s.  About three fifths of a full scan's work per step.
-template <typename IT>
+// kVB false: B constant ((dim, dstate) fp32, in a register; no tile, no
+// barrier).
+template <typename IT, bool kVB>
 __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_b[2 * 16 * kSC];               // [buf][n][64 steps]
 
@@ -630,7 +632,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     constexpr int64_t es64 = sizeof(IT);
     const rsrc_t Ru = make_rsrc_in(p.u, (b * p.u_bs + c0 * p.u_ds) * es64, p.u_end);
     const rsrc_t Rd = make_rsrc_in(p.delta, (b * p.dl_bs + c0 * p.dl_ds) * es64, p.dl_end);
-    const rsrc_t RB = make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end);
+    const rsrc_t RB = kVB ? make_rsrc_in(p.B, (b * p.B_bs + g * p.B_gs) * es64, p.B_end) : make_rsrc_n(nullptr, 0);
     constexpr uint32_t es = sizeof(IT);
     const uint32_t ou = uint32_t(row * p.u_ds + 4 * r) * es, od = uint32_t(row * p.dl_ds + 4 * r) * es;
     const uint32_t oB = uint32_t(row * p.B_ns + 4 * r) * es;
@@ -638,16 +640,17 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
     const float a2 = p.A[c * p.A_ds + r * p.A_ns] * kLog2e;
     const bool softplus = p.softplus != 0;
+    const float bconst = kVB ? 0.f : static_cast<const float*>(p.B)[c * p.B_gs + r * p.B_ns];
 
     struct Seg { float4 u, d, B; };
     auto fetch = [&](int sc, Seg& S) {
         const uint32_t so = uint32_t(sc * kSC) * es;
         S.u = bload4<IT>(Ru, ou, so);
         S.d = bload4<IT>(Rd, od, so);
-        S.B = bload4<IT>(RB, oB, so);
+        S.B = kVB ? bload4<IT>(RB, oB, so) : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     auto stage = [&](const Seg& S, int buf) {
-        *reinterpret_cast<float4*>(s_b + buf * 16 * kSC + bc64_slot(row, r)) = S.B;
+        if constexpr (kVB) *reinterpret_cast<float4*>(s_b + buf * 16 * kSC + bc64_slot(row, r)) = S.B;
     };
 
     float h = 0.f, dsum = 0.f;
@@ -656,7 +659,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
     stage(S, 0);
     for (int sc = sc0; sc < sc1; ++sc) {
         const int buf = (sc - sc0) & 1;
-        lds_barrier();   // B tile of sc staged
+        if constexpr (kVB) lds_barrier();   // B tile of sc staged
         const float4 cu = S.u, cd = S.d;
         fetch(sc + 1 < sc1 ? sc + 1 : sc1 - 1, S);
         float4 dt, dtu;
@@ -674,8 +677,12 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
             float Bq[kT];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
-                Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
+                if constexpr (kVB) {
+                    const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
+                    Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
+                } else {
+                    Bq[4 * i] = Bq[4 * i + 1] = Bq[4 * i + 2] = Bq[4 * i + 3] = bconst;
+                }
             }
             float a[kT];
             static_for<kT>([&](auto K) {
@@ -700,8 +707,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
 bool fwd_fast_ok(const FwdParams& p);
 constexpr int kSegMinSC = 4;
 int fwd_segments(const FwdParams& p) {
-    // (the segments' state pass reads variable B only)
-    if (!fwd_fast_ok(p) || !p.var_B || !p.var_C) return 1;
+    if (!fwd_fast_ok(p)) return 1;
     return seg_count(p.batch * (p.dim / kChPerWG), (p.seqlen + kSC - 1) / kSC, kSegMinSC);
 }
 
@@ -736,7 +742,8 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
         const int nseg = p.nseg > 1 ? p.nseg : 1;
         if (nseg > 1) {
             const dim3 agrid(unsigned(nblk * p.batch * (nseg - 1)));
-            hipLaunchKernelGGL((ss_fwd_seg_state<IT>), agrid, block, 0, stream, p);
+            if (p.var_B) hipLaunchKernelGGL((ss_fwd_seg_state<IT, true>), agrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_fwd_seg_state<IT, false>), agrid, block, 0, stream, p);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }

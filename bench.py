@@ -419,8 +419,8 @@ def cpu_model():
 
 def cpu_threads():
     """Host threads for the CPU baselines: every core this process may run
-    on, capped by OMP_NUM_THREADS when that is set (a GPU box allots each GPU
-    a share of its cores and sets it to that share)."""
+    on, capped by OMP_NUM_THREADS when that is set (a multi-GPU host that
+    gives each GPU's process a share of its cores sets it to that share)."""
     n = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS", "")
     if omp.isdigit() and int(omp) > 0:

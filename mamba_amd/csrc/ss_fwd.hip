@@ -252,8 +252,15 @@ __device__ __forceinline__ int ct_slot4(int t, int i) { return t * 16 + 4 * (i ^
 // false: constant, (dim, dstate) fp32, held in registers for the whole
 // launch (each lane its channel's B of its state; the 16 C of its channel).
 // With both constant the kernel has no B / C tile and no barrier.
+// 16-bit I/O (not state-sliced): the B tile is read just before the state
+// recurrence instead of ahead of the decay factors, which fits 128 VGPRs and
+// so 4 workgroups per CU (bf16 forward about 5 % faster at 1,280 and 1,536
+// workgroups; fp32, whose wider streams gain nothing from the fourth
+// workgroup, keeps the early reads and 3 per CU).
+template <typename IT, bool kAcc>
+constexpr bool fwd_late_b() { return sizeof(IT) != 4 && !kAcc; }
 template <typename IT, bool kZ, bool kAcc, bool kVB, bool kVC>
-__global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
+__global__ __launch_bounds__(kThreads, (fwd_late_b<IT, kAcc>() ? 4 : 3)) void ss_fwd_fast(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) float s_bc[2 * 2 * 16 * kSC];          // [buf][B [n][64 steps], C [64 steps][n]]
     __shared__ __attribute__((aligned(16))) float s_yp[kWaves * kRows * kYRow];    // [wave][row][n][16 steps]
     __shared__ __attribute__((aligned(16))) float s_yo[kWaves * kRows * kYoRow];   // [wave][row][64 steps]
@@ -518,14 +525,18 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
 
         static_for<kQ>([&](auto Q) {
             constexpr int q = decltype(Q)::value;
+            // B of this lane's state for the chunk's 16 steps (read here, or
+            // just before the recurrence for the 128-VGPR build)
             float Bq[kT];
+            if constexpr (!fwd_late_b<IT, kAcc>()) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (kVB) {
-                    const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
-                    Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
-                } else {
-                    Bq[4 * i] = Bq[4 * i + 1] = Bq[4 * i + 2] = Bq[4 * i + 3] = bconst;
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (kVB) {
+                        const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
+                        Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
+                    } else {
+                        Bq[4 * i] = Bq[4 * i + 1] = Bq[4 * i + 2] = Bq[4 * i + 3] = bconst;
+                    }
                 }
             }
             // states of the previous chunk, written by this row last chunk
@@ -552,6 +563,17 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_fast(const FwdParams p) {
                 }
                 pu = cu;     // this super-chunk's u, z wait for its outputs
                 pz = cz;
+            }
+            if constexpr (fwd_late_b<IT, kAcc>()) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (kVB) {
+                        const float4 vb = *reinterpret_cast<const float4*>(sB + bc64_slot(r, 4 * q + i));
+                        Bq[4 * i] = vb.x; Bq[4 * i + 1] = vb.y; Bq[4 * i + 2] = vb.z; Bq[4 * i + 3] = vb.w;
+                    } else {
+                        Bq[4 * i] = Bq[4 * i + 1] = Bq[4 * i + 2] = Bq[4 * i + 3] = bconst;
+                    }
+                }
             }
             float yp[kT];
             static_for<kT>([&](auto K) {

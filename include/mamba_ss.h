@@ -136,7 +136,7 @@ typedef struct ss_bwd_args {
        it, the dB / dC sums over channels are spread over several copies and
        added up at the end, instead of every channel block adding into the
        same dB / dC addresses; for a dstate of 16 S (32, 48, ..., 256; variable
-       B and C, not deterministic) it also holds two fp32 accumulators of
+       B and C) it also holds two fp32 accumulators of
        batch x dim x seqlen floats, with which the backward runs the dstate-16
        fast kernel once per 16-state slice (ABI v16).  NULL (or less than
        ss_bwd_workspace_bytes()) gives the same results, more slowly when many
@@ -154,11 +154,12 @@ typedef struct ss_bwd_args {
        channels, and dA, dD and ddelta_bias over batch rows and sequence
        segments, in a fixed order instead of by atomic adds, so repeated calls
        on the same inputs give the same bits.  Needs the fast kernels (dstate
-       16, variable B and C, dim and channels per group multiples of 16;
-       SS_ERR_UNSUPPORTED otherwise) and a workspace of
-       ss_bwd_workspace_bytes() bytes (one dB / dC partial per 16-channel
-       block: batch * dim / 8 * dstate * seqlen floats, seqlen rounded up to
-       a multiple of 32).  No counterpart in the reference, whose sums are
+       16, or 16 S as one pass per 16-state slice; variable B and C, dim and
+       channels per group multiples of 16; SS_ERR_UNSUPPORTED otherwise) and
+       a workspace of ss_bwd_workspace_bytes() bytes (one dB / dC partial per
+       16-channel block: batch * dim / 8 * 16 * seqlen floats, seqlen rounded
+       up to a multiple of 32, plus the accumulators of the 16 S passes).
+       No counterpart in the reference, whose sums are
        atomic (backward_kernel.cu:472-475,553-578). */
     int32_t deterministic;
 } ss_bwd_args;
@@ -224,9 +225,11 @@ int ss_bwd(const ss_bwd_args* a, void* stream);
    loops, harnesses that forbid hipMalloc).  Same arguments, kernels and
    results as ss_bwd; a->workspace and a->workspace_bytes are ignored.  The
    scratch that ss_bwd would take from a workspace (dB / dC slices, sequence
-   segment carries) comes from a fixed device buffer of
-   SS_NOALLOC_SCRATCH_BYTES bytes inside the library, one per GPU, held until
-   the process ends; arguments that need more (ss_bwd_workspace_bytes) are
+   segment carries, the accumulators of dstate 16 S) comes from a fixed
+   device buffer of SS_NOALLOC_SCRATCH_BYTES bytes inside the library, one
+   per GPU, held until the process ends.  A dstate of 16 S whose passes need
+   more runs as one pass on the general kernel, as ss_bwd without a
+   workspace; other arguments that need more (ss_bwd_workspace_bytes) are
    rejected with SS_ERR_UNSUPPORTED.  Every call on a GPU shares that GPU's
    buffer, and each call clears what it uses: calls that overlap in time on
    one GPU (several streams or threads) race and must be serialised by the

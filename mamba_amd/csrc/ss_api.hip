@@ -281,10 +281,10 @@ ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     return p;
 }
 
-// Slices of the backward for p (1 as for fwd_slices; not with deterministic
-// sums; the two accumulators below 2^31 bytes, addressed from one base).
+// Slices of the backward for p (1 as for fwd_slices; the two accumulators
+// below 2^31 bytes, addressed from one base).
 int bwd_slices(const ss::BwdParams& p) {
-    if (p.det || fwd_slices(p.f) <= 1) return 1;
+    if (fwd_slices(p.f) <= 1) return 1;
     ss::BwdParams q = p;
     q.f.dstate = ss::kT;
     if (!ss::bwd_fast_ok(q) || p.f.batch * p.f.dim * p.f.seqlen >= (int64_t(1) << 29)) return 1;
@@ -324,13 +324,14 @@ int64_t ws_bytes_for(const ss::BwdParams& p, int* slices, int* nseg, int64_t* sl
     return *slice_bytes + ss::fwd_seg_bytes(p.f, *nseg) + par;
 }
 
-// Deterministic sums need the fast kernels.
+// Deterministic sums need the fast kernels (dstate 16, or 16 S on them
+// once per slice).
 int check_det(const ss::BwdParams& p) {
     if (!p.det) return SS_OK;
-    if (!ss::bwd_fast_ok(p))
+    if (!ss::bwd_fast_ok(p) && bwd_slices(p) <= 1)
         return fail(SS_ERR_UNSUPPORTED,
-                    "deterministic sums need the fast backward (dstate 16, variable B and C, dim and channels "
-                    "per group multiples of 16)");
+                    "deterministic sums need the fast backward (dstate 16 or a multiple of 16, variable B and C, "
+                    "dim and channels per group multiples of 16)");
     return SS_OK;
 }
 
@@ -414,7 +415,9 @@ int bwd_run_slices(const ss_bwd_args* a, ss::BwdParams p, int S, void* ws, int s
         ss::BwdParams q = p;
         const int64_t n0 = int64_t(ss::kT) * s;
         q.f = slice_fwd(p.f, s, es);
-        q.zero_grads = 0;
+        // (deterministic sums: each pass stores or adds its own rows of the
+        // gradients in a fixed order; otherwise they were cleared up front)
+        q.zero_grads = p.det ? p.zero_grads : 0;
         q.dA = p.dA + n0;
         // dB / dC rows of this slice: (batch, group) blocks of dstate rows of
         // seqlen floats, the slice's 16 from row n0
@@ -435,6 +438,8 @@ int bwd_run_slices(const ss_bwd_args* a, ss::BwdParams p, int S, void* ws, int s
             q.f.seg_h = reinterpret_cast<float*>(static_cast<char*>(ws) + slice_bytes);
             q.f.seg_s = q.f.seg_h + q.f.batch * nseg * q.f.dim * 16;
         }
+        if (p.det)
+            q.det_par = reinterpret_cast<float*>(static_cast<char*>(ws) + slice_bytes + ss::fwd_seg_bytes(q.f, nseg));
         q.f.acc = acc;
         q.f.acc_in_end = s > 0 ? bwd_acc_bytes(p) : 0;
         q.f.acc_out_end = s < S - 1 ? bwd_acc_bytes(p) : 0;
@@ -448,6 +453,19 @@ int bwd_run_slices(const ss_bwd_args* a, ss::BwdParams p, int S, void* ws, int s
         if (e != hipSuccess) return fail(SS_ERR_HIP, "backward launch failed: %s", hipGetErrorString(e));
     }
     return ok();
+}
+
+// Workspace bytes for the backward's fastest path for p: the state-sliced
+// passes (what one pass needs, then the two accumulators) or one pass.
+int64_t bwd_ws_need(const ss::BwdParams& p, int itype) {
+    int slices = 1, nseg = 1;
+    int64_t slice_bytes = 0;
+    if (bwd_slices(p) > 1) {
+        ss::BwdParams q0 = p;
+        q0.f = slice_fwd(p.f, 0, elem_size(itype));
+        return ws_bytes_for(q0, &slices, &nseg, &slice_bytes) + bwd_acc_bytes(p);
+    }
+    return ws_bytes_for(p, &slices, &nseg, &slice_bytes);
 }
 
 int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
@@ -464,6 +482,9 @@ int bwd_run(const ss_bwd_args* a, void* ws, int64_t ws_bytes, void* stream) {
         const int64_t pass_bytes = ws_bytes_for(q0, &slices, &nseg, &slice_bytes);
         if (ws && ws_bytes >= pass_bytes + bwd_acc_bytes(p))
             return bwd_run_slices(a, p, S, ws, slices, nseg, slice_bytes, pass_bytes, static_cast<hipStream_t>(stream));
+        if (p.det)
+            return fail(SS_ERR_INVALID, "deterministic sums need a workspace of %lld bytes",
+                        (long long)(pass_bytes + bwd_acc_bytes(p)));
         // without that much workspace: the general kernel, as below
     }
     int slices = 1, nseg = 1;
@@ -622,14 +643,7 @@ int64_t ss_bwd_workspace_bytes(const ss_bwd_args* a) {
     const ss::BwdParams p = make_bwd_params(a);
     if (check_det(p) != SS_OK) return -1;
     ok();
-    int slices = 1, nseg = 1;
-    int64_t slice_bytes = 0;
-    if (bwd_slices(p) > 1) {
-        ss::BwdParams q0 = p;
-        q0.f = slice_fwd(p.f, 0, elem_size(a->f.itype));
-        return ws_bytes_for(q0, &slices, &nseg, &slice_bytes) + bwd_acc_bytes(p);
-    }
-    return ws_bytes_for(p, &slices, &nseg, &slice_bytes);
+    return bwd_ws_need(p, a->f.itype);
 }
 
 const char* ss_fwd_kernel_name(const ss_fwd_args* a) {
@@ -666,9 +680,12 @@ int ss_bwd_noalloc(const ss_bwd_args* a, void* stream) {
     const ss::BwdParams p = make_bwd_params(a);
     rc = check_det(p);
     if (rc != SS_OK) return rc;
+    // the state-sliced passes when their workspace fits (deterministic sums
+    // need it), else the one-pass backward
     int slices = 1, nseg = 1;
     int64_t slice_bytes = 0;
-    const int64_t need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
+    int64_t need = bwd_ws_need(p, a->f.itype);
+    if (need > kScratchBytes && !p.det && bwd_slices(p) > 1) need = ws_bytes_for(p, &slices, &nseg, &slice_bytes);
     if (need > kScratchBytes)
         return fail(SS_ERR_UNSUPPORTED,
                     "ss_bwd_noalloc: these arguments need %lld bytes of scratch, more than the %lld bytes "

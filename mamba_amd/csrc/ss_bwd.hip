@@ -876,13 +876,16 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_fast(const BwdParams q) {
 // Deterministic sums of the dA, dD, ddelta_bias partials: element i of
 // [dA (dim * 16), dD (dim), ddelta_bias (dim)] is the sum of the rows'
 // entries in row order, then added to the accumulator or, with overwrite,
-// stored in its place.
+// stored in its place.  dA rows are dA_N floats apart (16, or the call's
+// dstate for a pass of a state-sliced backward, whose dA is based at its
+// slice's first state).
 __global__ __launch_bounds__(256) void ss_det_param_reduce(const float* __restrict__ par, int rows, int64_t dim,
                                                            float* __restrict__ dA, float* __restrict__ dD,
-                                                           float* __restrict__ db, int overwrite) {
+                                                           float* __restrict__ db, int overwrite, int64_t dA_N) {
     const int64_t n = dim * (kT + 2);
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-        float* dst = i < dim * kT ? dA + i : (i < dim * (kT + 1) ? dD + (i - dim * kT) : db + (i - dim * (kT + 1)));
+        float* dst = i < dim * kT ? dA + (i / kT) * dA_N + i % kT
+                                  : (i < dim * (kT + 1) ? dD + (i - dim * kT) : db + (i - dim * (kT + 1)));
         if (i >= dim * kT && i < dim * (kT + 1) && !dD) continue;
         if (i >= dim * (kT + 1) && !db) continue;
         float s = 0.f;
@@ -1199,7 +1202,10 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
             }
         }
         const dim3 sgrid(unsigned(nblk * p.f.batch * nseg));
-        if (p.det) {
+        if (p.det && p.f.acc) {
+            if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, true, true, true, true>), sgrid, block, 0, stream, p);
+            else hipLaunchKernelGGL((ss_bwd_fast<IT, false, true, true, true, true>), sgrid, block, 0, stream, p);
+        } else if (p.det) {
             if (p.f.has_z) hipLaunchKernelGGL((ss_bwd_fast<IT, true, true, false, true, true>), sgrid, block, 0, stream, p);
             else hipLaunchKernelGGL((ss_bwd_fast<IT, false, true, false, true, true>), sgrid, block, 0, stream, p);
         } else if (p.f.acc) {
@@ -1214,7 +1220,8 @@ static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
             const int64_t n = p.f.dim * (kT + 2);
             const unsigned pgrid = unsigned((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
             hipLaunchKernelGGL(ss_det_param_reduce, dim3(pgrid), dim3(256), 0, stream, p.det_par,
-                               int(p.f.batch * nseg), p.f.dim, p.dA, p.dD, p.ddelta_bias, int(p.zero_grads));
+                               int(p.f.batch * nseg), p.f.dim, p.dA, p.dD, p.ddelta_bias, int(p.zero_grads),
+                               p.f.acc ? p.dA_N : int64_t(kT));
         }
         if (sliced && flat) {
             hipLaunchKernelGGL(ss_ws_reduce, dim3(rgrid), dim3(256), 0, stream,

@@ -738,7 +738,14 @@ def test_deterministic_workspace_query(nat, lib):
     b.deterministic = 1
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == (2 * 96 * (16 * 32768) * 4 + 1 * 8 * 1536 * 17 * 4
                                                           + 1 * 8 * 1536 * 18 * 4)
-    b = valid_bwd(nat, batch=1, dim=32, seqlen=100, dstate=32)     # dstate 32: the general kernel
+    # dstate 32: two passes of the fast kernel, one per 16-state slice; what
+    # one pass needs (2 dB / dC slices of 16 rows padded to 128 floats, one
+    # row of partials) then the two accumulators (batch x dim x seqlen fp32)
+    b = valid_bwd(nat, batch=1, dim=32, seqlen=100, dstate=32)
+    b.deterministic = 1
+    assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == (2 * 2 * (16 * 128) * 4 + 1 * 32 * 18 * 4
+                                                          + 2 * 32 * 100 * 4)
+    b = valid_bwd(nat, batch=1, dim=32, seqlen=100, dstate=24)     # dstate 24: the general kernel
     b.deterministic = 1
     assert lib.ss_bwd_workspace_bytes(ctypes.byref(b)) == -1
     assert "deterministic" in lib.ss_last_error().decode()

@@ -5,8 +5,9 @@ ddelta_bias over batch rows and sequence segments in a fixed order, so the
 backward gives the same bits on every run.  Checked, through the C ABI
 (``backward_into``):
 * three runs bit-identical in every output, on the serial fast kernel, on
-  a group with several dB / dC slices and on the sequence-segmented kernel
-  (one long sequence);
+  a group with several dB / dC slices, on the sequence-segmented kernel
+  (one long sequence) and on dstate 32 / 64 (one pass of the fast kernel
+  per 16-state slice, fixed-order sums in each);
 * the results against the float64 oracle (fp32 rtol / atol 1e-3) and
   against the atomic sums to 1e-5 relative (the same sums in another
   order);
@@ -44,12 +45,12 @@ def _say(msg):
     sys.stdout.flush()
 
 
-def _setup(batch, dim, L, seed, dtype=torch.float32):
+def _setup(batch, dim, L, seed, dtype=torch.float32, N=16):
     from mamba_amd import selective_scan as ss
-    x = make_inputs(batch, dim, 16, L, seed=seed, dtype=dtype)
+    x = make_inputs(batch, dim, N, L, seed=seed, dtype=dtype)
     t = {k: x[k].to(DEV) for k in NAMES + ("dout",)}
     out, y = torch.empty_like(t["delta"]), torch.empty_like(t["delta"])
-    xck = torch.empty((batch, ss.n_chunks(L), dim, 16), dtype=torch.float32, device=DEV)
+    xck = torch.empty((batch, ss.n_chunks(L), dim, N), dtype=torch.float32, device=DEV)
     ss.forward_into(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], True, out, xck,
                     z=t["z"], y=y)
     return x, t, out, y, xck
@@ -68,19 +69,22 @@ def _backward(t, y, xck, det, zero=True, init=None):
     return g
 
 
-# (batch, dim, seqlen): serial fast kernel, 2 channel blocks per slice group
-# boundary (192 blocks: 192 slices), one long sequence (8 segments), ragged
-# seqlens (1001: identity-padded tail chunks in slices with padded rows;
-# 2064: a wholly padded last chunk)
-CASES = [(2, 256, 512), (1, 3072, 256), (1, 256, 4096), (1, 256, 1001), (2, 64, 2064)]
+# (batch, dim, seqlen, dstate): serial fast kernel, 2 channel blocks per
+# slice group boundary (192 blocks: 192 slices), one long sequence (8
+# segments), ragged seqlens (1001: identity-padded tail chunks in slices with
+# padded rows; 2064: a wholly padded last chunk); dstate 32 and 64 (state
+# slices, one with sequence segments and one ragged)
+CASES = [(2, 256, 512, 16), (1, 3072, 256, 16), (1, 256, 4096, 16), (1, 256, 1001, 16), (2, 64, 2064, 16),
+         (2, 64, 300, 32), (1, 256, 4096, 32), (1, 32, 1001, 64)]
 
 
-@pytest.mark.parametrize("case", CASES, ids=["serial", "many-blocks", "segments", "ragged-1001", "ragged-2064"])
+@pytest.mark.parametrize("case", CASES, ids=["serial", "many-blocks", "segments", "ragged-1001", "ragged-2064",
+                                             "n32", "n32-segments", "n64-ragged"])
 def test_deterministic_backward_is_reproducible_and_correct(case):
     from mamba_amd import selective_scan as ss
-    batch, dim, L = case
-    _say(f"batch {batch} dim {dim} seqlen {L}")
-    x, t, out, y, xck = _setup(batch, dim, L, seed=300 + dim)
+    batch, dim, L, N = case
+    _say(f"batch {batch} dim {dim} seqlen {L} dstate {N}")
+    x, t, out, y, xck = _setup(batch, dim, L, seed=300 + dim + N, N=N)
     g0 = _backward(t, y, xck, det=True)
     nbytes = ss.workspace_bytes(t["u"], t["delta"], t["A"], t["B"], t["C"], t["D"], t["delta_bias"], t["dout"], xck,
                                 True, g0["du"], g0["ddelta"], g0["dA"], g0["dB"], g0["dC"], g0["dD"],
@@ -163,8 +167,8 @@ def test_torch_deterministic_setting_drives_autograd():
         a, b = grads(x), grads(x)
         for k in names:
             assert torch.equal(a[k], b[k]), k
-        # dstate 32: the general kernel, which has no deterministic sums
-        xr = make_inputs(1, 32, 32, 100, seed=332)
+        # dstate 24: the general kernel, which has no deterministic sums
+        xr = make_inputs(1, 32, 24, 100, seed=332)
         with pytest.raises(RuntimeError, match="deterministic"):
             grads(xr)
         torch.use_deterministic_algorithms(True, warn_only=True)

@@ -8,6 +8,9 @@ workspace from torch on the same inputs.  du, ddelta and dz come from the
 same kernels in the same order and must match bit for bit; dA, dB, dC, dD
 and ddelta_bias are fp32 atomic sums whose order varies between launches,
 so they are compared to 1e-5 relative (well inside the fp32 bar of 1e-3).
+With deterministic sums on dstate 32 (two passes of the fast kernel, one
+per 16-state slice, whose accumulators also sit in the buffer) every
+output matches bit for bit, again on two calls, the second smaller.
 """
 import ctypes
 import sys
@@ -32,13 +35,14 @@ def _grads(x, dev):
     return g
 
 
-def _run(x, g, entry):
+def _run(x, g, entry, det=0):
     """One backward through the C ABI: entry 'ss_bwd' (torch workspace) or 'ss_bwd_noalloc'."""
     u, dl, A, B, C, D, z, bias = (x[k] for k in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias"))
     lib = nat.load()
     b = ss._bwd_into_args(u, dl, A, B, C, D, bias, x["dout"], x["xck"], True, g["du"], g["ddelta"],
                           g["dA"], g["dB"], g["dC"], g["dD"], g["ddelta_bias"], z, x["y"], g["dz"])
     b.zero_grads = 1
+    b.deterministic = det
     need = lib.ss_bwd_workspace_bytes(ctypes.byref(b))
     assert need > 0, "the case must use scratch"
     ws = None
@@ -52,11 +56,11 @@ def _run(x, g, entry):
     return need
 
 
-def _case(batch, dim, seqlen, seed):
-    x = make_inputs(batch, dim, 16, seqlen, seed=seed, dtype=torch.float32)
+def _case(batch, dim, seqlen, seed, N=16):
+    x = make_inputs(batch, dim, N, seqlen, seed=seed, dtype=torch.float32)
     x = {k: (v.to(DEV) if v is not None else None) for k, v in x.items()}
     out = torch.empty_like(x["delta"])
-    x["xck"] = torch.empty((batch, ss.n_chunks(seqlen), dim, 16), dtype=torch.float32, device=DEV)
+    x["xck"] = torch.empty((batch, ss.n_chunks(seqlen), dim, N), dtype=torch.float32, device=DEV)
     x["y"] = torch.empty_like(out)
     ss.forward_into(x["u"], x["delta"], x["A"], x["B"], x["C"], x["D"], x["delta_bias"], True, out, x["xck"],
                     z=x["z"], y=x["y"])
@@ -82,3 +86,21 @@ def test_noalloc_backward_matches_workspace_backward_twice():
         for k in ("dA", "dB", "dC", "dD", "ddelta_bias"):
             w = want[k]
             assert_close(got[k], w, 1e-5, 1e-5 * float(w.abs().max()), k)
+
+
+# (batch, dim, seqlen, dstate): deterministic sums over state slices, the
+# second call smaller (ragged seqlen)
+DET_CASES = [(2, 256, 1000, 32, 2103), (1, 64, 777, 32, 2104)]
+
+
+def test_noalloc_deterministic_state_slices_twice():
+    for batch, dim, seqlen, N, seed in DET_CASES:
+        print(f"\n[no_alloc] deterministic batch {batch} dim {dim} seqlen {seqlen} dstate {N}", flush=True)
+        sys.stdout.flush()
+        x = _case(batch, dim, seqlen, seed, N=N)
+        want = _grads(x, DEV)
+        need = _run(x, want, "ss_bwd", det=1)
+        got = _grads(x, DEV)
+        assert _run(x, got, "ss_bwd_noalloc", det=1) == need <= nat.NOALLOC_SCRATCH_BYTES
+        for k in want:
+            assert torch.equal(got[k], want[k]), k

@@ -10,7 +10,10 @@ and ddelta_bias are fp32 atomic sums whose order varies between launches,
 so they are compared to 1e-5 relative (well inside the fp32 bar of 1e-3).
 With deterministic sums on dstate 32 (two passes of the fast kernel, one
 per 16-state slice, whose accumulators also sit in the buffer) every
-output matches bit for bit, again on two calls, the second smaller.
+output matches bit for bit, again on two calls, the second smaller.  A
+dstate-32 call whose state-slice passes need more than the buffer runs on
+the general kernel, as ss_bwd without a workspace; it is held to the
+workspace backward at the fp32 bar (1e-3: other kernels, other orders).
 """
 import ctypes
 import sys
@@ -104,3 +107,18 @@ def test_noalloc_deterministic_state_slices_twice():
         assert _run(x, got, "ss_bwd_noalloc", det=1) == need <= nat.NOALLOC_SCRATCH_BYTES
         for k in want:
             assert torch.equal(got[k], want[k]), k
+
+
+def test_noalloc_state_slices_too_large_run_on_the_general_kernel():
+    batch, dim, seqlen, N = 2, 1040, 2048, 32
+    print(f"\n[no_alloc] general kernel fallback batch {batch} dim {dim} seqlen {seqlen} dstate {N}", flush=True)
+    sys.stdout.flush()
+    x = _case(batch, dim, seqlen, 2105, N=N)
+    want = _grads(x, DEV)
+    need = _run(x, want, "ss_bwd")
+    assert need > nat.NOALLOC_SCRATCH_BYTES            # the slice passes' accumulators alone pass 32 MiB
+    got = _grads(x, DEV)
+    _run(x, got, "ss_bwd_noalloc")
+    for k in want:
+        w = want[k]
+        assert_close(got[k], w, 1e-3, 1e-3 * float(w.abs().max()), k)

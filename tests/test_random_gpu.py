@@ -18,7 +18,12 @@ and C, and in about a third of the cases gradient accumulators that hold
 seeded values (no zero_grads: the backward must add to them).  A fourth
 holds dstate 16 with B and C, or one of them, constant, which the fast
 kernels take.
+
+``MAMBA_AMD_RANDOM_SWEEP=N`` adds a sweep of N more seeds over all four
+draws (deterministic sums on about a third of the fast-kernel cases with a
+workspace); without it the sweep is skipped.
 """
+import os
 import random
 import sys
 
@@ -135,6 +140,31 @@ def test_random_general_shapes_against_c_oracle(i):
     print(f"\n[random general] case {i}: {c}", flush=True)
     sys.stdout.flush()
     _run_case(c)
+
+
+SWEEP = int(os.environ.get("MAMBA_AMD_RANDOM_SWEEP", "0"))
+
+
+@pytest.mark.skipif(SWEEP <= 0, reason="set MAMBA_AMD_RANDOM_SWEEP=N for a sweep of N more seeds")
+def test_random_sweep_against_c_oracle():
+    failures = []
+    for i in range(SWEEP):
+        rnd = random.Random(100000 + i)
+        kind = rnd.choice(["base", "slices", "general", "const"])
+        draw = {"base": _draw, "slices": _draw_slices, "general": _draw_general, "const": _draw_const_bc}[kind]
+        c = draw(100000 + i)
+        fast = (c["dstate"] % 16 == 0 and c["var_B"] and c["var_C"] and c["dim"] % 16 == 0
+                and (c["dim"] // c["n_groups"]) % 16 == 0)
+        if fast and c["workspace"] == "auto" and rnd.random() < 0.35:
+            c["det"] = True
+        try:
+            _run_case(c)
+        except AssertionError as e:
+            failures.append(f"seed {100000 + i} ({kind}): {c}: {str(e)[:200]}")
+            print(f"\n[random sweep] FAIL {failures[-1]}", flush=True)
+        if i % 100 == 99:
+            print(f"\n[random sweep] {i + 1}/{SWEEP} cases, {len(failures)} failures", flush=True)
+    assert not failures, "\n".join(failures[:10])
 
 
 def _run_case(c):

@@ -48,8 +48,15 @@ MiB (torch's copy kernel); under ``rocprofv3 --pmc FETCH_SIZE`` /
 ``WRITE_SIZE`` it gives the factor between those counters and bytes actually
 read / written, which scales the scan kernels' counters into ``traffic``.
 
+``--cpu-table`` instead prints one JSON line for each of the three scan
+configurations (2 x 64 x 256 fp32, the 8 x 1536 x 2048 fp32 benchmark, 4 x
+5120 x 8192 bf16 I/O): the GPU step beside the float64 C oracle and the
+PyTorch oracle ``selective_scan_ref`` on this host's cores (a markdown table
+of the same on stderr).
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--no-cpu]
        python bench.py --calibrate-copy 1024
+       python bench.py --cpu-table
 """
 import argparse
 import json
@@ -457,7 +464,7 @@ def algorithmic_bytes(batch, dim, dstate, seqlen, s, groups=1):
     return fwd, bwd
 
 
-def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
+def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0, seed=1001):
     """Times the C restatement of the reference's algorithm (oracle/ss_oracle.c:
     the reference kernels' arithmetic in float64, plain loops) forward +
     backward on this host's cores: one task per (batch row, 96-channel slice),
@@ -470,9 +477,10 @@ def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
     from oracle import c_oracle
 
     threads = cpu_threads()
-    slice_ch = 96 if dim % 96 == 0 else dim
+    # tasks of at most 96 channels (a divisor of dim when there is one)
+    slice_ch = next((k for k in (96, 80, 64, 48, 32, 16) if dim % k == 0), dim)
     x = {k: (v.double() if v is not None else None)
-         for k, v in synthetic_inputs(batch, dim, dstate, seqlen, seed=1001, dtype=torch.float32).items()}
+         for k, v in synthetic_inputs(batch, dim, dstate, seqlen, seed=seed, dtype=torch.float32).items()}
 
     def task(bi, lo):
         hi = lo + slice_ch
@@ -513,7 +521,7 @@ def cpu_baseline(dtype_name, batch, dim, seqlen, dstate, max_seconds=30.0):
     }
 
 
-def cpu_ref_sample(dtype_name, seqlen, dstate, batch=1, dim=96, reps=3):
+def cpu_ref_sample(dtype_name, seqlen, dstate, batch=1, dim=96, reps=3, seed=1001):
     """Times the PyTorch oracle ``selective_scan_ref`` (a per-step loop in
     fp32 with autograd for the backward) on this host's cores, forward
     (no_grad) and forward + backward, on a bounded sample: `batch` rows of
@@ -527,7 +535,7 @@ def cpu_ref_sample(dtype_name, seqlen, dstate, batch=1, dim=96, reps=3):
 
     threads = cpu_threads()
     torch.set_num_threads(threads)
-    x = synthetic_inputs(batch, dim, dstate, seqlen, seed=1001, dtype=torch.float32)
+    x = synthetic_inputs(batch, dim, dstate, seqlen, seed=seed, dtype=torch.float32)
     names = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
     g = {k: x[k].clone().requires_grad_(True) for k in names}
     args = lambda: (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"])
@@ -585,6 +593,77 @@ def time_copy(mib, reps=5):
     return n * 4, ms
 
 
+# The three scan configurations with the CPU baselines beside the GPU step:
+# (label, batch, dim, dstate, seqlen, dtype, seed, (batch, dim, seqlen) of
+# the selective_scan_ref sample or None for the whole configuration; its
+# per-step autograd graph makes 8192 steps take minutes, so the bf16 case is
+# sampled over its first 2048 steps)
+CPU_TABLE = [
+    ("2 x 64 x 256, fp32 (the CPU-runnable case)", 2, 64, 16, 256, "float32", 1000, None),
+    ("8 x 1536 x 2048, fp32 (the benchmark)", 8, 1536, 16, 2048, "float32", 1001, (1, 96, 2048)),
+    ("4 x 5120 x 8192, bf16 I/O", 4, 5120, 16, 8192, "bfloat16", 1002, (1, 96, 2048)),
+]
+
+
+def gpu_step_ms(batch, dim, dstate, seqlen, dtype_name, seed, steps, warmup):
+    """ms per selective_scan_fn forward + autograd backward on cuda:0 (the
+    step ``value`` times), inputs resident in HBM."""
+    import torch
+    from mamba_amd.ops.selective_scan_interface import selective_scan_fn
+
+    dev = torch.device("cuda:0")
+    x = synthetic_inputs(batch, dim, dstate, seqlen, seed=seed, dtype=getattr(torch, dtype_name))
+    names = ("u", "delta", "A", "B", "C", "D", "z", "delta_bias")
+    g = {k: x[k].to(dev).requires_grad_(True) for k in names}
+    dout = x["dout"].to(dev)
+
+    def step():
+        out = selective_scan_fn(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], z=g["z"],
+                                delta_bias=g["delta_bias"], delta_softplus=True)
+        return torch.autograd.grad(out, [g[k] for k in names], dout)
+
+    warm_up(step, warmup)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_cpu_table(args):
+    """One JSON line per scan configuration: the GPU step beside the float64 C
+    oracle (the whole configuration, or its first batch rows past 30 s) and
+    the PyTorch oracle selective_scan_ref (whole, or a sample of 96 channels
+    of one batch row), all GB/s by the same byte formula; a markdown table of
+    the same on stderr."""
+    rows = []
+    for label, batch, dim, dstate, seqlen, dtype_name, seed, sample in CPU_TABLE:
+        s = 2 if dtype_name != "float32" else 4
+        fwd_b, bwd_b = algorithmic_bytes(batch, dim, dstate, seqlen, s)
+        print(f"[bench] cpu table: {label}", file=sys.stderr, flush=True)
+        ms = gpu_step_ms(batch, dim, dstate, seqlen, dtype_name, seed, args.steps, args.warmup)
+        c = cpu_baseline(dtype_name, batch, dim, seqlen, dstate, seed=seed)
+        rb, rd, rl = sample if sample else (batch, dim, seqlen)
+        r = cpu_ref_sample(dtype_name, rl, dstate, batch=rb, dim=rd, seed=seed)
+        line = {"config": label, "batch": batch, "dim": dim, "dstate": dstate, "seqlen": seqlen,
+                "io_dtype": dtype_name, "gpu_ms_per_step": round(ms, 4),
+                "gpu_gbs": round((fwd_b + bwd_b) / (ms * 1e-3) / 1e9, 2),
+                "gpu_pct_hbm_peak": round(100.0 * (fwd_b + bwd_b) / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+                "c_oracle": c, "selective_scan_ref": dict(r, sample_shape=f"batch {rb} x dim {rd} x seqlen {rl}")}
+        print(json.dumps(line), flush=True)
+        rows.append(line)
+    print("| configuration | GPU step (ms) | GPU GB/s (% of 8 TB/s) | C oracle (s, GB/s, threads) "
+          "| selective_scan_ref fwd / fwd+bwd (s, sample, GB/s) |", file=sys.stderr)
+    print("|---|---|---|---|---|", file=sys.stderr)
+    for ln in rows:
+        c, r = ln["c_oracle"], ln["selective_scan_ref"]
+        print(f"| {ln['config']} | {ln['gpu_ms_per_step']:.4f} | {ln['gpu_gbs']:.1f} ({ln['gpu_pct_hbm_peak']:.2f} %) "
+              f"| {c['seconds']:.3f} s, {c['value']:.3f} GB/s, {c['cores']} | {r['fwd_s']:.3f} / "
+              f"{r['fwd_bwd_s']:.3f} s, {r['sample_shape']}, {r['value']:.4f} GB/s |", file=sys.stderr, flush=True)
+
+
 def calibrate_copy(mib, reps=5):
     """Copies `mib` MiB device to device `reps` times; prints one JSON line."""
     nbytes, ms = time_copy(mib, reps)
@@ -608,6 +687,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-ref-order", action="store_true",
                     help="block / LM workloads: skip timing the reference's op order")
+    ap.add_argument("--cpu-table", action="store_true",
+                    help="only the three scan configurations with the CPU baselines beside the GPU step")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only time a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -625,6 +706,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.cpu_table:
+        bench_cpu_table(args)
         return
     if args.workload in MODEL_WORKLOADS:
         bench_model(args)

@@ -999,6 +999,9 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
         float dy = kZ ? cur.o * cur.z * sigmoidf_(cur.z) : cur.o;
         dsum += dt;
         dpp_sources_ready(dt, dy, dsum);
+        // the carry's chain at raised wave priority (as in the full backward;
+        // 1 x 1536 x 32768 bf16 backward with segments 862 -> 834 us)
+        __builtin_amdgcn_s_setprio(1);
         float as[kT];
         static_for<kT>([&](auto K) {
             constexpr int k = decltype(K)::value;
@@ -1010,6 +1013,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_bwd_seg_carry(const BwdParams 
             bfmac<k>(gv, dy, Cq[k]);             // g_t = a_{t+1} g_{t+1} + dy_t C_t
             ga = gv * as[k];
         });
+        __builtin_amdgcn_s_setprio(0);
         stage(P, buf ^ 1);
     }
     const int64_t si = (b * p.nseg + seg) * p.dim + c;

@@ -242,7 +242,6 @@ int check_bwd(const ss_bwd_args* a, bool* empty) {
 ss::BwdParams make_bwd_params(const ss_bwd_args* a) {
     ss::BwdParams p{};
     p.f = make_fwd_params(&a->f);
-    p.wg_reduce = (p.f.dpg % ss::kChPerWG) == 0;
     p.bc_ld = a->f.seqlen;
     {
         const size_t es = elem_size(a->f.itype);

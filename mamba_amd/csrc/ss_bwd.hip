@@ -61,6 +61,13 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     const bool cval = c_raw < p.dim;
     const int64_t c = cval ? c_raw : p.dim - 1;
     const int64_t g = c / p.dpg;
+    // the workgroup's 16 channels (those past dim count as the last one,
+    // and add exact zeros) in one group: dB / dC are summed over them in LDS
+    // and added once per (state, step); otherwise every lane adds its own.
+    // Uniform over the workgroup, like the barriers it guards.
+    const int64_t wc0 = (blk % nblk) * kChPerWG;
+    const int64_t wc1 = wc0 + kChPerWG - 1 < p.dim ? wc0 + kChPerWG - 1 : p.dim - 1;
+    const bool wg_reduce = wc0 / p.dpg == wc1 / p.dpg;
     const int N = int(p.dstate);
     const int64_t L = p.seqlen;
     const bool var_B = kVarBC || p.var_B;
@@ -242,7 +249,7 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
                 *reinterpret_cast<float4*>(tr_s1 + o) = make_float4(s1p[0], s1p[1], s1p[2], s1p[3]);
                 *reinterpret_cast<float4*>(tr_s2 + o) = make_float4(s2p[0], s2p[1], s2p[2], s2p[3]);
                 if (var_B) {
-                    if (q.wg_reduce) {
+                    if (wg_reduce) {
                         *reinterpret_cast<float4*>(ch_dB + o) = make_float4(dBp[0], dBp[1], dBp[2], dBp[3]);
                     } else if (cval && nv) {
 #pragma unroll
@@ -253,7 +260,7 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
                     dBq += (dBp[0] + dBp[1]) + (dBp[2] + dBp[3]);
                 }
                 if (var_C) {
-                    if (q.wg_reduce) {
+                    if (wg_reduce) {
                         *reinterpret_cast<float4*>(ch_dC + o) = make_float4(dCp[0], dCp[1], dCp[2], dCp[3]);
                     } else if (cval && nv) {
 #pragma unroll
@@ -283,7 +290,7 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
             s2_red += b0 + b1;
 
             // sums over the workgroup's 16 channels, one global add per (state, step)
-            if (q.wg_reduce && (var_B || var_C)) {
+            if (wg_reduce && (var_B || var_C)) {
                 __syncthreads();
                 const int tid = threadIdx.x;
                 const int nl = tid >> 4, k = tid & 15;

@@ -62,7 +62,6 @@ inline int64_t fwd_seg_bytes(const FwdParams& p, int nseg) {
 
 struct BwdParams {
     FwdParams f;
-    int32_t wg_reduce;                        // all channels of a workgroup share one group
     int64_t do_bs, do_ds, du_bs, du_ds, dd_bs, dd_ds, dz_bs, dz_ds;
     const void* dout; void* du; void* ddelta; void* dz;
     float* dA; float* dB; float* dC; float* dD; float* ddelta_bias;

@@ -142,6 +142,27 @@ def test_random_general_shapes_against_c_oracle(i):
     _run_case(c)
 
 
+# channel blocks of 16 on the general kernels: a block with padding channels
+# past dim in one group (summed over the block in LDS), blocks that straddle
+# two groups (every lane adds its own dB / dC), and a wide row of 1000
+# channels in one group
+CHANNEL_CASES = [
+    dict(batch=2, dim=40, dstate=16, seqlen=300, n_groups=1, dtype=torch.float32),
+    dict(batch=2, dim=72, dstate=16, seqlen=211, n_groups=3, dtype=torch.float32),
+    dict(batch=1, dim=1000, dstate=16, seqlen=129, n_groups=1, dtype=torch.bfloat16),
+    dict(batch=1, dim=120, dstate=20, seqlen=97, n_groups=5, dtype=torch.float16),
+]
+
+
+@pytest.mark.parametrize("i", range(len(CHANNEL_CASES)))
+def test_general_kernels_channel_blocks_against_c_oracle(i):
+    c = dict(CHANNEL_CASES[i], var_B=True, var_C=True, has_z=True, has_D=True, has_bias=True, softplus=True,
+             pad=0, workspace="auto", seed=9960 + i, accumulate=i % 2 == 1)
+    print(f"\n[random channel blocks] case {i}: {c}", flush=True)
+    sys.stdout.flush()
+    _run_case(c)
+
+
 SWEEP = int(os.environ.get("MAMBA_AMD_RANDOM_SWEEP", "0"))
 
 

@@ -542,11 +542,6 @@ __global__ __launch_bounds__(kThreads, (fwd_late_b<IT, kAcc>() ? 4 : 3)) void ss
             // states of the previous chunk, written by this row last chunk
             float ys[kT];
             read_tile(ys);
-            // the decay factors and the state recurrence at raised wave
-            // priority, the C reads and the staging at normal (measured: bf16
-            // batch 16 x dim 1536 x seqlen 2048 258 -> 254 us, fp32 and batch
-            // 4 x dim 5120 x seqlen 8192 -0.5 %, same bits)
-            __builtin_amdgcn_s_setprio(1);
             // decay factors of all 16 steps first: they do not depend on h, so
             // the exp latency stays off the h chain
             float a[kT];
@@ -591,7 +586,6 @@ __global__ __launch_bounds__(kThreads, (fwd_late_b<IT, kAcc>() ? 4 : 3)) void ss
             for (int m = 0; m < 4; ++m)
                 *reinterpret_cast<float4*>(yrow + r * 16 + 4 * (m ^ ((r >> 1) & 3))) =
                     make_float4(yp[4 * m], yp[4 * m + 1], yp[4 * m + 2], yp[4 * m + 3]);
-            __builtin_amdgcn_s_setprio(0);
             // C of step r of this chunk, for its sum one chunk later (read
             // now: this buffer is not restaged before the next barrier)
             if constexpr (kVC) {

@@ -61,13 +61,21 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     const bool cval = c_raw < p.dim;
     const int64_t c = cval ? c_raw : p.dim - 1;
     const int64_t g = c / p.dpg;
-    // the workgroup's 16 channels (those past dim count as the last one,
-    // and add exact zeros) in one group: dB / dC are summed over them in LDS
-    // and added once per (state, step); otherwise every lane adds its own.
-    // Uniform over the workgroup, like the barriers it guards.
+    // the workgroup's first channel: dB / dC are summed over its 16 channels
+    // in LDS, one run of channels per group, and added once per (state,
+    // step) and group (channels past dim count as the last one: they add
+    // exact zeros)
     const int64_t wc0 = (blk % nblk) * kChPerWG;
-    const int64_t wc1 = wc0 + kChPerWG - 1 < p.dim ? wc0 + kChPerWG - 1 : p.dim - 1;
-    const bool wg_reduce = wc0 / p.dpg == wc1 / p.dpg;
+    // bit ch: channel ch is the last of its group in the workgroup (uniform:
+    // kept in a scalar register, so the branches on it are scalar)
+    uint32_t run_end_v = 1u << (kChPerWG - 1);
+    for (int ch = 0; ch < kChPerWG - 1; ++ch) {
+        const int64_t nc = wc0 + ch + 1;
+        if (nc < p.dim && nc % p.dpg == 0) run_end_v |= 1u << ch;
+    }
+    const uint32_t run_end = __builtin_amdgcn_readfirstlane(run_end_v);
+    const bool one_group = run_end == 1u << (kChPerWG - 1);
+    const int64_t g0 = wc0 / p.dpg;
     const int N = int(p.dstate);
     const int64_t L = p.seqlen;
     const bool var_B = kVarBC || p.var_B;
@@ -99,10 +107,8 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
     // x: (batch, chunk, dim, dstate)
     const float* xrow = p.x + (b * p.n_chunks * p.dim + c) * N;
     const int64_t x_chunk_stride = p.dim * N;
-    // fp32 gradient rows of variable B / C for this (batch, group): (dstate, seqlen)
+    // fp32 gradient rows of variable B / C: (batch, group, dstate, seqlen)
     const int64_t G = p.dim / p.dpg;
-    float* dBrow = q.dB + (b * G + g) * int64_t(N) * L;
-    float* dCrow = q.dC + (b * G + g) * int64_t(N) * L;
 
     const float Dv = p.D ? p.D[c] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[c] : 0.f;
@@ -249,24 +255,12 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
                 *reinterpret_cast<float4*>(tr_s1 + o) = make_float4(s1p[0], s1p[1], s1p[2], s1p[3]);
                 *reinterpret_cast<float4*>(tr_s2 + o) = make_float4(s2p[0], s2p[1], s2p[2], s2p[3]);
                 if (var_B) {
-                    if (wg_reduce) {
-                        *reinterpret_cast<float4*>(ch_dB + o) = make_float4(dBp[0], dBp[1], dBp[2], dBp[3]);
-                    } else if (cval && nv) {
-#pragma unroll
-                        for (int ki = 0; ki < 4; ++ki)
-                            if (4 * kg + ki < nval) atomicAdd(dBrow + n * L + t0 + 4 * kg + ki, dBp[ki]);
-                    }
+                    *reinterpret_cast<float4*>(ch_dB + o) = make_float4(dBp[0], dBp[1], dBp[2], dBp[3]);
                 } else {
                     dBq += (dBp[0] + dBp[1]) + (dBp[2] + dBp[3]);
                 }
                 if (var_C) {
-                    if (wg_reduce) {
-                        *reinterpret_cast<float4*>(ch_dC + o) = make_float4(dCp[0], dCp[1], dCp[2], dCp[3]);
-                    } else if (cval && nv) {
-#pragma unroll
-                        for (int ki = 0; ki < 4; ++ki)
-                            if (4 * kg + ki < nval) atomicAdd(dCrow + n * L + t0 + 4 * kg + ki, dCp[ki]);
-                    }
+                    *reinterpret_cast<float4*>(ch_dC + o) = make_float4(dCp[0], dCp[1], dCp[2], dCp[3]);
                 } else {
                     dCq += (dCp[0] + dCp[1]) + (dCp[2] + dCp[3]);
                 }
@@ -289,8 +283,9 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
             s1_red += a0 + a1;
             s2_red += b0 + b1;
 
-            // sums over the workgroup's 16 channels, one global add per (state, step)
-            if (wg_reduce && (var_B || var_C)) {
+            // sums over the workgroup's 16 channels, one global add per (state,
+            // step) and group of them
+            if (var_B || var_C) {
                 __syncthreads();
                 const int tid = threadIdx.x;
                 const int nl = tid >> 4, k = tid & 15;
@@ -301,14 +296,29 @@ __global__ __launch_bounds__(kThreads, 2) void ss_bwd_kernel(const BwdParams q) 
                     const bool use = arr == 0 ? var_B : var_C;
                     if (!use) continue;
                     const float* src = chb + arr * kChArr + ridx;
-                    float s0 = 0.f, s1 = 0.f;
+                    float* dst = (arr == 0 ? q.dB : q.dC) + (int64_t(ng) * L + t0 + k);
+                    const bool add = ng < N && k < nval;
+                    if (one_group) {
+                        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-                    for (int ch = 0; ch < kChPerWG; ch += 2) {
-                        s0 += src[ch * kT * kT];
-                        s1 += src[(ch + 1) * kT * kT];
+                        for (int ch = 0; ch < kChPerWG; ch += 2) {
+                            s0 += src[ch * kT * kT];
+                            s1 += src[(ch + 1) * kT * kT];
+                        }
+                        if (add) atomicAdd(dst + (b * G + g0) * int64_t(N) * L, s0 + s1);
+                    } else {
+                        float sum = 0.f;
+                        int64_t gc = g0;
+#pragma unroll
+                        for (int ch = 0; ch < kChPerWG; ++ch) {
+                            sum += src[ch * kT * kT];
+                            if ((run_end >> ch) & 1u) {
+                                if (add) atomicAdd(dst + (b * G + gc) * int64_t(N) * L, sum);
+                                sum = 0.f;
+                                ++gc;
+                            }
+                        }
                     }
-                    float* dst = arr == 0 ? dBrow : dCrow;
-                    if (ng < N && k < nval) atomicAdd(dst + ng * L + t0 + k, s0 + s1);
                 }
                 __syncthreads();
             }

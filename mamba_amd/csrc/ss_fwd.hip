@@ -706,7 +706,7 @@ __global__ __launch_bounds__(kThreads, 3) void ss_fwd_seg_state(const FwdParams 
                     Bq[4 * i] = Bq[4 * i + 1] = Bq[4 * i + 2] = Bq[4 * i + 3] = bconst;
                 }
             }
-            // the recurrence at raised wave priority (as in the full forward;
+            // the recurrence at raised wave priority (unlike the full forward;
             // 1 x 1536 x 32768 bf16 forward with segments 422 -> 408 us)
             __builtin_amdgcn_s_setprio(1);
             float a[kT];

@@ -149,6 +149,13 @@ ss::FwdParams make_fwd_params(const ss_fwd_args* a) {
     p.z_end = seq_end(p.z, B, D, L, p.z_bs, p.z_ds, es);
     p.o_end = seq_end(p.out, B, D, L, p.o_bs, p.o_ds, es);
     p.y_end = seq_end(p.y, B, D, L, p.y_bs, p.y_ds, es);
+    // out / y with every row on a 16-byte boundary: the fast forward stores
+    // them non-temporally (fp32 batch 8 x dim 1536 x seqlen 2048 forward
+    // -2 %); on rows off that boundary the same stores cost +24 % (seqlen
+    // 2047 184 -> 229 us), so those keep the default policy
+    const int64_t per16 = int64_t(16 / es);
+    p.store_nt = aligned(p.out, 16) && p.o_bs % per16 == 0 && p.o_ds % per16 == 0 &&
+                 (!p.y || (aligned(p.y, 16) && p.y_bs % per16 == 0 && p.y_ds % per16 == 0));
     // variable B / C: (batch, groups, dstate, seqlen)
     p.B_end = p.var_B && N > 0 ? seq_end(p.B, B, G, L, p.B_bs, p.B_gs, es) + (N - 1) * p.B_ns * int64_t(es) : 0;
     p.C_end = p.var_C && N > 0 ? seq_end(p.C, B, G, L, p.C_bs, p.C_gs, es) + (N - 1) * p.C_ns * int64_t(es) : 0;

@@ -426,14 +426,20 @@ __global__ __launch_bounds__(kThreads, (fwd_late_b<IT, kAcc>() ? 4 : 3)) void ss
         y.y = __builtin_fmaf(Dv, pu.y, y.y);
         y.z = __builtin_fmaf(Dv, pu.z, y.z);
         y.w = __builtin_fmaf(Dv, pu.w, y.w);
+        // (non-temporal out / y stores only for 16-byte aligned rows, see
+        // FwdParams::store_nt; the branch is uniform)
         if constexpr (kZ) {
-            bstore4<IT, kStoreNT>(make_rsrc_in(p.y, y_off + int64_t(sc) * kSC * es64, y_end), oy, y);
+            const rsrc_t Ry = make_rsrc_in(p.y, y_off + int64_t(sc) * kSC * es64, y_end);
+            if (p.store_nt) bstore4<IT, kStoreNT>(Ry, oy, y);
+            else bstore4<IT, kStoreDefault>(Ry, oy, y);
             y.x *= pz.x * sigmoidf_(pz.x);
             y.y *= pz.y * sigmoidf_(pz.y);
             y.z *= pz.z * sigmoidf_(pz.z);
             y.w *= pz.w * sigmoidf_(pz.w);
         }
-        bstore4<IT, kStoreNT>(make_rsrc_in(p.out, o_off + int64_t(sc) * kSC * es64, p.o_end), oo, y);
+        const rsrc_t Ro = make_rsrc_in(p.out, o_off + int64_t(sc) * kSC * es64, p.o_end);
+        if (p.store_nt) bstore4<IT, kStoreNT>(Ro, oo, y);
+        else bstore4<IT, kStoreDefault>(Ro, oo, y);
     };
     // as finish_super for the tail super-chunk: element stores of its lt steps
     auto finish_super_tail = [&](int sc) {
@@ -458,10 +464,10 @@ __global__ __launch_bounds__(kThreads, (fwd_late_b<IT, kAcc>() ? 4 : 3)) void ss
             if (4 * r + i < lt) {
                 float o = yv[i];
                 if constexpr (kZ) {
-                    bstore<IT, kStoreNT>(Ryt, oy + uint32_t(i) * es, 0, o);
+                    bstore<IT, kStoreDefault>(Ryt, oy + uint32_t(i) * es, 0, o);
                     o *= zv[i] * sigmoidf_(zv[i]);
                 }
-                bstore<IT, kStoreNT>(Ro, oo + uint32_t(i) * es, 0, o);
+                bstore<IT, kStoreDefault>(Ro, oo + uint32_t(i) * es, 0, o);
             }
         }
     };

@@ -15,6 +15,7 @@ struct FwdParams {
     int64_t n_chunks;
     int32_t var_B, var_C, has_z, softplus;
     int32_t vec_B, vec_C;                     // 16-byte aligned rows of variable B / C (general kernels)
+    int32_t store_nt;                         // out / y rows all 16-byte aligned: non-temporal stores (fast forward)
     int64_t u_bs, u_ds, dl_bs, dl_ds, z_bs, z_ds, o_bs, o_ds, y_bs, y_ds;
     int64_t A_ds, A_ns;
     int64_t B_bs, B_gs, B_ns, C_bs, C_gs, C_ns;

@@ -10,10 +10,12 @@
 // Layout: a workgroup of 256 threads covers 256 VW consecutive steps of one
 // (batch, channel) row (grid x: rows, grid y: segments); each thread VW
 // consecutive steps, one 16-byte vector: VW = 4 for fp32, 8 for 16-bit
-// types when rows are 8-element aligned (4 when they are only 4-element
-// aligned).  Rows that are not vector aligned are read element by element
-// (4 steps per thread).  The 3-step halo before a thread's steps comes from
-// the previous vector (an L1 / L2 hit).
+// types.  The vectors need only element alignment (this target accesses
+// memory in its unaligned mode: 16-byte loads and stores at any element
+// offset), so rows at any offset and of any length keep them; the one
+// vector that straddles a row's end is read and written element by element.
+// The 3-step halo before a thread's steps comes from the previous vector (an
+// L1 / L2 hit).
 // The op is HBM-bound: one read of x, one write of out (forward); reads of
 // x and dout, one write of dx, and per-workgroup sums of dweight / dbias
 // (backward).
@@ -32,7 +34,8 @@ constexpr int kCT = 256;            // threads per workgroup
 
 struct ConvParams {
     int64_t batch, dim, seqlen;
-    int32_t width, has_bias, silu, vec;         // vec: elements per vector access (4 or 8), 0 for element access
+    int32_t width, has_bias, silu;
+    int32_t exact;                               // seqlen a multiple of the vector's steps
     int64_t x_bs, x_ds, o_bs, o_ds, w_ds, w_ks;
     int64_t do_bs, do_ds, dx_bs, dx_ds;
     const void* x; const float* w; const float* bias; void* out;
@@ -48,29 +51,35 @@ __device__ __forceinline__ float ld(const IT* p, int64_t i, int64_t n) {
     return (i >= 0 && i < n) ? v : 0.f;
 }
 
-// VW consecutive elements starting at i (a multiple of VW, VW-element
-// aligned row, VW * sizeof(IT) <= 16); zeros outside [0, n) (n is a multiple
-// of VW on this path)
-template <typename IT, int VW>
+// 16-byte vectors with element alignment only
+typedef float f32x4_u __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4_u __attribute__((ext_vector_type(4), aligned(2)));
+
+// VW consecutive elements starting at i (a multiple of VW; 16 bytes: VW = 4
+// fp32, 8 16-bit; any element offset); zeros outside [0, n).  kExact: n is
+// a multiple of VW, so each vector lies wholly inside or outside the row
+// (one load, at a clamped index when outside); otherwise a vector that
+// straddles the row's end is read element by element.
+template <typename IT, int VW, bool kExact>
 __device__ __forceinline__ void ldv(const IT* p, int64_t i, int64_t n, float (&o)[VW]) {
+    static_assert(VW * sizeof(IT) == 16, "16-byte vectors");
     const bool in = i >= 0 && i < n;
+    if constexpr (!kExact) {
+        if (in && i + VW > n) {
+#pragma unroll
+            for (int k = 0; k < VW; ++k) o[k] = ld<IT>(p, i + k, n);
+            return;
+        }
+    }
     const int64_t c = in ? i : 0;
     if constexpr (sizeof(IT) == 4) {
-        static_assert(VW == 4, "fp32 rows: 4 elements per vector");
-        const float4 v = *reinterpret_cast<const float4*>(p + c);
+        const f32x4_u v = *reinterpret_cast<const f32x4_u*>(p + c);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     } else {
-        uint32_t w[VW / 2];
-        if constexpr (VW == 8) {
-            const uint4 v = *reinterpret_cast<const uint4*>(p + c);
-            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-        } else {
-            static_assert(VW == 4, "16-bit rows: 4 or 8 elements per vector");
-            const uint2 v = *reinterpret_cast<const uint2*>(p + c);
-            w[0] = v.x; w[1] = v.y;
-        }
+        const u32x4_u v = *reinterpret_cast<const u32x4_u*>(p + c);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int k = 0; k < VW / 2; ++k) {
+        for (int k = 0; k < 4; ++k) {
             if constexpr (__is_same(IT, bf16_t)) {
                 o[2 * k] = __uint_as_float(w[k] << 16);
                 o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
@@ -86,10 +95,20 @@ __device__ __forceinline__ void ldv(const IT* p, int64_t i, int64_t n, float (&o
     }
 }
 
-template <typename IT, int VW>
-__device__ __forceinline__ void stv(IT* p, const float (&v)[VW]) {
+// v into elements i .. i + VW - 1 of a row of n (0 <= i < n): one 16-byte
+// store, or (not kExact) element stores of those below n when the vector
+// straddles the row's end
+template <typename IT, int VW, bool kExact>
+__device__ __forceinline__ void stv(IT* p, int64_t i, int64_t n, const float (&v)[VW]) {
+    static_assert(VW * sizeof(IT) == 16, "16-byte vectors");
+    if (!kExact && i + VW > n) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k)
+            if (i + k < n) io<IT>::store(p + i + k, v[k]);
+        return;
+    }
     if constexpr (sizeof(IT) == 4) {
-        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<f32x4_u*>(p + i) = f32x4_u{v[0], v[1], v[2], v[3]};
     } else {
         uint32_t o[VW / 2];
 #pragma unroll
@@ -101,34 +120,25 @@ __device__ __forceinline__ void stv(IT* p, const float (&v)[VW]) {
                        (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[2 * k + 1]))) << 16);
             }
         }
-        if constexpr (VW == 8) *reinterpret_cast<uint4*>(p) = make_uint4(o[0], o[1], o[2], o[3]);
-        else *reinterpret_cast<uint2*>(p) = make_uint2(o[0], o[1]);
+        *reinterpret_cast<u32x4_u*>(p + i) = u32x4_u{o[0], o[1], o[2], o[3]};
     }
 }
 
-// x[t0 - VW .. t0 + VW * (1 + extra) - 1] into xs (VW = 0: element loads
-// of the same window with VW = 4)
-template <typename IT, int VW, int kExtra>
-__device__ __forceinline__ void load_window(const IT* row, int64_t t0, int64_t L,
-                                            float (&xs)[(VW ? VW : 4) * (2 + kExtra)]) {
-    constexpr int V = VW ? VW : 4;
-    if constexpr (VW != 0) {
+// x[t0 - VW .. t0 + VW * (1 + extra) - 1] into xs
+template <typename IT, int VW, bool kExact, int kExtra>
+__device__ __forceinline__ void load_window(const IT* row, int64_t t0, int64_t L, float (&xs)[VW * (2 + kExtra)]) {
 #pragma unroll
-        for (int q = 0; q < 2 + kExtra; ++q) {
-            float v[VW];
-            ldv<IT, VW>(row, t0 - VW + VW * q, L, v);
+    for (int q = 0; q < 2 + kExtra; ++q) {
+        float v[VW];
+        ldv<IT, VW, kExact>(row, t0 - VW + VW * q, L, v);
 #pragma unroll
-            for (int k = 0; k < VW; ++k) xs[VW * q + k] = v[k];
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < V * (2 + kExtra); ++i) xs[i] = ld<IT>(row, t0 - V + i, L);
+        for (int k = 0; k < VW; ++k) xs[VW * q + k] = v[k];
     }
 }
 
-template <typename IT, int VW>
+template <typename IT, int VW, bool kExact>
 __global__ __launch_bounds__(kCT) void conv1d_fwd_kernel(const ConvParams p) {
-    constexpr int V = VW ? VW : 4;                      // steps per thread
+    constexpr int V = VW;                               // steps per thread
     const int64_t row_id = blockIdx.x;                  // b * dim + d
     const int64_t b = row_id / p.dim, d = row_id % p.dim;
     const int64_t t0 = int64_t(blockIdx.y) * (kCT * V) + threadIdx.x * V;
@@ -141,7 +151,7 @@ __global__ __launch_bounds__(kCT) void conv1d_fwd_kernel(const ConvParams p) {
     const float bias = p.has_bias ? p.bias[d] : 0.f;
 
     float xs[2 * V];                                    // x[t0 - V .. t0 + V - 1]
-    load_window<IT, VW, 0>(xr, t0, p.seqlen, xs);
+    load_window<IT, VW, kExact, 0>(xr, t0, p.seqlen, xs);
     float o[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) {
@@ -150,18 +160,12 @@ __global__ __launch_bounds__(kCT) void conv1d_fwd_kernel(const ConvParams p) {
         for (int k = 0; k < 4; ++k) acc = __builtin_fmaf(w[k], xs[V + i - 3 + k], acc);
         o[i] = p.silu ? acc * sigmoidf_(acc) : acc;
     }
-    if constexpr (VW != 0) {
-        stv<IT, VW>(orow + t0, o);
-    } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i)
-            if (t0 + i < p.seqlen) io<IT>::store(orow + t0 + i, o[i]);
-    }
+    stv<IT, VW, kExact>(orow, t0, p.seqlen, o);
 }
 
-template <typename IT, int VW>
+template <typename IT, int VW, bool kExact>
 __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
-    constexpr int V = VW ? VW : 4;                      // steps per thread
+    constexpr int V = VW;                               // steps per thread
     __shared__ float red[kCT / 64][5];
     const int64_t row_id = blockIdx.x;
     const int64_t b = row_id / p.dim, d = row_id % p.dim;
@@ -178,19 +182,16 @@ __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
 
     // x[t0 - V .. t0 + 2 V - 1], dout[t0 .. t0 + 2 V - 1]
     float xs[3 * V];
-    load_window<IT, VW, 1>(xr, tl, p.seqlen, xs);
+    load_window<IT, VW, kExact, 1>(xr, tl, p.seqlen, xs);
     float gs[2 * V];
-    if constexpr (VW != 0) {
+    {
         float v[VW];
-        ldv<IT, VW>(gr, tl, p.seqlen, v);
+        ldv<IT, VW, kExact>(gr, tl, p.seqlen, v);
 #pragma unroll
         for (int k = 0; k < VW; ++k) gs[k] = v[k];
-        ldv<IT, VW>(gr, tl + VW, p.seqlen, v);
+        ldv<IT, VW, kExact>(gr, tl + VW, p.seqlen, v);
 #pragma unroll
         for (int k = 0; k < VW; ++k) gs[VW + k] = v[k];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 2 * V; ++i) gs[i] = ld<IT>(gr, tl + i, p.seqlen);
     }
     // dpre at t0 .. t0 + 2 V - 1 (zero beyond seqlen: gs is zero there)
     float dp[2 * V];
@@ -215,15 +216,7 @@ __global__ __launch_bounds__(kCT) void conv1d_bwd_kernel(const ConvParams p) {
         for (int k = 0; k < 4; ++k) acc = __builtin_fmaf(w[k], dp[i + 3 - k], acc);
         dxo[i] = acc;
     }
-    if (live) {
-        if constexpr (VW != 0) {
-            stv<IT, VW>(dxr + t0, dxo);
-        } else {
-#pragma unroll
-            for (int i = 0; i < V; ++i)
-                if (t0 + i < p.seqlen) io<IT>::store(dxr + t0 + i, dxo[i]);
-        }
-    }
+    if (live) stv<IT, VW, kExact>(dxr, t0, p.seqlen, dxo);
     // dw[k] += sum_t dpre[t] * x[t - 3 + k], dbias += sum_t dpre[t], over this thread's V steps
     float part[5];
 #pragma unroll
@@ -291,30 +284,25 @@ __global__ __launch_bounds__(256) void conv1d_bwd_reduce(const float* __restrict
     }
 }
 
-template <typename IT, int VW>
+template <typename IT, int VW, bool kExact>
 void launch_vw(const ConvParams& p, bool bwd, hipStream_t stream) {
-    constexpr int V = VW ? VW : 4;
+    constexpr int V = VW;
     const dim3 grid(unsigned(p.batch * p.dim), unsigned((p.seqlen + kCT * V - 1) / (kCT * V)));
     if (bwd) {
-        hipLaunchKernelGGL((conv1d_bwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
+        hipLaunchKernelGGL((conv1d_bwd_kernel<IT, VW, kExact>), grid, dim3(kCT), 0, stream, p);
         if (p.part)
             hipLaunchKernelGGL(conv1d_bwd_reduce, dim3(unsigned((p.dim * 5 + 255) / 256)), dim3(256), 0, stream,
                                p.part, p.batch, p.dim, int64_t(grid.y), int(p.width), p.dw, p.dbias);
     } else {
-        hipLaunchKernelGGL((conv1d_fwd_kernel<IT, VW>), grid, dim3(kCT), 0, stream, p);
+        hipLaunchKernelGGL((conv1d_fwd_kernel<IT, VW, kExact>), grid, dim3(kCT), 0, stream, p);
     }
 }
 
 template <typename IT>
 hipError_t launch_t(const ConvParams& p, bool bwd, hipStream_t stream) {
-    if constexpr (sizeof(IT) == 4) {
-        if (p.vec) launch_vw<IT, 4>(p, bwd, stream);
-        else launch_vw<IT, 0>(p, bwd, stream);
-    } else {
-        if (p.vec == 8) launch_vw<IT, 8>(p, bwd, stream);
-        else if (p.vec == 4) launch_vw<IT, 4>(p, bwd, stream);
-        else launch_vw<IT, 0>(p, bwd, stream);
-    }
+    // 16-byte vectors; rows of whole vectors take the branch-free loads
+    if (p.exact) launch_vw<IT, 16 / sizeof(IT), true>(p, bwd, stream);
+    else launch_vw<IT, 16 / sizeof(IT), false>(p, bwd, stream);
     return hipGetLastError();
 }
 
@@ -343,30 +331,13 @@ hipError_t conv1d_launch(const ss_conv1d_args* a, const ss_conv1d_bwd_args* g, h
     p.o_bs = a->out_batch_stride; p.o_ds = a->out_dim_stride;
     p.w_ds = a->w_dim_stride; p.w_ks = a->w_width_stride;
     p.x = a->x; p.w = a->weight; p.bias = a->has_bias ? a->bias : nullptr; p.out = a->out;
-    const size_t es = a->itype == SS_F32 ? 4 : 2;
     if (g) {
         p.do_bs = g->dout_batch_stride; p.do_ds = g->dout_dim_stride;
         p.dx_bs = g->dx_batch_stride; p.dx_ds = g->dx_dim_stride;
         p.dout = g->dout; p.dx = g->dx; p.dw = g->dweight; p.dbias = a->has_bias ? g->dbias : nullptr;
         p.part = g->workspace;
     }
-    // every row of every tensor the launch touches starts on an n-element
-    // boundary and seqlen is a multiple of n (so each n-step vector is
-    // wholly inside or wholly outside a row)
-    auto rows_aligned = [&](int64_t n) {
-        auto al = [&](const void* q) { return (reinterpret_cast<uintptr_t>(q) % (n * es)) == 0; };
-        bool ok = p.seqlen % n == 0 && al(a->x) && p.x_bs % n == 0 && p.x_ds % n == 0;
-        if (g) {
-            ok = ok && al(g->dout) && al(g->dx) && p.do_bs % n == 0 && p.do_ds % n == 0 &&
-                 p.dx_bs % n == 0 && p.dx_ds % n == 0;
-        } else {
-            ok = ok && al(a->out) && p.o_bs % n == 0 && p.o_ds % n == 0;
-        }
-        return ok;
-    };
-    // 16-byte vectors: 8 steps of a 16-bit type, 4 of fp32; 8-byte vectors of
-    // a 16-bit type when rows are only 4-element aligned
-    p.vec = (es == 2 && rows_aligned(8)) ? 8 : (rows_aligned(4) ? 4 : 0);
+    p.exact = p.seqlen % int64_t(a->itype == SS_F32 ? 4 : 8) == 0;
     return launch_conv(p, a->itype, g != nullptr, stream);
 }
 
